@@ -1,0 +1,252 @@
+"""Benchmark: the ZeRO optimizer step over one GPU's flat partition.
+
+Workload (the headline): a Llama-3-8B ZeRO-2
+one-rank shard of 1,003,782,656 contiguous elements. bf16 grads
+N(0, 5e-4^2), fp32 master N(0, 0.02^2), fp32 exp_avg = exp_avg_sq = 0, bf16
+params; AdamW lr 3e-4, betas (0.9, 0.95), eps 1e-8, weight_decay 0.1, gradient
+clipping at 1.0 (active: the grad norm is about 15.8); bf16 => no loss scaling.
+Synthetic data, generated on the GPU with a seeded generator.
+
+One step = K1 (unscale + inf/NaN + norm partials) -> K0 (finalize) -> K2
+(AdamW + cast), three launches on torch's current stream, no host sync.
+Algorithmic bytes: K1 2 B/elt, K2 28 B/elt, step 30 B/elt.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--numel N]
+
+Prints one JSON line (rank 0). --gpus above 1 is refused: this build runs and
+measures one GPU; the multi-GPU layout is described in the design notes.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HEADLINE_NUMEL = 1_003_782_656
+HBM_PEAK_GBS = 8000.0
+K1_BYTES, K2_BYTES = 2, 28
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--numel", type=int, default=HEADLINE_NUMEL)
+    ap.add_argument("--cpu-sample", type=int, default=16 * 1024 * 1024,
+                    help="elements in the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                                      "k2_adamw_flat_llama8b_shard_traffic.json"))
+    ap.add_argument("--tuning", default="", help="k1_bpc,k2_bpc,k2_unroll,nt (library launch-shape override)")
+    return ap.parse_args()
+
+
+def _progress(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_inputs(n: int, seed: int, device):
+    import torch
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    master = torch.empty(n, dtype=torch.float32, device=device)
+    grad = torch.empty(n, dtype=torch.bfloat16, device=device)
+    chunk = 1 << 27
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        master[s:e].normal_(0.0, 0.02, generator=gen)
+        grad[s:e].copy_(torch.empty(e - s, dtype=torch.float32, device=device).normal_(0.0, 5e-4, generator=gen))
+    exp_avg = torch.zeros(n, dtype=torch.float32, device=device)
+    exp_avg_sq = torch.zeros(n, dtype=torch.float32, device=device)
+    p16 = master.to(torch.bfloat16)
+    return master, exp_avg, exp_avg_sq, p16, grad
+
+
+def cpu_baseline(n_sample: int, hyper) -> dict | None:
+    """The C oracle (a CPU port of the step) on a bounded sample, on this
+    host's cores; plus torch.optim.AdamW on CPU (the reference's cpu_offload
+    route) on the same sample, for context."""
+    if n_sample <= 0:
+        return None
+    import numpy as np
+    import torch
+    root = os.path.dirname(os.path.abspath(__file__))
+    sys.path.insert(0, root)
+    from oracle import oracle as O
+
+    rng = np.random.default_rng(7)
+    p = (rng.standard_normal(n_sample, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    g32 = (rng.standard_normal(n_sample, dtype=np.float32) * np.float32(5e-4)).astype(np.float32)
+    g16 = O.cast16(g32, O.BF16)
+    m = np.zeros(n_sample, np.float32)
+    v = np.zeros(n_sample, np.float32)
+    p16 = np.empty(n_sample, np.uint16)
+    h = O.Hyper(lr=hyper.lr, beta1=hyper.beta1, beta2=hyper.beta2, eps=hyper.eps,
+                weight_decay=hyper.weight_decay, max_grad_norm=hyper.max_grad_norm)
+    times = []
+    for t in range(1, 4):
+        t0 = time.perf_counter()
+        ss = O.sumsq(g16, O.BF16, 1.0)
+        coef = O.clip_coef(ss ** 0.5, h.max_grad_norm, h.clip_eps)
+        O.adamw(p, m, v, p16, O.BF16, g16, O.BF16, O.step_scalars(h, t, 1.0, coef))
+        times.append(time.perf_counter() - t0)
+    port_s = sorted(times[1:])[len(times[1:]) // 2]
+
+    # torch.optim.AdamW on CPU fp32, as the reference's CPU route runs it.
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(min(threads, 16))
+    param = torch.nn.Parameter(torch.from_numpy(p.copy()))
+    opt = torch.optim.AdamW([param], lr=hyper.lr, betas=(hyper.beta1, hyper.beta2), eps=hyper.eps,
+                            weight_decay=hyper.weight_decay, foreach=False)
+    g16t = torch.from_numpy(g16.view(np.int16)).view(torch.bfloat16)
+    ttimes = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        g = g16t.float()
+        norm = g.norm(dtype=torch.float32).item()
+        if norm > hyper.max_grad_norm:
+            g.mul_(hyper.max_grad_norm / (norm + 1e-6))
+        param.grad = g
+        opt.step()
+        param.detach().to(torch.bfloat16)
+        ttimes.append(time.perf_counter() - t0)
+    torch_s = sorted(ttimes[1:])[len(ttimes[1:]) // 2]
+    return {
+        "value": round(n_sample / port_s / 1e9, 4),
+        "unit": "Gparam/s",
+        "cores": int(O.lib().dsxo_num_threads()),
+        "kind": "port",
+        "sample": f"{n_sample} elements of the same workload (bf16 grads N(0,5e-4^2), fp32 state), "
+                  f"one full step (norm + clip + AdamW + cast), median of 2 after 1 warm-up",
+        "torch_adamw_cpu": {"value": round(n_sample / torch_s / 1e9, 4), "unit": "Gparam/s",
+                            "threads": torch.get_num_threads(),
+                            "what": "torch.optim.AdamW(foreach=False) on CPU fp32 + fp32 norm/clip + bf16 cast"},
+    }
+
+
+def main() -> int:
+    a = _args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1",
+                          "gpus_requested": a.gpus}))
+        return 2
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from distributedspeed_amd import _lib, ops
+    from distributedspeed_amd.flat_step import AdamWHyper, FlatStep, ScalerConfig
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 2
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    lib = _lib.load()
+    if a.tuning:
+        k1, k2, u, nt = (int(x) for x in a.tuning.split(","))
+        _lib.call("dsx_set_tuning", k1, k2, u, nt)
+    n = int(a.numel)
+    hyper = AdamWHyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    _progress(f"generating {n} elements")
+    master, exp_avg, exp_avg_sq, p16, grad = make_inputs(n, 2, dev)
+    fs = FlatStep(n, dev, hyper, ScalerConfig(mode="none"))
+    torch.cuda.synchronize()
+
+    _progress(f"warmup {a.warmup}")
+    for _ in range(a.warmup):
+        fs.step(master, exp_avg, exp_avg_sq, p16, grad)
+    torch.cuda.synchronize()
+
+    _progress(f"timing {a.steps} steps")
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(a.steps):
+        fs.step(master, exp_avg, exp_avg_sq, p16, grad)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(stop) / a.steps
+
+    # Per-kernel durations: the same three launches issued one by one, each
+    # bracketed by events on the stream they run on (torch's current stream).
+    _progress("per-kernel timing")
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
+    hc, sc = hyper.to_c(), fs.scaler.to_c()
+    for i in range(a.steps):
+        fs.steps_issued += 1
+        fs.bc.ensure(fs.steps_issued)
+        e = ev[i]
+        e[0].record()
+        ops.unscale_norm(grad, fs.state, fs.partials, fs.nparts)
+        e[1].record()
+        ops.finalize(fs.partials, fs.nparts, fs.state, sc, hc, fs.bc.table, fs.bc.length, fs.scalars)
+        e[2].record()
+        ops.adamw_flat(master, exp_avg, exp_avg_sq, p16, grad, fs.scalars)
+        e[3].record()
+    torch.cuda.synchronize()
+    k1_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / a.steps
+    k0_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / a.steps
+    k2_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / a.steps
+    st = fs.read_state()
+    scal = fs.read_scalars()
+    if st.error or scal.skip:
+        print(json.dumps({"error": f"step state error={st.error} skip={scal.skip}"}))
+        return 1
+
+    gparams = n / (ms_step * 1e-3) / 1e9
+    e2e_gbs = (K1_BYTES + K2_BYTES) * n / (ms_step * 1e-3) / 1e9
+    k2_gbs = K2_BYTES * n / (k2_ms * 1e-3) / 1e9
+    k1_gbs = K1_BYTES * n / (k1_ms * 1e-3) / 1e9
+
+    traffic = None
+    if os.path.exists(a.traffic):
+        try:
+            with open(a.traffic) as f:
+                tj = json.load(f)
+            if int(tj.get("numel", -1)) == n:
+                traffic = tj.get("k2_hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    _progress("cpu baseline")
+    cpu = cpu_baseline(min(a.cpu_sample, n), hyper)
+
+    out = {
+        "metric": "AdamW step Gparam/s + achieved HBM TB/s (% of 8 TB/s), 1.0B-elt bf16 shard",
+        "value": round(gparams, 3),
+        "unit": "Gparam/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 state / bf16 grads+params",
+        "data": "synthetic (seeded torch generator on the GPU)",
+        "config": {"workload": "llama3-8b zero2 one-rank shard (BASELINE configs[2])", "numel": n,
+                   "grad_dtype": "bf16", "param_dtype": "bf16", "lr": hyper.lr, "betas": [hyper.beta1, hyper.beta2],
+                   "eps": hyper.eps, "weight_decay": hyper.weight_decay, "max_grad_norm": hyper.max_grad_norm,
+                   "parallelism": "dp1 (one rank's ZeRO shard)"},
+        "achieved_tbps_end_to_end": round(e2e_gbs / 1000, 4),
+        "pct_of_8tbps_end_to_end": round(100 * e2e_gbs / HBM_PEAK_GBS, 2),
+        "kernels_ms": {"k1_unscale_norm": round(k1_ms, 4), "k0_finalize": round(k0_ms, 4),
+                       "k2_adamw_flat": round(k2_ms, 4)},
+        "k1_gbs": round(k1_gbs, 1),
+        "roofline": {"bound": "hbm", "achieved": round(k2_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(k2_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "k2_adamw_flat", "algorithmic_bytes_per_launch": K2_BYTES * n},
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 3),
+        "torch": torch.__version__, "hip": torch.version.hip,
+        "device": torch.cuda.get_device_name(dev),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

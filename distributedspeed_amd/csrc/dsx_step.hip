@@ -1,0 +1,747 @@
+// dsx_step.hip -- gfx950 kernels and C ABI of libdsx.so (see include/dsx.h).
+//
+// The ZeRO optimizer step over one flat partition, as the reference's
+// ZeROOptimizer.step (Src/zero/optimizer.py:212-274) orders it: overflow
+// check / skip -> unscale -> norm -> clip -> AdamW -> loss-scaler update,
+// with the AdamW arithmetic of torch.optim.AdamW (torch/optim/adam.py:347-552)
+// that the reference calls at Src/zero/stage1.py:522-525 and
+// Src/zero/stage2.py:609-612.
+//
+// Everything is HBM-bound streaming. K2 moves 28 B per element (grad 2 +
+// master/m/v 12 read, master/m/v 12 + param16 2 written) and K1 2 B per
+// element. The kernels are grid-stride loops over 4-element slots (fp32 in
+// 16-byte loads, 16-bit values in 8-byte loads) so that every load and store
+// instruction of a wave touches one contiguous span; several slots per thread
+// are loaded before any is used, to keep enough bytes in flight per CU.
+//
+// Compile with -ffp-contract=off: the element math must round exactly where
+// torch rounds, and the only fused multiply-adds are the explicit fmaf calls
+// that mirror torch's lerp and addcmul kernels.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+#include <string.h>
+#include <math.h>
+
+#include "dsx.h"
+
+static_assert(sizeof(DsxState) == 64, "DsxState layout");
+static_assert(sizeof(DsxScalerConfig) == 32, "DsxScalerConfig layout");
+static_assert(sizeof(DsxAdamwHyper) == 56, "DsxAdamwHyper layout");
+static_assert(sizeof(DsxStepScalars) == 64, "DsxStepScalars layout");
+static_assert(sizeof(DsxTensorRef) == 48, "DsxTensorRef layout");
+static_assert(sizeof(DsxChunk) == 24, "DsxChunk layout");
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / 64;
+
+typedef float    f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+thread_local char g_err[512];
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail((int)e, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return DSX_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool is16(int dt) { return dt == DSX_F16 || dt == DSX_BF16; }
+
+// ---- launch shape ----------------------------------------------------------
+
+struct Tuning {
+  int k1_blocks_per_cu = 8;
+  int k2_blocks_per_cu = 8;
+  int k2_unroll = 4;      // slots per thread per trip: 2, 4 or 8
+  int nontemporal = 1;    // nontemporal hint on the streaming loads/stores
+};
+Tuning g_tune;
+
+int cu_count() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cache[dev] > 0) return cache[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  if (dev < 64) cache[dev] = cus;
+  return cus;
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---- element helpers -------------------------------------------------------
+
+template <bool NT, typename T>
+__device__ __forceinline__ T ld(const T* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void st(T* p, T v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+// 16-bit storage value (low half of h) -> fp32; exact for both formats.
+template <int DT>
+__device__ __forceinline__ float h2f(uint32_t h) {
+  if constexpr (DT == DSX_BF16) {
+    return __uint_as_float(h << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
+  }
+}
+
+// fp32 -> 16-bit, round to nearest even. NaN becomes the quiet NaN
+// 0x7FC0 (bf16, as c10::BFloat16 does) or sign|0x7E00 (fp16).
+template <int DT>
+__device__ __forceinline__ uint32_t f2h(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if constexpr (DT == DSX_BF16) {
+    if (x != x) return 0x7FC0u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  } else {
+    if (x != x) return ((u >> 16) & 0x8000u) | 0x7E00u;
+    return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)x);
+  }
+}
+
+// Step scalars held in registers.
+struct Sc {
+  float inv, coef, decay, w1, w1m1, b2, val2, eps, bc2s, nss;
+  bool small;
+};
+
+__device__ __forceinline__ Sc load_sc(const DsxStepScalars& s) {
+  Sc r;
+  r.inv = s.inv_scale; r.coef = s.clip_coef; r.decay = s.decay;
+  r.w1 = s.w1; r.w1m1 = s.w1m1; r.b2 = s.b2; r.val2 = s.val2;
+  r.eps = s.eps; r.bc2s = s.bc2s; r.nss = s.nss;
+  r.small = fabsf(s.w1) < 0.5f;
+  return r;
+}
+
+// One element of the step. Order and rounding follow torch's CPU kernels:
+// unscale and clip are fp32 multiplies; param.mul_(1 - lr*wd); lerp_ with a
+// scalar weight is fma(w, end - self, self) (or fma(w - 1, end - self, end)
+// for |w| >= 0.5); exp_avg_sq.mul_(b2).addcmul_(g, g, 1 - b2) is
+// fma((1 - b2) * g, g, v * b2); denom = sqrt(v) / bc2s + eps with IEEE sqrt
+// and division; addcdiv_ is p + (value * m) / denom.
+__device__ __forceinline__ void adamw_elt(float graw, float& p, float& m, float& v, const Sc& s) {
+  float g = graw * s.inv;
+  g = g * s.coef;
+  p = p * s.decay;
+  const float d = g - m;
+  m = s.small ? __builtin_fmaf(s.w1, d, m) : __builtin_fmaf(s.w1m1, d, g);
+  v = v * s.b2;
+  v = __builtin_fmaf(s.val2 * g, g, v);
+  const float den = __builtin_sqrtf(v) / s.bc2s + s.eps;
+  p = p + (s.nss * m) / den;
+}
+
+// Four elements held in vector registers.
+__device__ __forceinline__ void adamw4(const float (&g)[4], f4& p, f4& m, f4& v, const Sc& s) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float pk = p[k], mk = m[k], vk = v[k];
+    adamw_elt(g[k], pk, mk, vk, s);
+    p[k] = pk; m[k] = mk; v[k] = vk;
+  }
+}
+
+// ---- block reduction of a double -------------------------------------------
+
+__device__ __forceinline__ double wave_sum(double x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// Sum over the block; the result is valid in thread 0.
+__device__ __forceinline__ double block_sum(double x) {
+  __shared__ double lds[kWaves];
+  x = wave_sum(x);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = x;
+  __syncthreads();
+  double s = 0.0;
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += lds[w];
+  }
+  return s;
+}
+
+__device__ __forceinline__ float inv_of(float scale) {
+  // torch: GradScaler's inv_scale = scale.double().reciprocal().float();
+  // the reference's static path multiplies by the Python double 1/loss_scale.
+  return (float)(1.0 / (double)scale);
+}
+
+// ---- K1: unscale + inf/NaN + squared norm ----------------------------------
+// Each element contributes (double)(f32(g) * inv)^2. The square of a finite
+// fp32 value is exact in fp64 and the sum of 2^31 of them cannot overflow,
+// so the sum is non-finite exactly when some unscaled grad is inf or NaN.
+
+template <int GD, int U, bool NT>
+__global__ __launch_bounds__(kBlock) void k1_unscale_norm(const uint16_t* __restrict__ g, int64_t n,
+                                                          const DsxState* __restrict__ state,
+                                                          double* __restrict__ partials) {
+  const float inv = inv_of(state->scale);
+  const u4* g8 = reinterpret_cast<const u4*>(g);
+  const int64_t nvec = n >> 3;  // 8 elements per 16-byte slot
+  const int64_t stride = (int64_t)gridDim.x * kBlock * U;
+  double acc = 0.0;
+  for (int64_t i0 = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; i0 < nvec; i0 += stride) {
+    u4 G[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * kBlock;
+      G[u] = (i < nvec) ? ld<NT>(g8 + i) : u4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float a = h2f<GD>(G[u][k]) * inv;
+        const float b = h2f<GD>(G[u][k] >> 16) * inv;
+        acc = __builtin_fma((double)a, (double)a, acc);
+        acc = __builtin_fma((double)b, (double)b, acc);
+      }
+    }
+  }
+  const int64_t tail0 = nvec << 3;
+  const int64_t gt = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (gt < n - tail0) {
+    const float a = h2f<GD>(g[tail0 + gt]) * inv;
+    acc = __builtin_fma((double)a, (double)a, acc);
+  }
+  const double s = block_sum(acc);
+  if (threadIdx.x == 0) partials[blockIdx.x] = s;
+}
+
+// ---- K0: finalize ------------------------------------------------------------
+
+__global__ __launch_bounds__(kBlock) void k0_finalize(const double* __restrict__ partials, int32_t nparts,
+                                                      DsxState* __restrict__ state, DsxScalerConfig scfg,
+                                                      DsxAdamwHyper hp, const double* __restrict__ bc,
+                                                      int32_t bc_len, DsxStepScalars* __restrict__ out) {
+  double x = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += kBlock) x += partials[i];
+  const double sumsq = block_sum(x);
+  if (threadIdx.x != 0) return;
+
+  DsxState s = *state;
+  DsxStepScalars o = {};
+  o.sumsq = sumsq;
+  o.norm = sqrt(sumsq);
+  o.inv_scale = inv_of(s.scale);
+  o.clip_coef = 1.0f;
+  o.decay = 1.0f;
+  o.t = s.t;
+  const bool found_inf = !__builtin_isfinite(sumsq);
+  const bool dynamic = scfg.mode == DSX_SCALE_DYNAMIC;
+
+  if (found_inf) {
+    o.skip = 1;
+    s.overflow_count += 1;
+    if (dynamic) {
+      if (scfg.hysteresis <= 1 || s.hyst_left <= 1) {
+        const float next = s.scale * scfg.backoff_factor;
+        s.scale = next > scfg.min_scale ? next : scfg.min_scale;
+      } else {
+        s.hyst_left -= 1;
+      }
+      s.good_steps = 0;
+    }
+  } else {
+    const int32_t t = s.t + 1;
+    if (t > bc_len) {
+      o.skip = 1;
+      s.error |= DSX_STATE_ERR_BC_TABLE;
+    } else {
+      const double bc1 = bc[2 * (int64_t)(t - 1)];
+      const double bc2s = bc[2 * (int64_t)(t - 1) + 1];
+      if (hp.max_grad_norm > 0.0 && o.norm > hp.max_grad_norm)
+        o.clip_coef = (float)(hp.max_grad_norm / (o.norm + hp.clip_eps));
+      if (hp.weight_decay != 0.0) o.decay = (float)(1.0 - hp.lr * hp.weight_decay);
+      o.w1 = (float)(1.0 - hp.beta1);
+      o.w1m1 = o.w1 - 1.0f;
+      o.b2 = (float)hp.beta2;
+      o.val2 = (float)(1.0 - hp.beta2);
+      o.eps = (float)hp.eps;
+      o.bc2s = (float)bc2s;
+      o.nss = (float)(-(hp.lr / bc1));
+      o.t = t;
+      s.t = t;
+      if (dynamic) {
+        s.good_steps += 1;
+        if (s.good_steps >= scfg.window) {
+          const float next = s.scale * scfg.growth_factor;
+          if (__builtin_isfinite(next)) s.scale = next;
+          s.good_steps = 0;
+          s.hyst_left = scfg.hysteresis;
+        }
+      }
+    }
+  }
+  s.iter += 1;
+  s.last_skip = o.skip;
+  s.last_norm = o.norm;
+  *state = s;
+  *out = o;
+}
+
+__global__ void k_state_init(DsxState* state, float scale, int32_t hysteresis) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    DsxState s = {};
+    s.scale = scale;
+    s.hyst_left = hysteresis;
+    *state = s;
+  }
+}
+
+// ---- K2: AdamW + cast over a flat partition ----------------------------------
+
+template <int GD, int PD, int U, bool NT>
+__global__ __launch_bounds__(kBlock) void k2_adamw_flat(float* __restrict__ p, float* __restrict__ m,
+                                                        float* __restrict__ v, uint16_t* __restrict__ p16,
+                                                        const uint16_t* __restrict__ g, int64_t n,
+                                                        const DsxStepScalars* __restrict__ scp) {
+  if (scp->skip) return;
+  const Sc s = load_sc(*scp);
+  f4* p4 = reinterpret_cast<f4*>(p);
+  f4* m4 = reinterpret_cast<f4*>(m);
+  f4* v4 = reinterpret_cast<f4*>(v);
+  u2* o2 = reinterpret_cast<u2*>(p16);
+  const u2* g2 = reinterpret_cast<const u2*>(g);
+  const bool cast = p16 != nullptr;
+  const int64_t nvec = n >> 2;  // 4 elements per slot
+  const int64_t stride = (int64_t)gridDim.x * kBlock * U;
+  for (int64_t i0 = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; i0 < nvec; i0 += stride) {
+    u2 G[U];
+    f4 P[U], M[U], V[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * kBlock;
+      if (i < nvec) {
+        G[u] = ld<NT>(g2 + i);
+        P[u] = ld<NT>(p4 + i);
+        M[u] = ld<NT>(m4 + i);
+        V[u] = ld<NT>(v4 + i);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * kBlock;
+      if (i < nvec) {
+        float gf[4] = {h2f<GD>(G[u].x), h2f<GD>(G[u].x >> 16), h2f<GD>(G[u].y), h2f<GD>(G[u].y >> 16)};
+        f4 pp = P[u], mm = M[u], vv = V[u];
+        adamw4(gf, pp, mm, vv, s);
+        st<NT>(p4 + i, pp);
+        st<NT>(m4 + i, mm);
+        st<NT>(v4 + i, vv);
+        if (cast) {
+          u2 o;
+          o.x = f2h<PD>(pp[0]) | (f2h<PD>(pp[1]) << 16);
+          o.y = f2h<PD>(pp[2]) | (f2h<PD>(pp[3]) << 16);
+          st<NT>(o2 + i, o);
+        }
+      }
+    }
+  }
+  const int64_t tail0 = nvec << 2;
+  const int64_t gt = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (gt < n - tail0) {
+    const int64_t e = tail0 + gt;
+    float pe = p[e], me = m[e], ve = v[e];
+    adamw_elt(h2f<GD>(g[e]), pe, me, ve, s);
+    p[e] = pe; m[e] = me; v[e] = ve;
+    if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
+  }
+}
+
+// ---- K3: ragged lists ----------------------------------------------------------
+
+__device__ __forceinline__ bool chunk_aligned(const void* a, const void* b, const void* c,
+                                              const void* d, const void* e) {
+  const uintptr_t o = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                      reinterpret_cast<uintptr_t>(c) | (reinterpret_cast<uintptr_t>(d) << 1) |
+                      (reinterpret_cast<uintptr_t>(e) << 1);  // 16-bit arrays need 8-byte alignment
+  return (o & 15u) == 0;
+}
+
+template <int GD>
+__global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorRef* __restrict__ tensors,
+                                                                const DsxChunk* __restrict__ chunks,
+                                                                int64_t nchunks,
+                                                                const DsxState* __restrict__ state,
+                                                                double* __restrict__ partials) {
+  const float inv = inv_of(state->scale);
+  double acc = 0.0;
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const DsxChunk ch = chunks[c];
+    const uint16_t* g = static_cast<const uint16_t*>(tensors[ch.tensor].grad) + ch.start;
+    const int64_t len = ch.len;
+    int64_t done = 0;
+    if ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) {
+      const u4* g8 = reinterpret_cast<const u4*>(g);
+      const int64_t nvec = len >> 3;
+      for (int64_t i = threadIdx.x; i < nvec; i += kBlock) {
+        const u4 G = g8[i];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float a = h2f<GD>(G[k]) * inv;
+          const float b = h2f<GD>(G[k] >> 16) * inv;
+          acc = __builtin_fma((double)a, (double)a, acc);
+          acc = __builtin_fma((double)b, (double)b, acc);
+        }
+      }
+      done = nvec << 3;
+    }
+    for (int64_t e = done + threadIdx.x; e < len; e += kBlock) {
+      const float a = h2f<GD>(g[e]) * inv;
+      acc = __builtin_fma((double)a, (double)a, acc);
+    }
+  }
+  const double s = block_sum(acc);
+  if (threadIdx.x == 0) partials[blockIdx.x] = s;
+}
+
+template <int GD, int PD>
+__global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __restrict__ tensors,
+                                                         const DsxChunk* __restrict__ chunks, int64_t nchunks,
+                                                         const DsxStepScalars* __restrict__ scp) {
+  if (scp->skip) return;
+  const Sc s = load_sc(*scp);
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const DsxChunk ch = chunks[c];
+    const DsxTensorRef tr = tensors[ch.tensor];
+    float* p = tr.master + ch.start;
+    float* m = tr.exp_avg + ch.start;
+    float* v = tr.exp_avg_sq + ch.start;
+    uint16_t* p16 = tr.param16 ? static_cast<uint16_t*>(tr.param16) + ch.start : nullptr;
+    const uint16_t* g = static_cast<const uint16_t*>(tr.grad) + ch.start;
+    const bool cast = p16 != nullptr;
+    const int64_t len = ch.len;
+    int64_t done = 0;
+    if (chunk_aligned(p, m, v, cast ? (const void*)p16 : (const void*)g, g)) {
+      f4* p4 = reinterpret_cast<f4*>(p);
+      f4* m4 = reinterpret_cast<f4*>(m);
+      f4* v4 = reinterpret_cast<f4*>(v);
+      u2* o2 = reinterpret_cast<u2*>(p16);
+      const u2* g2 = reinterpret_cast<const u2*>(g);
+      const int64_t nvec = len >> 2;
+      for (int64_t i = threadIdx.x; i < nvec; i += kBlock) {
+        const u2 G = g2[i];
+        f4 pp = p4[i], mm = m4[i], vv = v4[i];
+        float gf[4] = {h2f<GD>(G.x), h2f<GD>(G.x >> 16), h2f<GD>(G.y), h2f<GD>(G.y >> 16)};
+        adamw4(gf, pp, mm, vv, s);
+        p4[i] = pp; m4[i] = mm; v4[i] = vv;
+        if (cast) {
+          u2 o;
+          o.x = f2h<PD>(pp[0]) | (f2h<PD>(pp[1]) << 16);
+          o.y = f2h<PD>(pp[2]) | (f2h<PD>(pp[3]) << 16);
+          o2[i] = o;
+        }
+      }
+      done = nvec << 2;
+    }
+    for (int64_t e = done + threadIdx.x; e < len; e += kBlock) {
+      float pe = p[e], me = m[e], ve = v[e];
+      adamw_elt(h2f<GD>(g[e]), pe, me, ve, s);
+      p[e] = pe; m[e] = me; v[e] = ve;
+      if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
+    }
+  }
+}
+
+// ---- host-side dispatch ----------------------------------------------------------
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+template <int GD, int U, bool NT>
+void launch_k1_u(const void* g, int64_t n, const DsxState* st, double* partials, int nparts, hipStream_t s) {
+  hipLaunchKernelGGL((k1_unscale_norm<GD, U, NT>), dim3(nparts), dim3(kBlock), 0, s,
+                     static_cast<const uint16_t*>(g), n, st, partials);
+}
+
+template <int GD>
+void launch_k1(const void* g, int64_t n, const DsxState* st, double* partials, int nparts, hipStream_t s) {
+  if (g_tune.nontemporal) launch_k1_u<GD, 4, true>(g, n, st, partials, nparts, s);
+  else launch_k1_u<GD, 4, false>(g, n, st, partials, nparts, s);
+}
+
+template <int GD, int PD, int U>
+void launch_k2_u(float* p, float* m, float* v, void* p16, const void* g, int64_t n, const DsxStepScalars* sc,
+                 hipStream_t s) {
+  const int64_t slots = n >> 2;
+  int64_t blocks = ceil_div(slots > 0 ? slots : 1, (int64_t)kBlock * U);
+  const int64_t cap = (int64_t)cu_count() * g_tune.k2_blocks_per_cu;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  if (g_tune.nontemporal)
+    hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, true>), dim3((unsigned)blocks), dim3(kBlock), 0, s, p, m, v,
+                       static_cast<uint16_t*>(p16), static_cast<const uint16_t*>(g), n, sc);
+  else
+    hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, false>), dim3((unsigned)blocks), dim3(kBlock), 0, s, p, m, v,
+                       static_cast<uint16_t*>(p16), static_cast<const uint16_t*>(g), n, sc);
+}
+
+template <int GD, int PD>
+void launch_k2(float* p, float* m, float* v, void* p16, const void* g, int64_t n, const DsxStepScalars* sc,
+               hipStream_t s) {
+  switch (g_tune.k2_unroll) {
+    case 2: launch_k2_u<GD, PD, 2>(p, m, v, p16, g, n, sc, s); break;
+    case 8: launch_k2_u<GD, PD, 8>(p, m, v, p16, g, n, sc, s); break;
+    default: launch_k2_u<GD, PD, 4>(p, m, v, p16, g, n, sc, s); break;
+  }
+}
+
+int check_flat(const float* master, const float* m, const float* v, const void* p16, int pdt, const void* g,
+               int gdt, int64_t n) {
+  if (n < 0) return fail(DSX_EINVAL, "n must be >= 0 (got %lld)", (long long)n);
+  if (!is16(gdt)) return fail(DSX_EINVAL, "grad dtype must be DSX_F16 or DSX_BF16 (got %d)", gdt);
+  if (p16 && !is16(pdt)) return fail(DSX_EINVAL, "param16 dtype must be DSX_F16 or DSX_BF16 (got %d)", pdt);
+  if (n == 0) return DSX_OK;
+  if (!master || !m || !v || !g) return fail(DSX_EINVAL, "null master/exp_avg/exp_avg_sq/grad pointer");
+  if (!aligned16(master) || !aligned16(m) || !aligned16(v) || !aligned16(g) || (p16 && !aligned16(p16)))
+    return fail(DSX_EINVAL, "flat buffers must be 16-byte aligned");
+  return DSX_OK;
+}
+
+int check_hyper(const DsxAdamwHyper& h) {
+  // Same admissible ranges as torch.optim.Adam's constructor (torch/optim/adam.py).
+  if (!(h.lr >= 0.0)) return fail(DSX_EINVAL, "Invalid learning rate: %g", h.lr);
+  if (!(h.eps >= 0.0)) return fail(DSX_EINVAL, "Invalid epsilon value: %g", h.eps);
+  if (!(h.beta1 >= 0.0 && h.beta1 < 1.0)) return fail(DSX_EINVAL, "Invalid beta parameter at index 0: %g", h.beta1);
+  if (!(h.beta2 >= 0.0 && h.beta2 < 1.0)) return fail(DSX_EINVAL, "Invalid beta parameter at index 1: %g", h.beta2);
+  if (!(h.weight_decay >= 0.0)) return fail(DSX_EINVAL, "Invalid weight_decay value: %g", h.weight_decay);
+  if (!(h.clip_eps >= 0.0)) return fail(DSX_EINVAL, "Invalid clip_eps: %g", h.clip_eps);
+  if (h.max_grad_norm != h.max_grad_norm) return fail(DSX_EINVAL, "max_grad_norm is NaN");
+  return DSX_OK;
+}
+
+int check_scaler(const DsxScalerConfig& c) {
+  if (c.mode < DSX_SCALE_NONE || c.mode > DSX_SCALE_DYNAMIC) return fail(DSX_EINVAL, "bad scaler mode %d", c.mode);
+  if (c.mode == DSX_SCALE_DYNAMIC) {
+    if (c.window < 1) return fail(DSX_EINVAL, "loss_scale_window must be >= 1 (got %d)", c.window);
+    if (c.hysteresis < 1) return fail(DSX_EINVAL, "hysteresis must be >= 1 (got %d)", c.hysteresis);
+    if (!(c.min_scale > 0.0f)) return fail(DSX_EINVAL, "min_loss_scale must be > 0 (got %g)", c.min_scale);
+    if (!(c.growth_factor > 1.0f)) return fail(DSX_EINVAL, "growth_factor must be > 1 (got %g)", c.growth_factor);
+    if (!(c.backoff_factor > 0.0f && c.backoff_factor < 1.0f))
+      return fail(DSX_EINVAL, "backoff_factor must be in (0, 1) (got %g)", c.backoff_factor);
+  }
+  return DSX_OK;
+}
+
+int check_parts(const double* partials, int32_t nparts) {
+  if (nparts < 1 || nparts > DSX_MAX_PARTIALS)
+    return fail(DSX_EINVAL, "nparts must be in [1, %d] (got %d)", DSX_MAX_PARTIALS, nparts);
+  if (!partials) return fail(DSX_EINVAL, "null partials");
+  return DSX_OK;
+}
+
+int do_unscale_norm(const void* g, int gdt, int64_t n, const DsxState* st, double* partials, int32_t nparts,
+                    hipStream_t s) {
+  if (gdt == DSX_BF16) launch_k1<DSX_BF16>(g, n, st, partials, nparts, s);
+  else launch_k1<DSX_F16>(g, n, st, partials, nparts, s);
+  return launch_status("dsx_unscale_norm");
+}
+
+int do_finalize(const double* partials, int32_t nparts, DsxState* st, const DsxScalerConfig& sc,
+                const DsxAdamwHyper& hp, const double* bc, int32_t bc_len, DsxStepScalars* out, hipStream_t s) {
+  hipLaunchKernelGGL(k0_finalize, dim3(1), dim3(kBlock), 0, s, partials, nparts, st, sc, hp, bc, bc_len, out);
+  return launch_status("dsx_finalize");
+}
+
+int do_adamw_flat(float* p, float* m, float* v, void* p16, int pdt, const void* g, int gdt, int64_t n,
+                  const DsxStepScalars* sc, hipStream_t s) {
+  if (n == 0) return DSX_OK;
+  const int pd = p16 ? pdt : gdt;  // pd only selects the cast when p16 != NULL
+  if (gdt == DSX_BF16) {
+    if (pd == DSX_BF16) launch_k2<DSX_BF16, DSX_BF16>(p, m, v, p16, g, n, sc, s);
+    else launch_k2<DSX_BF16, DSX_F16>(p, m, v, p16, g, n, sc, s);
+  } else {
+    if (pd == DSX_BF16) launch_k2<DSX_F16, DSX_BF16>(p, m, v, p16, g, n, sc, s);
+    else launch_k2<DSX_F16, DSX_F16>(p, m, v, p16, g, n, sc, s);
+  }
+  return launch_status("dsx_adamw_flat");
+}
+
+}  // namespace
+
+// ---- C ABI ---------------------------------------------------------------------
+
+extern "C" {
+
+int dsx_abi_version(void) { return DSX_ABI_VERSION; }
+
+const char* dsx_last_error(void) { return g_err; }
+
+int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll, int nontemporal) {
+  if (k1_blocks_per_cu < 1 || k1_blocks_per_cu > 32 || k2_blocks_per_cu < 1 || k2_blocks_per_cu > 64)
+    return fail(DSX_EINVAL, "blocks per CU out of range");
+  if (k2_unroll != 2 && k2_unroll != 4 && k2_unroll != 8) return fail(DSX_EINVAL, "k2_unroll must be 2, 4 or 8");
+  g_tune.k1_blocks_per_cu = k1_blocks_per_cu;
+  g_tune.k2_blocks_per_cu = k2_blocks_per_cu;
+  g_tune.k2_unroll = k2_unroll;
+  g_tune.nontemporal = nontemporal ? 1 : 0;
+  return DSX_OK;
+}
+
+int32_t dsx_suggest_partials(int64_t n) {
+  const int64_t slots = n > 0 ? (n >> 3) : 0;
+  const int64_t need = ceil_div(slots > 0 ? slots : 1, (int64_t)kBlock * 4);
+  int64_t cap = (int64_t)cu_count() * g_tune.k1_blocks_per_cu;
+  if (cap > DSX_MAX_PARTIALS) cap = DSX_MAX_PARTIALS;
+  return (int32_t)(need < cap ? need : cap);
+}
+
+int64_t dsx_count_chunks(const int64_t* numels, int32_t ntensors, int64_t chunk_elems) {
+  if (!numels || ntensors < 0 || chunk_elems < 8 || (chunk_elems & 7))
+    return fail(-1, "dsx_count_chunks: bad arguments"), -1;
+  int64_t c = 0;
+  for (int32_t i = 0; i < ntensors; ++i) {
+    if (numels[i] < 0) return fail(-1, "dsx_count_chunks: negative numel"), -1;
+    c += ceil_div(numels[i], chunk_elems);
+  }
+  return c;
+}
+
+int64_t dsx_build_chunks(const int64_t* numels, int32_t ntensors, int64_t chunk_elems, DsxChunk* out, int64_t cap) {
+  const int64_t need = dsx_count_chunks(numels, ntensors, chunk_elems);
+  if (need < 0) return -1;
+  if (!out || cap < need) return fail(-1, "dsx_build_chunks: capacity %lld < %lld", (long long)cap, (long long)need), -1;
+  int64_t c = 0;
+  for (int32_t i = 0; i < ntensors; ++i) {
+    for (int64_t s = 0; s < numels[i]; s += chunk_elems) {
+      out[c].tensor = i;
+      out[c].reserved = 0;
+      out[c].start = s;
+      out[c].len = numels[i] - s < chunk_elems ? numels[i] - s : chunk_elems;
+      ++c;
+    }
+  }
+  return c;
+}
+
+int dsx_state_init(DsxState* state, float init_scale, int32_t hysteresis, void* stream) {
+  if (!state) return fail(DSX_EINVAL, "null state");
+  if (!(init_scale > 0.0f) || !__builtin_isfinite(init_scale))
+    return fail(DSX_EINVAL, "initial loss scale must be finite and > 0 (got %g)", init_scale);
+  if (hysteresis < 1) return fail(DSX_EINVAL, "hysteresis must be >= 1 (got %d)", hysteresis);
+  hipLaunchKernelGGL(k_state_init, dim3(1), dim3(64), 0, as_stream(stream), state, init_scale, hysteresis);
+  return launch_status("dsx_state_init");
+}
+
+int dsx_unscale_norm(const void* grad, int grad_dtype, int64_t n, const DsxState* state, double* partials,
+                     int32_t nparts, void* stream) {
+  if (!is16(grad_dtype)) return fail(DSX_EINVAL, "grad dtype must be DSX_F16 or DSX_BF16 (got %d)", grad_dtype);
+  if (n < 0) return fail(DSX_EINVAL, "n must be >= 0");
+  if (n > 0 && (!grad || !aligned16(grad))) return fail(DSX_EINVAL, "grad must be non-null and 16-byte aligned");
+  if (!state) return fail(DSX_EINVAL, "null state");
+  int rc = check_parts(partials, nparts);
+  if (rc) return rc;
+  return do_unscale_norm(grad, grad_dtype, n, state, partials, nparts, as_stream(stream));
+}
+
+int dsx_finalize(const double* partials, int32_t nparts, DsxState* state, DsxScalerConfig scaler,
+                 DsxAdamwHyper hyper, const double* bc_table, int32_t bc_len, DsxStepScalars* out, void* stream) {
+  int rc = check_parts(partials, nparts);
+  if (!rc) rc = check_scaler(scaler);
+  if (!rc) rc = check_hyper(hyper);
+  if (rc) return rc;
+  if (!state || !out) return fail(DSX_EINVAL, "null state or scalars");
+  if (bc_len < 0 || (bc_len > 0 && !bc_table)) return fail(DSX_EINVAL, "bad bias-correction table");
+  return do_finalize(partials, nparts, state, scaler, hyper, bc_table, bc_len, out, as_stream(stream));
+}
+
+int dsx_adamw_flat(float* master, float* exp_avg, float* exp_avg_sq, void* param16, int param_dtype,
+                   const void* grad, int grad_dtype, int64_t n, const DsxStepScalars* scalars, void* stream) {
+  int rc = check_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n);
+  if (rc) return rc;
+  if (!scalars) return fail(DSX_EINVAL, "null scalars");
+  return do_adamw_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, scalars,
+                       as_stream(stream));
+}
+
+int dsx_zero_step_flat(float* master, float* exp_avg, float* exp_avg_sq, void* param16, int param_dtype,
+                       const void* grad, int grad_dtype, int64_t n, DsxState* state, DsxScalerConfig scaler,
+                       DsxAdamwHyper hyper, const double* bc_table, int32_t bc_len, double* partials,
+                       int32_t nparts, DsxStepScalars* out, void* stream) {
+  int rc = check_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n);
+  if (!rc) rc = check_parts(partials, nparts);
+  if (!rc) rc = check_scaler(scaler);
+  if (!rc) rc = check_hyper(hyper);
+  if (rc) return rc;
+  if (!state || !out) return fail(DSX_EINVAL, "null state or scalars");
+  if (bc_len < 0 || (bc_len > 0 && !bc_table)) return fail(DSX_EINVAL, "bad bias-correction table");
+  hipStream_t s = as_stream(stream);
+  rc = do_unscale_norm(grad, grad_dtype, n, state, partials, nparts, s);
+  if (!rc) rc = do_finalize(partials, nparts, state, scaler, hyper, bc_table, bc_len, out, s);
+  if (!rc) rc = do_adamw_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, out, s);
+  return rc;
+}
+
+int dsx_unscale_norm_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int grad_dtype,
+                           const DsxState* state, double* partials, int32_t nparts, void* stream) {
+  if (!is16(grad_dtype)) return fail(DSX_EINVAL, "grad dtype must be DSX_F16 or DSX_BF16 (got %d)", grad_dtype);
+  if (nchunks < 0 || (nchunks > 0 && (!tensors || !chunks))) return fail(DSX_EINVAL, "bad chunk table");
+  if (!state) return fail(DSX_EINVAL, "null state");
+  int rc = check_parts(partials, nparts);
+  if (rc) return rc;
+  hipStream_t s = as_stream(stream);
+  if (grad_dtype == DSX_BF16)
+    hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_BF16>), dim3(nparts), dim3(kBlock), 0, s, tensors, chunks, nchunks,
+                       state, partials);
+  else
+    hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_F16>), dim3(nparts), dim3(kBlock), 0, s, tensors, chunks, nchunks,
+                       state, partials);
+  return launch_status("dsx_unscale_norm_multi");
+}
+
+int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int param_dtype,
+                    int grad_dtype, const DsxStepScalars* scalars, void* stream) {
+  if (!is16(grad_dtype)) return fail(DSX_EINVAL, "grad dtype must be DSX_F16 or DSX_BF16 (got %d)", grad_dtype);
+  if (!is16(param_dtype)) return fail(DSX_EINVAL, "param16 dtype must be DSX_F16 or DSX_BF16 (got %d)", param_dtype);
+  if (nchunks < 0 || (nchunks > 0 && (!tensors || !chunks))) return fail(DSX_EINVAL, "bad chunk table");
+  if (!scalars) return fail(DSX_EINVAL, "null scalars");
+  if (nchunks == 0) return DSX_OK;
+  int64_t blocks = (int64_t)cu_count() * g_tune.k2_blocks_per_cu;
+  if (blocks > nchunks) blocks = nchunks;
+  hipStream_t s = as_stream(stream);
+  const dim3 grid((unsigned)blocks), blk(kBlock);
+  if (grad_dtype == DSX_BF16) {
+    if (param_dtype == DSX_BF16)
+      hipLaunchKernelGGL((k2_adamw_multi<DSX_BF16, DSX_BF16>), grid, blk, 0, s, tensors, chunks, nchunks, scalars);
+    else
+      hipLaunchKernelGGL((k2_adamw_multi<DSX_BF16, DSX_F16>), grid, blk, 0, s, tensors, chunks, nchunks, scalars);
+  } else {
+    if (param_dtype == DSX_BF16)
+      hipLaunchKernelGGL((k2_adamw_multi<DSX_F16, DSX_BF16>), grid, blk, 0, s, tensors, chunks, nchunks, scalars);
+    else
+      hipLaunchKernelGGL((k2_adamw_multi<DSX_F16, DSX_F16>), grid, blk, 0, s, tensors, chunks, nchunks, scalars);
+  }
+  return launch_status("dsx_adamw_multi");
+}
+
+}  // extern "C"

@@ -1,0 +1,226 @@
+"""torch-tensor wrappers over the libdsx C ABI (include/dsx.h).
+
+Every function checks shapes, dtypes, devices and alignment on the host
+before anything is launched, then enqueues on torch's current HIP stream.
+Nothing here synchronises the host with the device.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import (DSX_BF16, DSX_F16, DsxAdamwHyper, DsxScalerConfig, DsxStepScalars, DsxState)
+
+_DT = {torch.float16: DSX_F16, torch.bfloat16: DSX_BF16}
+
+STATE_BYTES = ctypes.sizeof(DsxState)
+SCALARS_BYTES = ctypes.sizeof(DsxStepScalars)
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DT[dt]
+    except KeyError:
+        raise TypeError(f"expected a float16 or bfloat16 tensor, got {dt}") from None
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype | None, numel: int | None, device: torch.device,
+          align: int = 16) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if numel is not None and t.numel() != numel:
+        raise ValueError(f"{name} has {t.numel()} elements, expected {numel}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.numel() and t.data_ptr() % align:
+        raise ValueError(f"{name} must be {align}-byte aligned")
+
+
+def _device(t: torch.Tensor) -> torch.device:
+    if t.device.type != "cuda":
+        raise ValueError(f"libdsx runs on the GPU; got a tensor on {t.device}")
+    return t.device
+
+
+def new_state(device: torch.device, init_scale: float = 1.0, hysteresis: int = 1) -> torch.Tensor:
+    """A DsxState on `device` (uint8[64]), initialised on the current stream."""
+    st = torch.empty(STATE_BYTES, dtype=torch.uint8, device=device)
+    _lib.call("dsx_state_init", _ptr(st), ctypes.c_float(init_scale), int(hysteresis), _stream(st.device))
+    return st
+
+
+def new_scalars(device: torch.device) -> torch.Tensor:
+    return torch.zeros(SCALARS_BYTES, dtype=torch.uint8, device=device)
+
+
+def scalars_from_host(sc: DsxStepScalars, device: torch.device) -> torch.Tensor:
+    """Upload a host-built DsxStepScalars (for driving K2 directly)."""
+    raw = torch.frombuffer(bytearray(bytes(sc)), dtype=torch.uint8)
+    return raw.to(device)
+
+
+def read_state(st: torch.Tensor) -> DsxState:
+    """Copy a DsxState to the host (synchronises with the stream)."""
+    return DsxState.from_buffer_copy(bytes(st.cpu().numpy().tobytes()))
+
+
+def read_scalars(sc: torch.Tensor) -> DsxStepScalars:
+    return DsxStepScalars.from_buffer_copy(bytes(sc.cpu().numpy().tobytes()))
+
+
+def scale_view(st: torch.Tensor) -> torch.Tensor:
+    """fp32 one-element device view of DsxState.scale (no host sync)."""
+    return st[0:4].view(torch.float32)
+
+
+def suggest_partials(n: int) -> int:
+    return int(_lib.load().dsx_suggest_partials(int(n)))
+
+
+def unscale_norm(grad: torch.Tensor, state: torch.Tensor, partials: torch.Tensor, nparts: int | None = None) -> None:
+    """K1: partials[:nparts] = per-block fp64 sums of (grad * inv_scale)^2."""
+    dev = _device(grad)
+    _need(grad, "grad", None, None, dev)
+    gdt = dtype_code(grad.dtype)
+    _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
+    nparts = nparts or partials.numel()
+    _need(partials, "partials", torch.float64, None, dev, 8)
+    if nparts > partials.numel():
+        raise ValueError("nparts exceeds the partials buffer")
+    _lib.call("dsx_unscale_norm", _ptr(grad), gdt, grad.numel(), _ptr(state), _ptr(partials), int(nparts),
+              _stream(dev))
+
+
+def finalize(partials: torch.Tensor, nparts: int, state: torch.Tensor, scaler: DsxScalerConfig,
+             hyper: DsxAdamwHyper, bc_table: torch.Tensor, bc_len: int, out: torch.Tensor) -> None:
+    """K0: norm, skip decision, clip coefficient, step scalars, scaler update."""
+    dev = _device(state)
+    _need(partials, "partials", torch.float64, None, dev, 8)
+    _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
+    _need(out, "scalars", torch.uint8, SCALARS_BYTES, dev, 8)
+    _need(bc_table, "bc_table", torch.float64, None, dev, 8)
+    if bc_table.numel() < 2 * bc_len:
+        raise ValueError("bc_table shorter than bc_len")
+    _lib.call("dsx_finalize", _ptr(partials), int(nparts), _ptr(state), scaler, hyper, _ptr(bc_table), int(bc_len),
+              _ptr(out), _stream(dev))
+
+
+def adamw_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
+               param16: torch.Tensor | None, grad: torch.Tensor, scalars: torch.Tensor) -> None:
+    """K2: AdamW + 16-bit cast over a flat partition (in place)."""
+    dev = _device(master)
+    n = master.numel()
+    for name, t in (("master", master), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
+        _need(t, name, torch.float32, n, dev)
+    _need(grad, "grad", None, n, dev)
+    gdt = dtype_code(grad.dtype)
+    pdt = gdt
+    if param16 is not None:
+        _need(param16, "param16", None, n, dev)
+        pdt = dtype_code(param16.dtype)
+    _need(scalars, "scalars", torch.uint8, SCALARS_BYTES, dev, 8)
+    _lib.call("dsx_adamw_flat", _ptr(master), _ptr(exp_avg), _ptr(exp_avg_sq), _ptr(param16), pdt, _ptr(grad), gdt,
+              n, _ptr(scalars), _stream(dev))
+
+
+def zero_step_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
+                   param16: torch.Tensor | None, grad: torch.Tensor, state: torch.Tensor,
+                   scaler: DsxScalerConfig, hyper: DsxAdamwHyper, bc_table: torch.Tensor, bc_len: int,
+                   partials: torch.Tensor, nparts: int, out: torch.Tensor) -> None:
+    """K1 -> K0 -> K2 in one call (three launches on the current stream)."""
+    dev = _device(master)
+    n = master.numel()
+    for name, t in (("master", master), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
+        _need(t, name, torch.float32, n, dev)
+    _need(grad, "grad", None, n, dev)
+    gdt = dtype_code(grad.dtype)
+    pdt = gdt
+    if param16 is not None:
+        _need(param16, "param16", None, n, dev)
+        pdt = dtype_code(param16.dtype)
+    _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
+    _need(out, "scalars", torch.uint8, SCALARS_BYTES, dev, 8)
+    _need(partials, "partials", torch.float64, None, dev, 8)
+    if nparts > partials.numel():
+        raise ValueError("nparts exceeds the partials buffer")
+    _need(bc_table, "bc_table", torch.float64, None, dev, 8)
+    if bc_table.numel() < 2 * bc_len:
+        raise ValueError("bc_table shorter than bc_len")
+    _lib.call("dsx_zero_step_flat", _ptr(master), _ptr(exp_avg), _ptr(exp_avg_sq), _ptr(param16), pdt, _ptr(grad),
+              gdt, n, _ptr(state), scaler, hyper, _ptr(bc_table), int(bc_len), _ptr(partials), int(nparts), _ptr(out),
+              _stream(dev))
+
+
+# ---- ragged lists (K3) --------------------------------------------------------------
+
+class ChunkTable:
+    """Device-resident tensor and chunk tables of a ragged list (built once;
+    the pointers must stay valid while the table is used)."""
+
+    def __init__(self, masters, exp_avgs, exp_avg_sqs, params16, grads, chunk_elems: int = 65536):
+        k = len(masters)
+        if not (len(exp_avgs) == len(exp_avg_sqs) == len(grads) == k) or (params16 is not None and len(params16) != k):
+            raise ValueError("tensor lists must have equal lengths")
+        if k == 0:
+            raise ValueError("empty tensor list")
+        dev = _device(masters[0])
+        self.device = dev
+        self.gdt = dtype_code(grads[0].dtype)
+        self.pdt = dtype_code(params16[0].dtype) if params16 is not None else self.gdt
+        refs = (_lib.DsxTensorRef * k)()
+        numels = (ctypes.c_int64 * k)()
+        for i in range(k):
+            n = masters[i].numel()
+            for name, t in (("master", masters[i]), ("exp_avg", exp_avgs[i]), ("exp_avg_sq", exp_avg_sqs[i])):
+                _need(t, f"{name}[{i}]", torch.float32, n, dev, 4)
+            _need(grads[i], f"grad[{i}]", grads[0].dtype, n, dev, 2)
+            p16 = None
+            if params16 is not None:
+                p16 = params16[i]
+                _need(p16, f"param16[{i}]", params16[0].dtype, n, dev, 2)
+            refs[i] = _lib.DsxTensorRef(masters[i].data_ptr(), exp_avgs[i].data_ptr(), exp_avg_sqs[i].data_ptr(),
+                                        p16.data_ptr() if p16 is not None else None, grads[i].data_ptr(), n)
+            numels[i] = n
+        L = _lib.load()
+        cnt = L.dsx_count_chunks(numels, k, int(chunk_elems))
+        if cnt < 0:
+            raise ValueError(_lib.last_error())
+        chunks = (_lib.DsxChunk * max(cnt, 1))()
+        got = L.dsx_build_chunks(numels, k, int(chunk_elems), chunks, cnt)
+        if got != cnt:
+            raise RuntimeError(_lib.last_error())
+        self.nchunks = int(cnt)
+        self.numel = int(sum(numels))
+        self.tensors = torch.frombuffer(bytearray(bytes(refs)), dtype=torch.uint8).to(dev)
+        self.chunks = torch.frombuffer(bytearray(bytes(chunks)), dtype=torch.uint8).to(dev)
+
+
+def unscale_norm_multi(table: ChunkTable, state: torch.Tensor, partials: torch.Tensor, nparts: int) -> None:
+    dev = table.device
+    _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
+    _need(partials, "partials", torch.float64, None, dev, 8)
+    if nparts > partials.numel():
+        raise ValueError("nparts exceeds the partials buffer")
+    _lib.call("dsx_unscale_norm_multi", _ptr(table.tensors), _ptr(table.chunks), table.nchunks, table.gdt,
+              _ptr(state), _ptr(partials), int(nparts), _stream(dev))
+
+
+def adamw_multi(table: ChunkTable, scalars: torch.Tensor) -> None:
+    dev = table.device
+    _need(scalars, "scalars", torch.uint8, SCALARS_BYTES, dev, 8)
+    _lib.call("dsx_adamw_multi", _ptr(table.tensors), _ptr(table.chunks), table.nchunks, table.pdt, table.gdt,
+              _ptr(scalars), _stream(dev))

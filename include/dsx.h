@@ -1,0 +1,249 @@
+/*
+ * dsx.h -- C ABI of libdsx.so, the gfx950 (MI355X) ZeRO optimizer step.
+ *
+ * The step over one flat partition of n elements is three stream-ordered
+ * launches with no host synchronisation between them:
+ *
+ *   K1 dsx_unscale_norm   16-bit grads -> per-block fp64 partial sums of
+ *                         (g * inv_scale)^2; a non-finite grad makes the sum
+ *                         non-finite, which is how overflow is detected.
+ *   K0 dsx_finalize       partials -> global norm, found_inf, clip
+ *                         coefficient, optimizer step t, fp32 step scalars,
+ *                         and the loss-scaler update (device-resident state).
+ *   K2 dsx_adamw_flat     one pass: unscale, clip, AdamW, 16-bit cast.
+ *                         Reads 14 B/elt and writes 14 B/elt; returns at
+ *                         once (no memory traffic) when K0 decided to skip.
+ *   K3 dsx_*_multi        K1/K2 over a ragged list of tensors, driven by a
+ *                         chunk table (one launch per pass for any count).
+ *
+ * Conventions
+ *   - Every pointer argument is a DEVICE pointer owned by the caller, except
+ *     where a comment says "host". The library allocates no device memory;
+ *     scratch (the fp64 partials) is passed in by the caller.
+ *   - Element counts are int64_t. Flat buffers must be 16-byte aligned; any n
+ *     is accepted (the n % 8 tail is handled in-kernel).
+ *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL means
+ *     the null stream). No call synchronises the host with the device.
+ *   - Return value: 0 on success; DSX_EINVAL (== hipErrorInvalidValue) for a
+ *     rejected argument; otherwise the hipError_t of a failed launch.
+ *     dsx_last_error() returns a thread-local message for the last failure.
+ *
+ * Arithmetic (fp32, in this order, no FMA contraction except where named):
+ *   g  = f32(g16) * inv_scale;  g = g * clip_coef
+ *   p  = p * decay                               decay = f32(1 - lr*wd)
+ *   m  = fma(w1, g - m, m)           if |w1| < .5, else fma(w1 - 1, g - m, g)
+ *   v  = v * b2;  v = fma(val2 * g, g, v)        val2 = f32(1 - beta2)
+ *   d  = sqrt(v) / bc2s + eps                    IEEE sqrt and division
+ *   p  = p + (nss * m) / d                       nss = f32(-lr / bc1[t])
+ *   p16 = round_to_nearest_even(p)
+ */
+#ifndef DSX_H_
+#define DSX_H_
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSX_ABI_VERSION 1
+
+/* element types */
+#define DSX_F32  0
+#define DSX_F16  1
+#define DSX_BF16 2
+
+/* loss-scaler modes */
+#define DSX_SCALE_NONE    0 /* bf16 / fp32: scale stays 1, overflow still skips */
+#define DSX_SCALE_STATIC  1 /* fp16.loss_scale > 0 */
+#define DSX_SCALE_DYNAMIC 2 /* fp16.loss_scale == 0 */
+
+/* status codes */
+#define DSX_OK     0
+#define DSX_EINVAL 1
+
+/* state error bits (DsxState.error) */
+#define DSX_STATE_ERR_BC_TABLE 1 /* bias-correction table shorter than t */
+
+/* upper bound on the partials one K1 launch may write */
+#define DSX_MAX_PARTIALS 8192
+
+/* Device-resident optimizer + loss-scaler state (64 bytes). */
+typedef struct DsxState {
+  float   scale;          /* loss scale the next backward multiplies by      */
+  int32_t good_steps;     /* clean steps since the last overflow or growth   */
+  int32_t hyst_left;      /* overflows still tolerated before a backoff      */
+  int32_t t;              /* AdamW step count; skipped steps do not count    */
+  int64_t iter;           /* finalize calls so far                           */
+  int64_t overflow_count; /* skipped steps so far                            */
+  int32_t error;          /* DSX_STATE_ERR_* bits, sticky                    */
+  int32_t last_skip;      /* 1 if the last finalize skipped                  */
+  double  last_norm;      /* global grad norm seen by the last finalize      */
+  int64_t reserved[2];
+} DsxState;
+
+/* Loss-scaler configuration (by value). */
+typedef struct DsxScalerConfig {
+  int32_t mode;           /* DSX_SCALE_*                                     */
+  int32_t window;         /* loss_scale_window: clean steps per growth       */
+  int32_t hysteresis;     /* overflows tolerated before a backoff (>= 1)     */
+  int32_t reserved;
+  float   min_scale;      /* min_loss_scale                                  */
+  float   growth_factor;  /* 2.0                                             */
+  float   backoff_factor; /* 0.5                                             */
+  float   reserved2;
+} DsxScalerConfig;
+
+/* AdamW hyper-parameters for one step (by value; host doubles, as torch). */
+typedef struct DsxAdamwHyper {
+  double lr;
+  double beta1;
+  double beta2;
+  double eps;
+  double weight_decay;
+  double max_grad_norm;   /* <= 0 disables clipping                          */
+  double clip_eps;        /* added to the norm in the clip coefficient (1e-6) */
+} DsxAdamwHyper;
+
+/* fp32 scalars of one step, written by dsx_finalize (64 bytes). */
+typedef struct DsxStepScalars {
+  int32_t skip;           /* nonzero: overflow (or error), K2 does nothing   */
+  int32_t t;              /* step number used for bias correction            */
+  float   inv_scale;      /* 1 / scale used by this step's backward          */
+  float   clip_coef;      /* 1.0f when not clipping                          */
+  float   decay;          /* f32(1 - lr*wd), 1.0f when wd == 0               */
+  float   w1;             /* f32(1 - beta1), lerp weight                     */
+  float   w1m1;           /* w1 - 1.0f                                       */
+  float   b2;             /* f32(beta2)                                      */
+  float   val2;           /* f32(1 - beta2)                                  */
+  float   eps;            /* f32(eps)                                        */
+  float   bc2s;           /* f32(sqrt(1 - beta2^t))                          */
+  float   nss;            /* f32(-(lr / (1 - beta1^t)))                      */
+  double  sumsq;          /* sum of squared unscaled grads (fp64)            */
+  double  norm;           /* sqrt(sumsq)                                     */
+} DsxStepScalars;
+
+/* One tensor of a ragged list (K3). master/exp_avg/exp_avg_sq fp32;
+ * param16 and grad are 16-bit of the dtype given to the call; param16 may be
+ * NULL (no cast written). */
+typedef struct DsxTensorRef {
+  float*      master;
+  float*      exp_avg;
+  float*      exp_avg_sq;
+  void*       param16;
+  const void* grad;
+  int64_t     numel;
+} DsxTensorRef;
+
+/* One chunk of a ragged list: elements [start, start+len) of tensor `tensor`. */
+typedef struct DsxChunk {
+  int32_t tensor;
+  int32_t reserved;
+  int64_t start;
+  int64_t len;
+} DsxChunk;
+
+/* ---- library ---------------------------------------------------------- */
+
+int         dsx_abi_version(void);
+const char* dsx_last_error(void);
+
+/* Launch-shape override for the current process (library tuning; no
+ * counterpart in the reference): K1 and K2 blocks per CU, K2 slots per
+ * thread per trip (2, 4 or 8) and the nontemporal hint (0/1). */
+int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll,
+                   int nontemporal);
+
+/* Partials a K1 launch over n elements should use on the current device
+ * (a multiple of the CU count, <= DSX_MAX_PARTIALS). */
+int32_t dsx_suggest_partials(int64_t n);
+
+/* Number of chunks dsx_build_chunks produces (host only, no GPU). */
+int64_t dsx_count_chunks(const int64_t* numels /* host */, int32_t ntensors,
+                         int64_t chunk_elems);
+
+/* Fill `out` (host, capacity cap) with the chunk table of a ragged list.
+ * Returns the count, or -1 (with dsx_last_error) on bad arguments. */
+int64_t dsx_build_chunks(const int64_t* numels /* host */, int32_t ntensors,
+                         int64_t chunk_elems, DsxChunk* out /* host */,
+                         int64_t cap);
+
+/* ---- state ------------------------------------------------------------ */
+
+/* Write an initial DsxState (scale, hysteresis; counters zero) on `stream`.
+ * Replaces GradScaler(init_scale=2**initial_scale_power, ...) construction,
+ * Src/zero/optimizer.py:102-110; fields Src/zero/__init__.py:103-109. */
+int dsx_state_init(DsxState* state, float init_scale, int32_t hysteresis,
+                   void* stream);
+
+/* ---- K1: unscale + inf/NaN detect + squared L2 norm ------------------- */
+
+/* partials[0..nparts) = per-block sums of (f32(g) * inv_scale)^2 in fp64,
+ * inv_scale = f32(1 / (double)state->scale). Grads are only read.
+ * Replaces Src/zero/utils.py:126-154 (compute_norm, one .item() per
+ * tensor) and the unscale/found_inf of GradScaler the engine intends
+ * (Src/zero/optimizer.py:236-242, 276-298). */
+int dsx_unscale_norm(const void* grad, int grad_dtype, int64_t n,
+                     const DsxState* state, double* partials, int32_t nparts,
+                     void* stream);
+
+/* ---- K0: finalize ------------------------------------------------------ */
+
+/* Reduce the partials; decide skip (non-finite sum); on a clean step advance
+ * t and emit the step scalars (clip coefficient max_norm/(norm+clip_eps) if
+ * norm > max_norm); update the loss scaler. bc_table holds bc_len pairs
+ * {1 - beta1^t, (1 - beta2^t)^0.5} for t = 1..bc_len, computed on the host
+ * in double exactly as torch/optim/adam.py:529-535 does.
+ * Replaces Src/zero/optimizer.py:212-274 (skip/clip/update order),
+ * Src/zero/utils.py:187-216 (clip) and GradScaler.update
+ * (Src/zero/optimizer.py:265-266). */
+int dsx_finalize(const double* partials, int32_t nparts, DsxState* state,
+                 DsxScalerConfig scaler, DsxAdamwHyper hyper,
+                 const double* bc_table, int32_t bc_len, DsxStepScalars* out,
+                 void* stream);
+
+/* ---- K2: AdamW + cast over a flat partition -------------------------- */
+
+/* In place on master/exp_avg/exp_avg_sq (fp32, n elements); writes param16
+ * (param_dtype F16/BF16; may be NULL). No-op when scalars->skip.
+ * Replaces torch.optim.AdamW.step called at Src/zero/stage1.py:522-525 and
+ * Src/zero/stage2.py:609-612, and FusedKernels.fused_adam_step,
+ * Src/engine.py:871-890. */
+int dsx_adamw_flat(float* master, float* exp_avg, float* exp_avg_sq,
+                   void* param16, int param_dtype, const void* grad,
+                   int grad_dtype, int64_t n, const DsxStepScalars* scalars,
+                   void* stream);
+
+/* K1 -> K0 -> K2 over one flat partition: the whole engine.step() of
+ * Src/zero/optimizer.py:212-274 for stage 1/2 at world size 1. `partials`
+ * has room for nparts doubles; `out` receives this step's scalars. */
+int dsx_zero_step_flat(float* master, float* exp_avg, float* exp_avg_sq,
+                       void* param16, int param_dtype, const void* grad,
+                       int grad_dtype, int64_t n, DsxState* state,
+                       DsxScalerConfig scaler, DsxAdamwHyper hyper,
+                       const double* bc_table, int32_t bc_len,
+                       double* partials, int32_t nparts, DsxStepScalars* out,
+                       void* stream);
+
+/* ---- K3: ragged lists (multi-tensor apply) ---------------------------- */
+
+/* K1 over the chunks of a tensor list (tensors/chunks are device arrays).
+ * Replaces the per-tensor loop of Src/zero/utils.py:147-152. */
+int dsx_unscale_norm_multi(const DsxTensorRef* tensors, const DsxChunk* chunks,
+                           int64_t nchunks, int grad_dtype,
+                           const DsxState* state, double* partials,
+                           int32_t nparts, void* stream);
+
+/* K2 over the chunks of a tensor list; per element identical to
+ * dsx_adamw_flat. Replaces torch AdamW's per-tensor loop
+ * (torch/optim/adam.py:396) behind Src/zero/stage2.py:609-612. */
+int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks,
+                    int64_t nchunks, int param_dtype, int grad_dtype,
+                    const DsxStepScalars* scalars, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSX_H_ */

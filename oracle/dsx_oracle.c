@@ -1,0 +1,172 @@
+/*
+ * dsx_oracle.c -- CPU restatement of the ZeRO optimizer step, used ONLY as a
+ * checker (tests/, __graft_entry__.smoke(), bench.py's cpu_baseline leg).
+ * Nothing in the product links or calls this file.
+ *
+ * What it restates, and where the reference defines it:
+ *   - squared L2 norm of the unscaled grads, summed in fp64:
+ *       Src/zero/utils.py:126-154 (compute_norm), Src/zero/stage2.py:683-707
+ *   - unscale by the inverse loss scale and non-finite detection:
+ *       Src/zero/optimizer.py:236-242, 276-298 (GradScaler.unscale_ semantics,
+ *       torch/amp/grad_scaler.py:235-286)
+ *   - clipping g *= max_norm / (norm + 1e-6) iff norm > max_norm:
+ *       Src/zero/utils.py:187-216
+ *   - AdamW (decoupled weight decay) with torch's per-op rounding, called by
+ *       the reference at Src/zero/stage1.py:522-525, Src/zero/stage2.py:609-612;
+ *       algorithm torch/optim/adam.py:347-552 (_single_tensor_adam):
+ *         p *= f32(1 - lr*wd)                         adam.py:415-418
+ *         m  = lerp(m, g, f32(1 - beta1))             adam.py:456
+ *              (ATen's vectorised lerp: one fused multiply-add,
+ *               torch/include/ATen/native/Lerp.h:21-35 for the branch)
+ *         v  = fma(f32(1 - beta2) * g, g, v * beta2)  adam.py:476 (addcmul_)
+ *         d  = sqrt(v) / f32(bc2_sqrt) + f32(eps)     adam.py:543-545
+ *         p  = p + (f32(-lr/bc1) * m) / d             adam.py:547 (addcdiv_)
+ *   - the 16-bit cast of the updated fp32 master (round to nearest even).
+ *
+ * Built with -ffp-contract=off so that every operation rounds on its own;
+ * fmaf() is called exactly where torch's CPU kernels fuse. sqrtf() and '/'
+ * are IEEE correctly rounded here. torch's own CPU sqrt (MKL VML) is not, so
+ * the master weight can differ from torch CPU by 1 ulp; m and v cannot.
+ *
+ * The fp16/bf16 conversions are written from the IEEE 754 binary16 and
+ * bfloat16 definitions, without hardware conversion instructions.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#define DSXO_F16 1
+#define DSXO_BF16 2
+
+typedef struct DsxoScalars {
+  float inv_scale, clip_coef, decay, w1, w1m1, b2, val2, eps, bc2s, nss;
+} DsxoScalars;
+
+static inline uint32_t f2u(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+static inline float u2f(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+
+/* binary16 -> binary32, exact. */
+float dsxo_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1Fu;
+  const uint32_t man = h & 0x3FFu;
+  if (exp == 0x1Fu) return u2f(sign | 0x7F800000u | (man << 13)); /* inf / NaN */
+  if (exp != 0) return u2f(sign | ((exp + 112u) << 23) | (man << 13));
+  /* zero or subnormal: man * 2^-24 is exact in binary32 */
+  const float mag = (float)man * 0x1p-24f;
+  return sign ? -mag : mag;
+}
+
+float dsxo_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* binary32 -> binary16, round to nearest, ties to even. NaN -> sign|0x7E00. */
+uint16_t dsxo_f32_to_f16(float x) {
+  const uint32_t u = f2u(x);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return (uint16_t)(sign | 0x7E00u);
+  if (a == 0x7F800000u) return (uint16_t)(sign | 0x7C00u);
+  const int e = (int)(a >> 23) - 127; /* unbiased exponent */
+  if (e > 15) return (uint16_t)(sign | 0x7C00u);
+  if (e >= -14) {
+    /* normal range of binary16: keep 10 of 23 mantissa bits */
+    uint32_t mant = (a & 0x7FFFFFu) | 0x800000u; /* 24 bits */
+    uint32_t q = mant >> 13, rem = mant & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q += 1;
+    uint32_t exp16 = (uint32_t)(e + 15);
+    if (q == 0x800u) { q = 0x400u; exp16 += 1; } /* mantissa carried out */
+    if (exp16 >= 31) return (uint16_t)(sign | 0x7C00u);
+    return (uint16_t)(sign | (exp16 << 10) | (q & 0x3FFu));
+  }
+  if (e < -25) return (uint16_t)sign; /* below half the smallest subnormal */
+  /* subnormal binary16: value = q * 2^-24 */
+  const uint32_t mant = (a & 0x7FFFFFu) | 0x800000u; /* value = mant * 2^(e-23) */
+  const int shift = -e - 1;                          /* 2^(e-23) / 2^-24 = 2^(e+1) */
+  uint32_t q = mant >> shift;
+  const uint32_t rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1);
+  if (rem > half || (rem == half && (q & 1u))) q += 1;
+  return (uint16_t)(sign | q); /* q == 0x400 rolls into the smallest normal */
+}
+
+/* binary32 -> bfloat16, round to nearest, ties to even. NaN -> 0x7FC0. */
+uint16_t dsxo_f32_to_bf16(float x) {
+  const uint32_t u = f2u(x);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  const uint32_t hi = u >> 16, lo = u & 0xFFFFu;
+  uint32_t r = hi;
+  if (lo > 0x8000u || (lo == 0x8000u && (hi & 1u))) r += 1; /* may carry into inf: correct */
+  return (uint16_t)r;
+}
+
+static inline float load16(const uint16_t* g, int64_t i, int dt) {
+  return dt == DSXO_BF16 ? dsxo_bf16_to_f32(g[i]) : dsxo_f16_to_f32(g[i]);
+}
+
+/* Sum over i of (double)(f32(g[i]) * inv_scale)^2, sequentially in index
+ * order. Non-finite iff some unscaled grad is inf or NaN. */
+double dsxo_sumsq(const uint16_t* g, int dt, int64_t n, float inv_scale) {
+  double acc = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const float a = load16(g, i, dt) * inv_scale;
+    acc += (double)a * (double)a;
+  }
+  return acc;
+}
+
+/* Same sum, split into `nblocks` contiguous blocks summed separately and then
+ * added in block order -- a second summation order for cross-checks. */
+double dsxo_sumsq_blocked(const uint16_t* g, int dt, int64_t n, float inv_scale, int64_t nblocks) {
+  double total = 0.0;
+  if (nblocks < 1) nblocks = 1;
+  const int64_t per = (n + nblocks - 1) / nblocks;
+  for (int64_t b = 0; b < nblocks; ++b) {
+    const int64_t lo = b * per, hi = lo + per < n ? lo + per : n;
+    if (lo >= n) break;
+    total += dsxo_sumsq(g + lo, dt, hi - lo, inv_scale);
+  }
+  return total;
+}
+
+static inline void step_elt(float graw, float* p, float* m, float* v, const DsxoScalars* s) {
+  float g = graw * s->inv_scale;
+  g = g * s->clip_coef;
+  float pp = *p * s->decay;
+  const float d = g - *m;
+  const float mm = (fabsf(s->w1) < 0.5f) ? fmaf(s->w1, d, *m) : fmaf(s->w1m1, d, g);
+  float vv = *v * s->b2;
+  vv = fmaf(s->val2 * g, g, vv);
+  const float den = sqrtf(vv) / s->bc2s + s->eps;
+  pp = pp + (s->nss * mm) / den;
+  *p = pp;
+  *m = mm;
+  *v = vv;
+}
+
+/* One AdamW step over n elements, in place; p16 (may be NULL) receives the
+ * cast master. Elements are independent, so the loop may run in parallel. */
+void dsxo_adamw(float* p, float* m, float* v, uint16_t* p16, int pdt, const uint16_t* g, int gdt, int64_t n,
+                const DsxoScalars* s) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    step_elt(load16(g, i, gdt), p + i, m + i, v + i, s);
+    if (p16) p16[i] = pdt == DSXO_BF16 ? dsxo_f32_to_bf16(p[i]) : dsxo_f32_to_f16(p[i]);
+  }
+}
+
+/* Array conversions used by the tests. */
+void dsxo_cast_f32(const float* x, uint16_t* out, int dt, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = dt == DSXO_BF16 ? dsxo_f32_to_bf16(x[i]) : dsxo_f32_to_f16(x[i]);
+}
+
+void dsxo_widen(const uint16_t* h, float* out, int dt, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = load16(h, i, dt);
+}
+
+int dsxo_num_threads(void) {
+#ifdef _OPENMP
+  extern int omp_get_max_threads(void);
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}

@@ -1,0 +1,361 @@
+"""GPU parity: the HIP kernels (through libdsx.so's C ABI) against the CPU
+oracle on the same seeded inputs. Integer/byte results and fp32 state must be
+bit-identical: the kernels follow the oracle's operation order and rounding
+(IEEE division/sqrt, explicit fma only), so any difference is a bug."""
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import (BF16, F16, f32_to_torch, make_state, np16_to_torch, torch16_to_np)
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[gpu-test] {msg}", file=sys.stderr, flush=True)
+
+
+def _run_k2(gpu, p, m, v, g16, gdt, pdt, sc_host, with_p16=True):
+    import torch
+    from distributedspeed_amd import _lib, ops
+    n = p.size
+    tp, tm, tv = (f32_to_torch(a, gpu) for a in (p, m, v))
+    tg = np16_to_torch(g16, gdt, gpu)
+    tp16 = torch.empty(n, dtype=torch.float16 if pdt == F16 else torch.bfloat16, device=gpu) if with_p16 else None
+    c = _lib.DsxStepScalars()
+    c.skip = 0
+    c.t = 1
+    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss"):
+        setattr(c, k, getattr(sc_host, k))
+    scal = ops.scalars_from_host(c, gpu)
+    ops.adamw_flat(tp, tm, tv, tp16, tg, scal)
+    torch.cuda.synchronize()
+    return (tp.cpu().numpy(), tm.cpu().numpy(), tv.cpu().numpy(),
+            torch16_to_np(tp16) if with_p16 else None)
+
+
+HYPERS = [
+    dict(lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01),   # config 1 (MLP)
+    dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1),     # config 3 (Llama-3-8B)
+    dict(lr=1e-2, beta1=0.3, beta2=0.5, eps=1e-6, weight_decay=0.0),      # lerp's |w| >= 0.5 branch, wd = 0
+]
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 7, 8, 1000, 65537, 262147])
+@pytest.mark.parametrize("gdt,pdt", [(F16, F16), (BF16, BF16), (BF16, F16)])
+@pytest.mark.parametrize("hi", range(len(HYPERS)))
+def test_k2_single_step_bit_exact(gpu, oracle, n, gdt, pdt, hi):
+    O = oracle
+    h = O.Hyper(**HYPERS[hi])
+    scale = 2.0 ** 16 if gdt == F16 else 1.0
+    p, m, v, g16 = make_state(n, seed=1000 + n + hi, gdt=gdt, g_sigma=1e-3, scale=scale)
+    t = 1 + hi * 3
+    coef = 0.37 if hi == 1 else 1.0
+    sc = O.step_scalars(h, t, O.inv_scale_of(scale), coef)
+    _say(f"k2 n={n} gdt={gdt} pdt={pdt} hyper={hi}")
+    gp, gm, gv, gp16 = _run_k2(gpu, p, m, v, g16, gdt, pdt, sc)
+    rp, rm, rv, rp16 = p.copy(), m.copy(), v.copy(), np.empty(n, np.uint16)
+    O.adamw(rp, rm, rv, rp16, pdt, g16, gdt, sc)
+    for name, a, b in (("master", gp, rp), ("exp_avg", gm, rm), ("exp_avg_sq", gv, rv)):
+        bad = O.ulp_diff_f32(a, b) != 0
+        assert not bad.any(), f"{name}: {bad.sum()} mismatches, first at {np.flatnonzero(bad)[:5]}"
+    assert np.array_equal(gp16, rp16), f"param16: {(gp16 != rp16).sum()} mismatches"
+
+
+def test_k2_without_param16(gpu, oracle):
+    O = oracle
+    n = 4099
+    p, m, v, g16 = make_state(n, 5, BF16, 1e-3)
+    sc = O.step_scalars(O.Hyper(), 2, 1.0, 1.0)
+    gp, gm, gv, _ = _run_k2(gpu, p, m, v, g16, BF16, BF16, sc, with_p16=False)
+    O.adamw(p, m, v, None, BF16, g16, BF16, sc)
+    assert np.array_equal(gp.view(np.uint32), p.view(np.uint32))
+    assert np.array_equal(gm.view(np.uint32), m.view(np.uint32))
+    assert np.array_equal(gv.view(np.uint32), v.view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [0, 1, 9, 1000, 1 << 20, 3_000_017])
+@pytest.mark.parametrize("gdt", [F16, BF16])
+def test_k1_norm_matches_oracle(gpu, oracle, n, gdt):
+    import torch
+    from distributedspeed_amd import ops
+    O = oracle
+    scale = 2.0 ** 16 if gdt == F16 else 1.0
+    _, _, _, g16 = make_state(max(n, 1), 77 + n, gdt, 1e-3, scale=scale)
+    g16 = g16[:n]
+    st = ops.new_state(gpu, scale, 1)
+    nparts = ops.suggest_partials(n)
+    parts = torch.zeros(nparts, dtype=torch.float64, device=gpu)
+    tg = np16_to_torch(g16, gdt, gpu) if n else torch.empty(0, dtype=torch.float16 if gdt == F16 else torch.bfloat16,
+                                                             device=gpu)
+    ops.unscale_norm(tg, st, parts, nparts)
+    got = float(parts.sum().item())
+    ref = O.sumsq(g16, gdt, O.inv_scale_of(scale)) if n else 0.0
+    assert math.isfinite(got)
+    assert got == pytest.approx(ref, rel=1e-12, abs=0.0)
+
+
+@pytest.mark.parametrize("pos", ["first", "middle", "last", "tail"])
+@pytest.mark.parametrize("bad", ["+inf", "-inf", "nan"])
+@pytest.mark.parametrize("gdt", [F16, BF16])
+def test_k1_detects_nonfinite(gpu, oracle, pos, bad, gdt):
+    import torch
+    from distributedspeed_amd import ops
+    n = 100_003
+    _, _, _, g16 = make_state(n, 3, gdt, 1e-3, edges=False)
+    code = {F16: {"+inf": 0x7C00, "-inf": 0xFC00, "nan": 0x7E00},
+            BF16: {"+inf": 0x7F80, "-inf": 0xFF80, "nan": 0x7FC0}}[gdt][bad]
+    idx = {"first": 0, "middle": n // 2, "last": n - 1, "tail": n - 2}[pos]
+    g16[idx] = code
+    st = ops.new_state(gpu, 1.0, 1)
+    parts = torch.zeros(ops.suggest_partials(n), dtype=torch.float64, device=gpu)
+    ops.unscale_norm(np16_to_torch(g16, gdt, gpu), st, parts)
+    assert not math.isfinite(float(parts.sum().item()))
+    assert not math.isfinite(oracle.sumsq(g16, gdt, 1.0))
+
+
+def _flat_run(gpu, O, n, gdt, pdt, hyper, scaler_cfg, steps, seed, g_sigma, inject=None, p_sigma=0.02):
+    """Run `steps` full steps through FlatStep and the oracle side by side;
+    compare every step bit-for-bit. inject(step) -> index to set to +inf."""
+    import torch
+    from distributedspeed_amd import ops
+    from distributedspeed_amd.flat_step import AdamWHyper, FlatStep, ScalerConfig
+
+    p, m, v, _ = make_state(n, seed, gdt, g_sigma, edges=False, mv_warm=False, p_sigma=p_sigma)
+    p16 = O.cast16(p, pdt)
+    hp = AdamWHyper(**hyper)
+    sc = ScalerConfig(**scaler_cfg)
+    fs = FlatStep(n, gpu, hp, sc)
+    tp, tm, tv = (f32_to_torch(a, gpu) for a in (p, m, v))
+    tp16 = np16_to_torch(p16, pdt, gpu)
+    ospec = O.LossScalerSpec(scale=sc.init_scale if sc.mode != "none" else 1.0, window=sc.window,
+                             hysteresis=sc.hysteresis if sc.mode == "dynamic" else 1, min_scale=sc.min_scale,
+                             dynamic=sc.mode == "dynamic")
+    orc = O.ZeroStepOracle(p, m, v, p16, pdt, gdt, O.Hyper(**hyper), ospec)
+    rng = np.random.default_rng(seed + 1)
+    history = []
+    for step in range(1, steps + 1):
+        scale = ospec.scale
+        g32 = (rng.standard_normal(n) * g_sigma * scale).astype(np.float32)
+        g16 = O.cast16(g32, gdt)
+        if inject is not None:
+            idx = inject(step)
+            if idx is not None:
+                g16[idx] = 0x7C00 if gdt == F16 else 0x7F80
+        fs.step(tp, tm, tv, tp16, np16_to_torch(g16, gdt, gpu))
+        r = orc.step(g16)
+        scal = fs.read_scalars()
+        st = fs.read_state()
+        history.append((bool(scal.skip), st.scale, st.t))
+        assert bool(scal.skip) == r.skipped, f"step {step}: skip {scal.skip} vs {r.skipped}"
+        assert st.scale == r.scale_next, f"step {step}: scale {st.scale} vs {r.scale_next}"
+        assert st.t == r.t
+        if not r.skipped:
+            assert scal.norm == pytest.approx(r.norm, rel=1e-12)
+            assert scal.clip_coef == np.float32(r.clip_coef)
+        gp, gm, gv = tp.cpu().numpy(), tm.cpu().numpy(), tv.cpu().numpy()
+        for name, a, b in (("master", gp, p), ("exp_avg", gm, m), ("exp_avg_sq", gv, v)):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {step} {name} differs"
+        assert np.array_equal(torch16_to_np(tp16), p16), f"step {step} param16 differs"
+    return history, fs
+
+
+def test_config1_mlp_ten_steps(gpu, oracle):
+    """3-layer MLP partition, fp16, static scale 2^16, 10 steps."""
+    n = 784 * 1024 + 1024 + 1024 * 1024 + 1024 + 1024 * 10 + 10
+    assert n == 1_863_690
+    _say("config1 mlp 10 steps")
+    hist, _ = _flat_run(gpu, oracle, n, F16, F16,
+                        dict(lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, max_grad_norm=0.0),
+                        dict(mode="static", init_scale=2.0 ** 16), steps=10, seed=0, g_sigma=0.01)
+    assert [h[2] for h in hist] == list(range(1, 11))
+
+
+def test_config2_gpt2_overflow_at_step3(gpu, oracle):
+    """configs[1] semantics at reduced size: fp16, dynamic scale 2^16,
+    hysteresis 1, clip 1.0; step 3 carries one +inf -> skip and halve."""
+    n = 2_000_003
+    inj_rng = np.random.default_rng(1000 + 1)
+    idx3 = int(inj_rng.integers(0, n))
+    _say("config2 gpt2 overflow")
+    hist, fs = _flat_run(gpu, oracle, n, F16, F16,
+                         dict(lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, max_grad_norm=1.0),
+                         dict(mode="dynamic", init_scale=2.0 ** 16, window=1000, hysteresis=1, min_scale=1.0),
+                         steps=20, seed=1, g_sigma=1e-3, inject=lambda s: idx3 if s == 3 else None)
+    assert [h[0] for h in hist] == [False, False, True] + [False] * 17
+    assert hist[1][1] == 2.0 ** 16 and hist[2][1] == 2.0 ** 15
+    assert hist[-1][2] == 19
+    assert fs.read_state().overflow_count == 1
+
+
+def test_scaler_sequence_config4_semantics(gpu, oracle):
+    """configs[3] scaler (init 2^16, window 1000, hysteresis 2, min 1) over
+    2000 steps with Bernoulli(1e-3) overflows, plus a dense variant that
+    reaches every branch (growth, hysteresis countdown, min clamp)."""
+    for (steps, prob, window, hyst, min_scale, seed) in ((2000, 1e-3, 1000, 2, 1.0, 4),
+                                                        (600, 0.3, 7, 3, 2.0 ** 13, 5)):
+        rng = np.random.default_rng(seed + 1000)
+        flags = rng.random(steps) < prob
+        _say(f"scaler sequence steps={steps} p={prob}")
+        hist, _ = _flat_run(gpu, oracle, 1024, F16, F16,
+                            dict(lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, max_grad_norm=0.0),
+                            dict(mode="dynamic", init_scale=2.0 ** 16, window=window, hysteresis=hyst,
+                                 min_scale=min_scale),
+                            steps=steps, seed=seed, g_sigma=1e-3,
+                            inject=lambda s: 5 if flags[s - 1] else None)
+        assert sum(h[0] for h in hist) == int(flags.sum())
+
+
+def test_llama8b_shard_full_size_one_step(gpu, oracle):
+    """configs[2] at full size (1,003,782,656 elements): one step, bit-exact
+    against the oracle, plus the step's norm against an fp64 brute force."""
+    import torch
+    from distributedspeed_amd.flat_step import AdamWHyper, FlatStep, ScalerConfig
+    O = oracle
+    n = 1_003_782_656
+    _say("llama8b full-size step: generating")
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(3)
+    tp = torch.empty(n, dtype=torch.float32, device=gpu).normal_(0.0, 0.02, generator=gen)
+    tg = torch.empty(n, dtype=torch.bfloat16, device=gpu)
+    for s in range(0, n, 1 << 27):
+        e = min(n, s + (1 << 27))
+        tg[s:e].copy_(torch.empty(e - s, device=gpu).normal_(0.0, 5e-4, generator=gen))
+    tm = torch.zeros(n, dtype=torch.float32, device=gpu)
+    tv = torch.zeros(n, dtype=torch.float32, device=gpu)
+    tp16 = tp.to(torch.bfloat16)
+    p = tp.cpu().numpy()
+    g16 = torch16_to_np(tg)
+    hyper = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    fs = FlatStep(n, gpu, AdamWHyper(**hyper), ScalerConfig(mode="none"))
+    _say("llama8b full-size step: gpu step")
+    fs.step(tp, tm, tv, tp16, tg)
+    scal = fs.read_scalars()
+    _say("llama8b full-size step: oracle step")
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    p16 = np.empty(n, np.uint16)
+    ss = O.sumsq(g16, BF16, 1.0)
+    assert scal.sumsq == pytest.approx(ss, rel=1e-12)
+    coef = O.clip_coef(math.sqrt(ss), 1.0)
+    assert coef < 1.0 and scal.clip_coef == np.float32(coef)
+    O.adamw(p, m, v, p16, BF16, g16, BF16, O.step_scalars(O.Hyper(**hyper), 1, 1.0, coef))
+    _say("llama8b full-size step: compare")
+    assert np.array_equal(tp.cpu().numpy().view(np.uint32), p.view(np.uint32))
+    assert np.array_equal(tm.cpu().numpy().view(np.uint32), m.view(np.uint32))
+    assert np.array_equal(tv.cpu().numpy().view(np.uint32), v.view(np.uint32))
+    assert np.array_equal(torch16_to_np(tp16), p16)
+
+
+def test_multi_tensor_equals_flat(gpu, oracle):
+    """K3 over a ragged list (including tensors at unaligned offsets) is
+    bit-identical to K2 over the same elements; its norm matches K1's."""
+    import torch
+    from distributedspeed_amd import ops
+    O = oracle
+    sizes = [4096 * 3, 1, 7, 14336 + 3, 65536 * 2 + 5, 4096, 9]
+    offs = []
+    pos = 0
+    for i, s in enumerate(sizes):
+        pos += (i % 3)  # 0, 1 or 2 elements of padding -> some views are unaligned
+        offs.append(pos)
+        pos += s
+    total = pos
+    p, m, v, g16 = make_state(total, 11, F16, 1e-3, scale=2.0 ** 10)
+    h = O.Hyper(lr=1e-3, weight_decay=0.05)
+    sc = O.step_scalars(h, 3, O.inv_scale_of(2.0 ** 10), 0.5)
+    # flat reference through K2 on the whole buffer
+    gp, gm, gv, gp16 = _run_k2(gpu, p, m, v, g16, F16, F16, sc)
+    # ragged list through K3
+    tp, tm, tv = (f32_to_torch(a, gpu) for a in (p, m, v))
+    tg = np16_to_torch(g16, F16, gpu)
+    tp16 = torch.zeros(total, dtype=torch.float16, device=gpu)
+    views = lambda t: [t[o:o + s] for o, s in zip(offs, sizes)]  # noqa: E731
+    table = ops.ChunkTable(views(tp), views(tm), views(tv), views(tp16), views(tg), chunk_elems=4096)
+    c = oracle  # noqa: F841
+    from distributedspeed_amd import _lib
+    hs = _lib.DsxStepScalars()
+    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss"):
+        setattr(hs, k, getattr(sc, k))
+    scal = ops.scalars_from_host(hs, gpu)
+    ops.adamw_multi(table, scal)
+    st = ops.new_state(gpu, 2.0 ** 10, 1)
+    parts = torch.zeros(64, dtype=torch.float64, device=gpu)
+    ops.unscale_norm_multi(table, st, parts, 64)
+    torch.cuda.synchronize()
+    covered = np.zeros(total, bool)
+    for o, s in zip(offs, sizes):
+        covered[o:o + s] = True
+    for name, a, b in (("master", tp.cpu().numpy(), gp), ("exp_avg", tm.cpu().numpy(), gm),
+                       ("exp_avg_sq", tv.cpu().numpy(), gv)):
+        assert np.array_equal(a[covered].view(np.uint32), b[covered].view(np.uint32)), name
+        # padding elements are not part of any tensor and must be untouched
+        orig = {"master": p, "exp_avg": m, "exp_avg_sq": v}[name]
+        assert np.array_equal(a[~covered].view(np.uint32), orig[~covered].view(np.uint32)), name
+    assert np.array_equal(torch16_to_np(tp16)[covered], gp16[covered])
+    ref = sum(O.sumsq(np.ascontiguousarray(g16[o:o + s]), F16, O.inv_scale_of(2.0 ** 10)) for o, s in zip(offs, sizes))
+    assert float(parts.sum().item()) == pytest.approx(ref, rel=1e-12)
+
+
+def test_skip_leaves_state_bit_identical(gpu, oracle):
+    import torch
+    from distributedspeed_amd.flat_step import AdamWHyper, FlatStep, ScalerConfig
+    n = 10_007
+    p, m, v, g16 = make_state(n, 21, F16, 1e-3, scale=2.0 ** 16)
+    g16[n - 1] = 0x7E00  # NaN in the tail
+    tp, tm, tv = (f32_to_torch(a, gpu) for a in (p, m, v))
+    tp16 = np16_to_torch(oracle.cast16(p, F16), F16, gpu)
+    before = [t.clone() for t in (tp, tm, tv, tp16)]
+    fs = FlatStep(n, gpu, AdamWHyper(max_grad_norm=1.0),
+                  ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, hysteresis=2))
+    fs.step(tp, tm, tv, tp16, np16_to_torch(g16, F16, gpu))
+    st = fs.read_state()
+    assert fs.read_scalars().skip == 1 and st.t == 0 and st.overflow_count == 1
+    assert st.scale == 2.0 ** 16 and st.hyst_left == 1  # hysteresis absorbs the first overflow
+    for a, b in zip(before, (tp, tm, tv, tp16)):
+        assert torch.equal(a.view(torch.uint8) if a.dtype != torch.float32 else a.view(torch.int32),
+                           b.view(torch.uint8) if b.dtype != torch.float32 else b.view(torch.int32))
+
+
+def test_short_bias_table_flags_error_and_skips(gpu):
+    """A bias-correction table shorter than t is reported through the state's
+    error bits and the step is skipped; the kernel still exits normally."""
+    import torch
+    from distributedspeed_amd import _lib, ops
+    from distributedspeed_amd.flat_step import AdamWHyper, ScalerConfig
+    n = 4096
+    tp = torch.ones(n, device=gpu)
+    tm, tv = torch.zeros(n, device=gpu), torch.zeros(n, device=gpu)
+    tg = torch.full((n,), 0.5, dtype=torch.bfloat16, device=gpu)
+    st = ops.new_state(gpu, 1.0, 1)
+    sc = ops.new_scalars(gpu)
+    parts = torch.zeros(8, dtype=torch.float64, device=gpu)
+    bc = torch.zeros(2, dtype=torch.float64, device=gpu)
+    ops.zero_step_flat(tp, tm, tv, None, tg, st, ScalerConfig().to_c(), AdamWHyper().to_c(), bc, 0, parts, 8, sc)
+    s = ops.read_state(st)
+    assert s.error & _lib.DSX_STATE_ERR_BC_TABLE
+    assert ops.read_scalars(sc).skip == 1
+    assert torch.equal(tp, torch.ones(n, device=gpu))
+
+
+def test_host_rejects_bad_arguments(gpu):
+    import torch
+    from distributedspeed_amd import _lib, ops
+    n = 1024
+    buf = torch.zeros(n + 4, device=gpu)
+    tm, tv = torch.zeros(n, device=gpu), torch.zeros(n, device=gpu)
+    tg = torch.zeros(n, dtype=torch.bfloat16, device=gpu)
+    sc = ops.new_scalars(gpu)
+    with pytest.raises(ValueError):  # master view 4 bytes off alignment
+        ops.adamw_flat(buf[1:n + 1], tm, tv, None, tg, sc)
+    with pytest.raises(ValueError):
+        ops.adamw_flat(torch.zeros(n + 1, device=gpu), tm, tv, None, tg, sc)
+    with pytest.raises(TypeError):
+        ops.adamw_flat(buf[:n], tm, tv, None, tg.float(), sc)
+    with pytest.raises(_lib.DsxError):  # the C layer's own check, reached directly
+        _lib.call("dsx_adamw_flat", buf[1:].data_ptr(), tm.data_ptr(), tv.data_ptr(), None, 2, tg.data_ptr(), 2,
+                  n, sc.data_ptr(), None)
