@@ -64,12 +64,13 @@ def make_state(n: int, seed: int, gdt: int, g_sigma: float, scale: float = 1.0, 
 
 
 def cancellation_ulp_ok(ours: np.ndarray, ref: np.ndarray, decayed: np.ndarray, k: float = 2.0) -> np.ndarray:
-    """|ours - ref| <= k * spacing(max(|ours|, |decayed|)).
+    """|ours - ref| <= k * spacing(max(|ours|, |decayed|, |ours - decayed|)).
 
-    The master update is p_new = p_decayed + u. Where p_new nearly cancels
-    (|p_new| << |p_decayed|), one ulp of u is many ulps of p_new, so the
-    tolerance is taken in ulps of the larger operand of that final add."""
-    scale = np.maximum(np.abs(ours), np.abs(decayed)).astype(np.float32)
+    The master update is p_new = p_decayed + u. Where the add cancels
+    (|p_new| << |u|), one ulp of u is many ulps of p_new, so the tolerance is
+    taken in ulps of the largest operand or result of that final add."""
+    upd = np.abs(ours.astype(np.float64) - decayed.astype(np.float64))
+    scale = np.maximum(np.maximum(np.abs(ours), np.abs(decayed)), upd).astype(np.float32)
     tol = k * np.spacing(scale)
     diff = np.abs(ours.astype(np.float64) - ref.astype(np.float64))
     return (diff <= tol) | (np.isnan(ours) & np.isnan(ref))

@@ -1,0 +1,118 @@
+"""The C ABI without a GPU: libdsx.so loads, exports every function
+include/dsx.h declares with the layout the Python binding assumes, and its
+host-only entry points and argument checks work (no kernel is launched)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dsx.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsx_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from distributedspeed_amd import _lib
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    from distributedspeed_amd import _lib
+    names = _declared()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in dsx.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_struct_layouts_match_header(lib):
+    from distributedspeed_amd import _lib
+    text = open(HEADER).read()
+    for struct in ("DsxState", "DsxScalerConfig", "DsxAdamwHyper", "DsxStepScalars", "DsxTensorRef", "DsxChunk"):
+        body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
+        body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+        fields = re.findall(r"([A-Za-z_][A-Za-z0-9_\s\*]*?)\s+\*?([a-z0-9_]+)(\[\d+\])?\s*;", body)
+        cls = getattr(_lib, struct)
+        assert [f[1] for f in fields] == [f[0] for f in cls._fields_], struct
+
+
+def test_abi_version_and_error_string(lib):
+    assert lib.dsx_abi_version() == 1
+    assert isinstance(lib.dsx_last_error(), bytes)
+
+
+def test_chunk_table_host_side(lib):
+    from distributedspeed_amd import _lib
+    sizes = [0, 1, 8, 9, 65536, 65537, 200000]
+    arr = (ctypes.c_int64 * len(sizes))(*sizes)
+    cnt = lib.dsx_count_chunks(arr, len(sizes), 65536)
+    assert cnt == sum(-(-s // 65536) for s in sizes)
+    out = (_lib.DsxChunk * cnt)()
+    assert lib.dsx_build_chunks(arr, len(sizes), 65536, out, cnt) == cnt
+    covered = {}
+    for c in out:
+        assert 0 < c.len <= 65536 and c.start % 65536 == 0
+        covered[c.tensor] = covered.get(c.tensor, 0) + c.len
+    assert covered == {i: s for i, s in enumerate(sizes) if s}
+    # bad arguments: chunk size not a multiple of 8, too small a buffer
+    assert lib.dsx_count_chunks(arr, len(sizes), 100) == -1
+    assert lib.dsx_build_chunks(arr, len(sizes), 65536, out, cnt - 1) == -1
+    assert b"capacity" in lib.dsx_last_error()
+
+
+def test_argument_checks_reject_before_launch(lib):
+    """Rejected arguments return DSX_EINVAL with a message and never reach a
+    HIP call (this runs without a GPU)."""
+    from distributedspeed_amd import _lib
+    EINVAL = _lib.DSX_EINVAL
+    al = 1 << 20  # a 16-byte aligned fake address; never dereferenced on these paths
+    sc = _lib.DsxStepScalars()
+    # bad grad dtype
+    assert lib.dsx_adamw_flat(al, al, al, None, 2, al, 7, 16, ctypes.byref(sc), None) == EINVAL
+    assert b"grad dtype" in lib.dsx_last_error()
+    # misaligned master
+    assert lib.dsx_adamw_flat(al + 4, al, al, None, 2, al, 2, 16, ctypes.byref(sc), None) == EINVAL
+    assert b"aligned" in lib.dsx_last_error()
+    # negative n
+    assert lib.dsx_adamw_flat(al, al, al, None, 2, al, 2, -1, ctypes.byref(sc), None) == EINVAL
+    # bad hyper-parameters use torch.optim.Adam's wording
+    hp = _lib.DsxAdamwHyper(-1.0, 0.9, 0.999, 1e-8, 0.0, 0.0, 1e-6)
+    scfg = _lib.DsxScalerConfig(0, 1000, 1, 0, 1.0, 2.0, 0.5, 0.0)
+    assert lib.dsx_finalize(al, 1, al, scfg, hp, al, 1, al, None) == EINVAL
+    assert b"Invalid learning rate" in lib.dsx_last_error()
+    hp = _lib.DsxAdamwHyper(1e-3, 1.0, 0.999, 1e-8, 0.0, 0.0, 1e-6)
+    assert lib.dsx_finalize(al, 1, al, scfg, hp, al, 1, al, None) == EINVAL
+    assert b"beta parameter at index 0" in lib.dsx_last_error()
+    # bad scaler configuration
+    hp = _lib.DsxAdamwHyper(1e-3, 0.9, 0.999, 1e-8, 0.0, 0.0, 1e-6)
+    bad = _lib.DsxScalerConfig(2, 0, 1, 0, 1.0, 2.0, 0.5, 0.0)
+    assert lib.dsx_finalize(al, 1, al, bad, hp, al, 1, al, None) == EINVAL
+    assert b"loss_scale_window" in lib.dsx_last_error()
+    # partial count out of range
+    assert lib.dsx_unscale_norm(al, 2, 16, al, al, 0, None) == EINVAL
+    assert lib.dsx_unscale_norm(al, 2, 16, al, al, _lib.DSX_MAX_PARTIALS + 1, None) == EINVAL
+    # tuning validation
+    assert lib.dsx_set_tuning(8, 8, 3, 1) == EINVAL
+    assert lib.dsx_set_tuning(0, 8, 4, 1) == EINVAL
+
+
+def test_python_layer_mirrors_torch_errors():
+    from distributedspeed_amd.flat_step import AdamWHyper, ScalerConfig
+    with pytest.raises(ValueError, match="Invalid learning rate"):
+        AdamWHyper(lr=-1).validate()
+    with pytest.raises(ValueError, match="Invalid beta parameter at index 1"):
+        AdamWHyper(beta2=1.0).validate()
+    with pytest.raises(ValueError, match="Invalid epsilon"):
+        AdamWHyper(eps=-1e-8).validate()
+    with pytest.raises(ValueError, match="hysteresis"):
+        ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, hysteresis=0).validate()
