@@ -40,7 +40,39 @@ def _args():
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                       "k2_adamw_flat_llama8b_shard_traffic.json"))
     ap.add_argument("--tuning", default="", help="k1_bpc,k2_bpc,k2_unroll,nt (library launch-shape override)")
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="for rocprofv3 --pmc runs: launch K1, K0, K2 three times each and one 1 GiB fp32 "
+                         "copy (the byte-counter calibration), then exit without timing")
     return ap.parse_args()
+
+
+def profile_kernels(n: int, dev) -> int:
+    """Three dispatches of each kernel of the step plus a plain copy kernel of
+    known size (2^28 fp32 = 1 GiB read and 1 GiB written), so that
+    FETCH_SIZE / WRITE_SIZE per dispatch can be scaled by what the counters
+    report for the copy."""
+    import torch
+    from distributedspeed_amd import ops
+    from distributedspeed_amd.flat_step import AdamWHyper, FlatStep, ScalerConfig
+    hyper = AdamWHyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    master, exp_avg, exp_avg_sq, p16, grad = make_inputs(n, 2, dev)
+    fs = FlatStep(n, dev, hyper, ScalerConfig(mode="none"))
+    hc, sc = hyper.to_c(), fs.scaler.to_c()
+    for _ in range(3):
+        fs.steps_issued += 1
+        fs.bc.ensure(fs.steps_issued)
+        ops.unscale_norm(grad, fs.state, fs.partials, fs.nparts)
+        ops.finalize(fs.partials, fs.nparts, fs.state, sc, hc, fs.bc.table, fs.bc.length, fs.scalars)
+        ops.adamw_flat(master, exp_avg, exp_avg_sq, p16, grad, fs.scalars)
+    torch.cuda.synchronize()
+    del master, exp_avg, exp_avg_sq, p16, grad
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    _progress("profile-kernels done")
+    return 0
 
 
 def _progress(msg: str) -> None:
@@ -147,6 +179,8 @@ def main() -> int:
         k1, k2, u, nt = (int(x) for x in a.tuning.split(","))
         _lib.call("dsx_set_tuning", k1, k2, u, nt)
     n = int(a.numel)
+    if a.profile_kernels:
+        return profile_kernels(n, dev)
     hyper = AdamWHyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     _progress(f"generating {n} elements")
     master, exp_avg, exp_avg_sq, p16, grad = make_inputs(n, 2, dev)

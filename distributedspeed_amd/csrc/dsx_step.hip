@@ -65,9 +65,13 @@ bool is16(int dt) { return dt == DSX_F16 || dt == DSX_BF16; }
 
 // ---- launch shape ----------------------------------------------------------
 
+// Defaults from launch-shape sweeps on MI355X over a 1.0e9-element
+// partition: K2 (50:50 read/write) is fastest with one 256-thread block per
+// CU -- more concurrent streams cost DRAM efficiency -- and K1 (read-only)
+// with two. Nontemporal hints help both by a few percent.
 struct Tuning {
-  int k1_blocks_per_cu = 8;
-  int k2_blocks_per_cu = 8;
+  int k1_blocks_per_cu = 2;
+  int k2_blocks_per_cu = 1;
   int k2_unroll = 4;      // slots per thread per trip: 2, 4 or 8
   int nontemporal = 1;    // nontemporal hint on the streaming loads/stores
 };

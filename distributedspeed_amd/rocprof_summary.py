@@ -1,0 +1,147 @@
+"""Summarise rocprofv3 CSV output of the step's kernels.
+
+    python -m distributedspeed_amd.rocprof_summary \
+        --trace DIR (from --kernel-trace --stats) \
+        --fetch DIR (from --pmc FETCH_SIZE) --write DIR (from --pmc WRITE_SIZE) \
+        --numel N --out-md FILE --out-json FILE --command "..."
+
+Byte counters are scaled by what they report for a plain copy kernel of
+known size in the same run (the 1 GiB fp32 copy `bench.py --profile-kernels`
+issues; it appears as __amd_rocclr_copyBuffer), so FETCH_SIZE/WRITE_SIZE
+become HBM bytes per dispatch whatever unit or channel coverage the counter
+has on this device.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import glob
+import json
+import os
+
+KERNELS = {"k2_adamw_flat": 28, "k1_unscale_norm": 2, "k0_finalize": 0, "k2_adamw_multi": 28,
+           "k1_unscale_norm_multi": 2}
+COPY_NAME = "__amd_rocclr_copyBuffer"
+COPY_BYTES = 1 << 30
+
+
+def _short(name: str) -> str | None:
+    for k in sorted(KERNELS, key=len, reverse=True):
+        if k in name:
+            return k
+    if COPY_NAME in name:
+        return "copy"
+    return None
+
+
+def _csv(dirname: str, suffix: str) -> str:
+    hits = glob.glob(os.path.join(dirname, "**", f"*{suffix}"), recursive=True)
+    if not hits:
+        raise FileNotFoundError(f"no *{suffix} under {dirname}")
+    return hits[0]
+
+
+def kernel_stats(trace_dir: str) -> dict:
+    out = {}
+    for r in csv.DictReader(open(_csv(trace_dir, "kernel_stats.csv"))):
+        k = _short(r["Name"])
+        if k and k != "copy":
+            out[k] = {"calls": int(r["Calls"]), "avg_ns": float(r["AverageNs"]), "min_ns": float(r["MinNs"]),
+                      "max_ns": float(r["MaxNs"]), "pct": float(r["Percentage"]), "name": r["Name"]}
+    return out
+
+
+def counter_per_dispatch(pmc_dir: str) -> dict:
+    """{kernel: [KiB per dispatch, ...]} summed over the counter's instances."""
+    per = collections.defaultdict(float)
+    names = {}
+    for r in csv.DictReader(open(_csv(pmc_dir, "counter_collection.csv"))):
+        k = _short(r["Kernel_Name"])
+        if k is None:
+            continue
+        if k == "copy" and int(r["Grid_Size"]) < 4096:
+            continue  # small copies (parameter uploads), not the calibration copy
+        per[(k, int(r["Dispatch_Id"]))] += float(r["Counter_Value"])
+        names[k] = r["Counter_Name"]
+    out = collections.defaultdict(list)
+    for (k, _), v in sorted(per.items(), key=lambda x: x[0][1]):
+        out[k].append(v)
+    return dict(out)
+
+
+def summarise(trace_dir, fetch_dir, write_dir, numel) -> dict:
+    stats = kernel_stats(trace_dir)
+    fetch = counter_per_dispatch(fetch_dir)
+    write = counter_per_dispatch(write_dir)
+    f_copy = sum(fetch["copy"]) / len(fetch["copy"])
+    w_copy = sum(write["copy"]) / len(write["copy"])
+    f_scale = COPY_BYTES / (f_copy * 1024)
+    w_scale = COPY_BYTES / (w_copy * 1024)
+    res = {"numel": int(numel), "fetch_scale": f_scale, "write_scale": w_scale,
+           "copy_fetch_kib": f_copy, "copy_write_kib": w_copy, "kernels": {}}
+    for k, per_elt in KERNELS.items():
+        if k not in fetch and k not in stats:
+            continue
+        d = {}
+        if k in stats:
+            d.update(avg_ms=stats[k]["avg_ns"] / 1e6, calls=stats[k]["calls"], pct=stats[k]["pct"])
+        if k in fetch and k in write:
+            fb = sum(fetch[k]) / len(fetch[k]) * 1024 * f_scale
+            wb = sum(write[k]) / len(write[k]) * 1024 * w_scale
+            d.update(fetch_bytes=fb, write_bytes=wb, hbm_bytes=fb + wb)
+            if per_elt:
+                d["algorithmic_bytes"] = per_elt * numel
+                d["traffic_over_algorithmic"] = (fb + wb) / (per_elt * numel)
+        if "avg_ms" in d and per_elt:
+            d["achieved_gbs"] = per_elt * numel / (d["avg_ms"] * 1e-3) / 1e9
+            d["frac_of_8tbs"] = d["achieved_gbs"] / 8000.0
+        res["kernels"][k] = d
+    k2 = res["kernels"].get("k2_adamw_flat", {})
+    res["k2_hbm_bytes_per_launch"] = k2.get("hbm_bytes")
+    res["k1_hbm_bytes_per_launch"] = res["kernels"].get("k1_unscale_norm", {}).get("hbm_bytes")
+    return res
+
+
+def markdown(res: dict, command: str, title: str) -> str:
+    lines = [f"# {title}", "", "Commands (run on one MI355X, from the repository root as $R):", "",
+             "```", command.strip(), "```", "",
+             f"Byte-counter calibration: a {COPY_BYTES >> 20} MiB fp32 copy reads FETCH_SIZE "
+             f"{res['copy_fetch_kib']:.1f} KiB and WRITE_SIZE {res['copy_write_kib']:.1f} KiB per dispatch, "
+             f"so FETCH_SIZE is scaled by {res['fetch_scale']:.4f} and WRITE_SIZE by {res['write_scale']:.4f}.", "",
+             f"n = {res['numel']:,} elements.", "",
+             "| kernel | calls | avg ms | algorithmic GB | achieved GB/s | % of 8 TB/s | HBM read GB | HBM write GB | traffic / algorithmic |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for k, d in res["kernels"].items():
+        alg = d.get("algorithmic_bytes")
+        lines.append("| {} | {} | {} | {} | {} | {} | {} | {} | {} |".format(
+            k, d.get("calls", ""), f"{d['avg_ms']:.4f}" if "avg_ms" in d else "",
+            f"{alg / 1e9:.3f}" if alg else "", f"{d['achieved_gbs']:.0f}" if "achieved_gbs" in d else "",
+            f"{100 * d['frac_of_8tbs']:.1f}" if "frac_of_8tbs" in d else "",
+            f"{d['fetch_bytes'] / 1e9:.3f}" if "fetch_bytes" in d else "",
+            f"{d['write_bytes'] / 1e9:.3f}" if "write_bytes" in d else "",
+            f"{d['traffic_over_algorithmic']:.4f}" if "traffic_over_algorithmic" in d else ""))
+    return "\n".join(lines) + "\n"
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--trace", required=True)
+    ap.add_argument("--fetch", required=True)
+    ap.add_argument("--write", required=True)
+    ap.add_argument("--numel", type=int, required=True)
+    ap.add_argument("--out-md", required=True)
+    ap.add_argument("--out-json", required=True)
+    ap.add_argument("--command", default="")
+    ap.add_argument("--title", default="rocprofv3 summary")
+    a = ap.parse_args()
+    res = summarise(a.trace, a.fetch, a.write, a.numel)
+    with open(a.out_json, "w") as f:
+        json.dump(res, f, indent=1)
+    with open(a.out_md, "w") as f:
+        f.write(markdown(res, a.command, a.title))
+    print(json.dumps({k: res[k] for k in ("k2_hbm_bytes_per_launch", "k1_hbm_bytes_per_launch", "fetch_scale")}))
+
+
+if __name__ == "__main__":
+    main()
