@@ -20,6 +20,7 @@ DSX_SCALE_NONE, DSX_SCALE_STATIC, DSX_SCALE_DYNAMIC = 0, 1, 2
 DSX_EINVAL = 1
 DSX_STATE_ERR_BC_TABLE = 1
 DSX_MAX_PARTIALS = 8192
+DSX_MAX_GROUPS = 16
 ABI_VERSION = 1
 
 _c = ctypes
@@ -53,7 +54,7 @@ class DsxStepScalars(_c.Structure):
 
 class DsxTensorRef(_c.Structure):
     _fields_ = [("master", _P), ("exp_avg", _P), ("exp_avg_sq", _P), ("param16", _P), ("grad", _P),
-                ("numel", _c.c_int64)]
+                ("numel", _c.c_int64), ("group", _c.c_int32), ("reserved", _c.c_int32)]
 
 
 class DsxChunk(_c.Structure):
@@ -61,7 +62,7 @@ class DsxChunk(_c.Structure):
 
 
 for _s, _n in ((DsxState, 64), (DsxScalerConfig, 32), (DsxAdamwHyper, 56), (DsxStepScalars, 64),
-               (DsxTensorRef, 48), (DsxChunk, 24)):
+               (DsxTensorRef, 56), (DsxChunk, 24)):
     assert _c.sizeof(_s) == _n, (_s.__name__, _c.sizeof(_s))
 
 # name -> (restype, argtypes); every symbol include/dsx.h declares.
@@ -75,6 +76,8 @@ SIGNATURES = {
     "dsx_state_init": (_c.c_int, [_P, _c.c_float, _c.c_int32, _P]),
     "dsx_unscale_norm": (_c.c_int, [_P, _c.c_int, _c.c_int64, _P, _P, _c.c_int32, _P]),
     "dsx_finalize": (_c.c_int, [_P, _c.c_int32, _P, DsxScalerConfig, DsxAdamwHyper, _P, _c.c_int32, _P, _P]),
+    "dsx_finalize_groups": (_c.c_int, [_P, _c.c_int32, _P, DsxScalerConfig, _P, _P, _P, _c.c_int32, _c.c_int32,
+                                       _P, _P]),
     "dsx_adamw_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, _P]),
     "dsx_zero_step_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, DsxScalerConfig,
                                       DsxAdamwHyper, _P, _c.c_int32, _P, _c.c_int32, _P, _P]),

@@ -7,12 +7,12 @@
 // that the reference calls at Src/zero/stage1.py:522-525 and
 // Src/zero/stage2.py:609-612.
 //
-// Everything is HBM-bound streaming. K2 moves 28 B per element (grad 2 +
-// master/m/v 12 read, master/m/v 12 + param16 2 written) and K1 2 B per
-// element. The kernels are grid-stride loops over 4-element slots (fp32 in
-// 16-byte loads, 16-bit values in 8-byte loads) so that every load and store
-// instruction of a wave touches one contiguous span; several slots per thread
-// are loaded before any is used, to keep enough bytes in flight per CU.
+// Everything is HBM-bound streaming. K2 moves 28 B per element with 16-bit
+// grads (grad 2 + master/m/v 12 read, master/m/v 12 + param16 2 written) and
+// K1 2 B per element. The kernels are grid-stride loops over 4-element slots
+// (fp32 in 16-byte loads, 16-bit values in 8-byte loads) so that every load
+// and store instruction of a wave touches one contiguous span; several slots
+// per thread are loaded before any is used, to keep bytes in flight.
 //
 // Compile with -ffp-contract=off: the element math must round exactly where
 // torch rounds, and the only fused multiply-adds are the explicit fmaf calls
@@ -31,7 +31,7 @@ static_assert(sizeof(DsxState) == 64, "DsxState layout");
 static_assert(sizeof(DsxScalerConfig) == 32, "DsxScalerConfig layout");
 static_assert(sizeof(DsxAdamwHyper) == 56, "DsxAdamwHyper layout");
 static_assert(sizeof(DsxStepScalars) == 64, "DsxStepScalars layout");
-static_assert(sizeof(DsxTensorRef) == 48, "DsxTensorRef layout");
+static_assert(sizeof(DsxTensorRef) == 56, "DsxTensorRef layout");
 static_assert(sizeof(DsxChunk) == 24, "DsxChunk layout");
 
 namespace {
@@ -60,8 +60,9 @@ int launch_status(const char* what) {
   return DSX_OK;
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+__host__ __device__ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool is16(int dt) { return dt == DSX_F16 || dt == DSX_BF16; }
+bool is_grad_dtype(int dt) { return dt == DSX_F16 || dt == DSX_BF16 || dt == DSX_F32; }
 
 // ---- launch shape ----------------------------------------------------------
 
@@ -128,6 +129,48 @@ __device__ __forceinline__ uint32_t f2h(float x) {
   }
 }
 
+// Grad formats: element storage, the 4-element slot K2 loads, and how a
+// 16-byte K1 slot unpacks.
+template <int GD>
+struct Grad {  // DSX_F16 / DSX_BF16
+  using elem = uint16_t;
+  using slot4 = u2;
+  static constexpr int per16 = 8;
+  __device__ static float one(elem e) { return h2f<GD>(e); }
+  __device__ static void four(const slot4& s, float (&g)[4]) {
+    g[0] = h2f<GD>(s.x); g[1] = h2f<GD>(s.x >> 16); g[2] = h2f<GD>(s.y); g[3] = h2f<GD>(s.y >> 16);
+  }
+  __device__ static double sumsq16(const u4& s, float inv, double acc) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float a = h2f<GD>(s[k]) * inv;
+      const float b = h2f<GD>(s[k] >> 16) * inv;
+      acc = __builtin_fma((double)a, (double)a, acc);
+      acc = __builtin_fma((double)b, (double)b, acc);
+    }
+    return acc;
+  }
+};
+
+template <>
+struct Grad<DSX_F32> {
+  using elem = float;
+  using slot4 = f4;
+  static constexpr int per16 = 4;
+  __device__ static float one(elem e) { return e; }
+  __device__ static void four(const slot4& s, float (&g)[4]) {
+    g[0] = s[0]; g[1] = s[1]; g[2] = s[2]; g[3] = s[3];
+  }
+  __device__ static double sumsq16(const u4& s, float inv, double acc) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float a = __uint_as_float(s[k]) * inv;
+      acc = __builtin_fma((double)a, (double)a, acc);
+    }
+    return acc;
+  }
+};
+
 // Step scalars held in registers.
 struct Sc {
   float inv, coef, decay, w1, w1m1, b2, val2, eps, bc2s, nss;
@@ -171,6 +214,14 @@ __device__ __forceinline__ void adamw4(const float (&g)[4], f4& p, f4& m, f4& v,
   }
 }
 
+template <int PD>
+__device__ __forceinline__ u2 pack4(const f4& p) {
+  u2 o;
+  o.x = f2h<PD>(p[0]) | (f2h<PD>(p[1]) << 16);
+  o.y = f2h<PD>(p[2]) | (f2h<PD>(p[3]) << 16);
+  return o;
+}
+
 // ---- block reduction of a double -------------------------------------------
 
 __device__ __forceinline__ double wave_sum(double x) {
@@ -206,36 +257,30 @@ __device__ __forceinline__ float inv_of(float scale) {
 // so the sum is non-finite exactly when some unscaled grad is inf or NaN.
 
 template <int GD, int U, bool NT>
-__global__ __launch_bounds__(kBlock) void k1_unscale_norm(const uint16_t* __restrict__ g, int64_t n,
+__global__ __launch_bounds__(kBlock) void k1_unscale_norm(const void* __restrict__ gv, int64_t n,
                                                           const DsxState* __restrict__ state,
                                                           double* __restrict__ partials) {
+  using G = Grad<GD>;
   const float inv = inv_of(state->scale);
-  const u4* g8 = reinterpret_cast<const u4*>(g);
-  const int64_t nvec = n >> 3;  // 8 elements per 16-byte slot
+  const u4* g16 = static_cast<const u4*>(gv);
+  const typename G::elem* g = static_cast<const typename G::elem*>(gv);
+  const int64_t nvec = n / G::per16;
   const int64_t stride = (int64_t)gridDim.x * kBlock * U;
   double acc = 0.0;
   for (int64_t i0 = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; i0 < nvec; i0 += stride) {
-    u4 G[U];
+    u4 S[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t i = i0 + (int64_t)u * kBlock;
-      G[u] = (i < nvec) ? ld<NT>(g8 + i) : u4{0u, 0u, 0u, 0u};
+      S[u] = (i < nvec) ? ld<NT>(g16 + i) : u4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float a = h2f<GD>(G[u][k]) * inv;
-        const float b = h2f<GD>(G[u][k] >> 16) * inv;
-        acc = __builtin_fma((double)a, (double)a, acc);
-        acc = __builtin_fma((double)b, (double)b, acc);
-      }
-    }
+    for (int u = 0; u < U; ++u) acc = G::sumsq16(S[u], inv, acc);
   }
-  const int64_t tail0 = nvec << 3;
+  const int64_t tail0 = nvec * G::per16;
   const int64_t gt = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (gt < n - tail0) {
-    const float a = h2f<GD>(g[tail0 + gt]) * inv;
+    const float a = G::one(g[tail0 + gt]) * inv;
     acc = __builtin_fma((double)a, (double)a, acc);
   }
   const double s = block_sum(acc);
@@ -244,28 +289,72 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm(const uint16_t* __rest
 
 // ---- K0: finalize ------------------------------------------------------------
 
+struct Groups {
+  DsxAdamwHyper hyper[DSX_MAX_GROUPS];
+  const double* bc[DSX_MAX_GROUPS];
+  int32_t t_offset[DSX_MAX_GROUPS];
+  int32_t n;
+};
+
+// Global part of a step (norm, skip, clip, t, scaler) once; per-group fp32
+// scalars for each parameter group.
 __global__ __launch_bounds__(kBlock) void k0_finalize(const double* __restrict__ partials, int32_t nparts,
                                                       DsxState* __restrict__ state, DsxScalerConfig scfg,
-                                                      DsxAdamwHyper hp, const double* __restrict__ bc,
-                                                      int32_t bc_len, DsxStepScalars* __restrict__ out) {
+                                                      Groups grp, int32_t bc_len,
+                                                      DsxStepScalars* __restrict__ out) {
   double x = 0.0;
   for (int i = threadIdx.x; i < nparts; i += kBlock) x += partials[i];
   const double sumsq = block_sum(x);
   if (threadIdx.x != 0) return;
 
   DsxState s = *state;
-  DsxStepScalars o = {};
-  o.sumsq = sumsq;
-  o.norm = sqrt(sumsq);
-  o.inv_scale = inv_of(s.scale);
-  o.clip_coef = 1.0f;
-  o.decay = 1.0f;
-  o.t = s.t;
+  const double norm = sqrt(sumsq);
+  const float inv = inv_of(s.scale);
   const bool found_inf = !__builtin_isfinite(sumsq);
   const bool dynamic = scfg.mode == DSX_SCALE_DYNAMIC;
+  const int32_t t = s.t + 1;
+  bool skip = found_inf;
+  if (!found_inf) {
+    for (int k = 0; k < grp.n; ++k) {
+      const int32_t tk = t - grp.t_offset[k];
+      if (tk < 1 || tk > bc_len) {
+        skip = true;
+        s.error |= DSX_STATE_ERR_BC_TABLE;
+      }
+    }
+  }
+  float coef = 1.0f;
+  const DsxAdamwHyper& h0 = grp.hyper[0];
+  if (!skip && h0.max_grad_norm > 0.0 && norm > h0.max_grad_norm)
+    coef = (float)(h0.max_grad_norm / (norm + h0.clip_eps));
+
+  for (int k = 0; k < grp.n; ++k) {
+    const DsxAdamwHyper& hp = grp.hyper[k];
+    DsxStepScalars o = {};
+    o.sumsq = sumsq;
+    o.norm = norm;
+    o.inv_scale = inv;
+    o.clip_coef = coef;
+    o.decay = 1.0f;
+    o.skip = skip ? 1 : 0;
+    o.t = (skip ? s.t : t) - grp.t_offset[k];
+    if (!skip) {
+      const int32_t tk = t - grp.t_offset[k];
+      const double bc1 = grp.bc[k][2 * (int64_t)(tk - 1)];
+      const double bc2s = grp.bc[k][2 * (int64_t)(tk - 1) + 1];
+      if (hp.weight_decay != 0.0) o.decay = (float)(1.0 - hp.lr * hp.weight_decay);
+      o.w1 = (float)(1.0 - hp.beta1);
+      o.w1m1 = o.w1 - 1.0f;
+      o.b2 = (float)hp.beta2;
+      o.val2 = (float)(1.0 - hp.beta2);
+      o.eps = (float)hp.eps;
+      o.bc2s = (float)bc2s;
+      o.nss = (float)(-(hp.lr / bc1));
+    }
+    out[k] = o;
+  }
 
   if (found_inf) {
-    o.skip = 1;
     s.overflow_count += 1;
     if (dynamic) {
       if (scfg.hysteresis <= 1 || s.hyst_left <= 1) {
@@ -276,42 +365,22 @@ __global__ __launch_bounds__(kBlock) void k0_finalize(const double* __restrict__
       }
       s.good_steps = 0;
     }
-  } else {
-    const int32_t t = s.t + 1;
-    if (t > bc_len) {
-      o.skip = 1;
-      s.error |= DSX_STATE_ERR_BC_TABLE;
-    } else {
-      const double bc1 = bc[2 * (int64_t)(t - 1)];
-      const double bc2s = bc[2 * (int64_t)(t - 1) + 1];
-      if (hp.max_grad_norm > 0.0 && o.norm > hp.max_grad_norm)
-        o.clip_coef = (float)(hp.max_grad_norm / (o.norm + hp.clip_eps));
-      if (hp.weight_decay != 0.0) o.decay = (float)(1.0 - hp.lr * hp.weight_decay);
-      o.w1 = (float)(1.0 - hp.beta1);
-      o.w1m1 = o.w1 - 1.0f;
-      o.b2 = (float)hp.beta2;
-      o.val2 = (float)(1.0 - hp.beta2);
-      o.eps = (float)hp.eps;
-      o.bc2s = (float)bc2s;
-      o.nss = (float)(-(hp.lr / bc1));
-      o.t = t;
-      s.t = t;
-      if (dynamic) {
-        s.good_steps += 1;
-        if (s.good_steps >= scfg.window) {
-          const float next = s.scale * scfg.growth_factor;
-          if (__builtin_isfinite(next)) s.scale = next;
-          s.good_steps = 0;
-          s.hyst_left = scfg.hysteresis;
-        }
+  } else if (!skip) {
+    s.t = t;
+    if (dynamic) {
+      s.good_steps += 1;
+      if (s.good_steps >= scfg.window) {
+        const float next = s.scale * scfg.growth_factor;
+        if (__builtin_isfinite(next)) s.scale = next;
+        s.good_steps = 0;
+        s.hyst_left = scfg.hysteresis;
       }
     }
   }
   s.iter += 1;
-  s.last_skip = o.skip;
-  s.last_norm = o.norm;
+  s.last_skip = skip ? 1 : 0;
+  s.last_norm = norm;
   *state = s;
-  *out = o;
 }
 
 __global__ void k_state_init(DsxState* state, float scale, int32_t hysteresis) {
@@ -328,26 +397,29 @@ __global__ void k_state_init(DsxState* state, float scale, int32_t hysteresis) {
 template <int GD, int PD, int U, bool NT>
 __global__ __launch_bounds__(kBlock) void k2_adamw_flat(float* __restrict__ p, float* __restrict__ m,
                                                         float* __restrict__ v, uint16_t* __restrict__ p16,
-                                                        const uint16_t* __restrict__ g, int64_t n,
+                                                        const void* __restrict__ gv, int64_t n,
                                                         const DsxStepScalars* __restrict__ scp) {
+  using G = Grad<GD>;
+  using GS = typename G::slot4;
   if (scp->skip) return;
   const Sc s = load_sc(*scp);
   f4* p4 = reinterpret_cast<f4*>(p);
   f4* m4 = reinterpret_cast<f4*>(m);
   f4* v4 = reinterpret_cast<f4*>(v);
   u2* o2 = reinterpret_cast<u2*>(p16);
-  const u2* g2 = reinterpret_cast<const u2*>(g);
+  const GS* g4 = static_cast<const GS*>(gv);
+  const typename G::elem* g = static_cast<const typename G::elem*>(gv);
   const bool cast = p16 != nullptr;
   const int64_t nvec = n >> 2;  // 4 elements per slot
   const int64_t stride = (int64_t)gridDim.x * kBlock * U;
   for (int64_t i0 = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; i0 < nvec; i0 += stride) {
-    u2 G[U];
+    GS Gs[U];
     f4 P[U], M[U], V[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t i = i0 + (int64_t)u * kBlock;
       if (i < nvec) {
-        G[u] = ld<NT>(g2 + i);
+        Gs[u] = ld<NT>(g4 + i);
         P[u] = ld<NT>(p4 + i);
         M[u] = ld<NT>(m4 + i);
         V[u] = ld<NT>(v4 + i);
@@ -357,18 +429,14 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_flat(float* __restrict__ p, f
     for (int u = 0; u < U; ++u) {
       const int64_t i = i0 + (int64_t)u * kBlock;
       if (i < nvec) {
-        float gf[4] = {h2f<GD>(G[u].x), h2f<GD>(G[u].x >> 16), h2f<GD>(G[u].y), h2f<GD>(G[u].y >> 16)};
+        float gf[4];
+        G::four(Gs[u], gf);
         f4 pp = P[u], mm = M[u], vv = V[u];
         adamw4(gf, pp, mm, vv, s);
         st<NT>(p4 + i, pp);
         st<NT>(m4 + i, mm);
         st<NT>(v4 + i, vv);
-        if (cast) {
-          u2 o;
-          o.x = f2h<PD>(pp[0]) | (f2h<PD>(pp[1]) << 16);
-          o.y = f2h<PD>(pp[2]) | (f2h<PD>(pp[3]) << 16);
-          st<NT>(o2 + i, o);
-        }
+        if (cast) st<NT>(o2 + i, pack4<PD>(pp));
       }
     }
   }
@@ -377,7 +445,7 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_flat(float* __restrict__ p, f
   if (gt < n - tail0) {
     const int64_t e = tail0 + gt;
     float pe = p[e], me = m[e], ve = v[e];
-    adamw_elt(h2f<GD>(g[e]), pe, me, ve, s);
+    adamw_elt(G::one(g[e]), pe, me, ve, s);
     p[e] = pe; m[e] = me; v[e] = ve;
     if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
   }
@@ -385,44 +453,28 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_flat(float* __restrict__ p, f
 
 // ---- K3: ragged lists ----------------------------------------------------------
 
-__device__ __forceinline__ bool chunk_aligned(const void* a, const void* b, const void* c,
-                                              const void* d, const void* e) {
-  const uintptr_t o = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
-                      reinterpret_cast<uintptr_t>(c) | (reinterpret_cast<uintptr_t>(d) << 1) |
-                      (reinterpret_cast<uintptr_t>(e) << 1);  // 16-bit arrays need 8-byte alignment
-  return (o & 15u) == 0;
-}
-
 template <int GD>
 __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorRef* __restrict__ tensors,
                                                                 const DsxChunk* __restrict__ chunks,
                                                                 int64_t nchunks,
                                                                 const DsxState* __restrict__ state,
                                                                 double* __restrict__ partials) {
+  using G = Grad<GD>;
   const float inv = inv_of(state->scale);
   double acc = 0.0;
   for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
     const DsxChunk ch = chunks[c];
-    const uint16_t* g = static_cast<const uint16_t*>(tensors[ch.tensor].grad) + ch.start;
+    const typename G::elem* g = static_cast<const typename G::elem*>(tensors[ch.tensor].grad) + ch.start;
     const int64_t len = ch.len;
     int64_t done = 0;
-    if ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) {
-      const u4* g8 = reinterpret_cast<const u4*>(g);
-      const int64_t nvec = len >> 3;
-      for (int64_t i = threadIdx.x; i < nvec; i += kBlock) {
-        const u4 G = g8[i];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float a = h2f<GD>(G[k]) * inv;
-          const float b = h2f<GD>(G[k] >> 16) * inv;
-          acc = __builtin_fma((double)a, (double)a, acc);
-          acc = __builtin_fma((double)b, (double)b, acc);
-        }
-      }
-      done = nvec << 3;
+    if (aligned16(g)) {
+      const u4* g16 = reinterpret_cast<const u4*>(g);
+      const int64_t nvec = len / G::per16;
+      for (int64_t i = threadIdx.x; i < nvec; i += kBlock) acc = G::sumsq16(g16[i], inv, acc);
+      done = nvec * G::per16;
     }
     for (int64_t e = done + threadIdx.x; e < len; e += kBlock) {
-      const float a = h2f<GD>(g[e]) * inv;
+      const float a = G::one(g[e]) * inv;
       acc = __builtin_fma((double)a, (double)a, acc);
     }
   }
@@ -433,45 +485,47 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorR
 template <int GD, int PD>
 __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __restrict__ tensors,
                                                          const DsxChunk* __restrict__ chunks, int64_t nchunks,
-                                                         const DsxStepScalars* __restrict__ scp) {
-  if (scp->skip) return;
-  const Sc s = load_sc(*scp);
+                                                         const DsxStepScalars* __restrict__ scalars) {
+  using G = Grad<GD>;
+  using GS = typename G::slot4;
+  if (scalars[0].skip) return;  // the skip decision is global
   for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
     const DsxChunk ch = chunks[c];
     const DsxTensorRef tr = tensors[ch.tensor];
+    const Sc s = load_sc(scalars[tr.group]);
     float* p = tr.master + ch.start;
     float* m = tr.exp_avg + ch.start;
     float* v = tr.exp_avg_sq + ch.start;
     uint16_t* p16 = tr.param16 ? static_cast<uint16_t*>(tr.param16) + ch.start : nullptr;
-    const uint16_t* g = static_cast<const uint16_t*>(tr.grad) + ch.start;
+    const typename G::elem* g = static_cast<const typename G::elem*>(tr.grad) + ch.start;
     const bool cast = p16 != nullptr;
     const int64_t len = ch.len;
+    // Vector path when every array is aligned for its 4-element slot.
+    const uintptr_t mis = (reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(m) |
+                           reinterpret_cast<uintptr_t>(v)) & 15u;
+    const uintptr_t gmis = reinterpret_cast<uintptr_t>(g) & (sizeof(GS) - 1);
+    const uintptr_t omis = cast ? (reinterpret_cast<uintptr_t>(p16) & 7u) : 0;
     int64_t done = 0;
-    if (chunk_aligned(p, m, v, cast ? (const void*)p16 : (const void*)g, g)) {
+    if (!mis && !gmis && !omis) {
       f4* p4 = reinterpret_cast<f4*>(p);
       f4* m4 = reinterpret_cast<f4*>(m);
       f4* v4 = reinterpret_cast<f4*>(v);
       u2* o2 = reinterpret_cast<u2*>(p16);
-      const u2* g2 = reinterpret_cast<const u2*>(g);
+      const GS* g4 = reinterpret_cast<const GS*>(g);
       const int64_t nvec = len >> 2;
       for (int64_t i = threadIdx.x; i < nvec; i += kBlock) {
-        const u2 G = g2[i];
+        float gf[4];
+        G::four(g4[i], gf);
         f4 pp = p4[i], mm = m4[i], vv = v4[i];
-        float gf[4] = {h2f<GD>(G.x), h2f<GD>(G.x >> 16), h2f<GD>(G.y), h2f<GD>(G.y >> 16)};
         adamw4(gf, pp, mm, vv, s);
         p4[i] = pp; m4[i] = mm; v4[i] = vv;
-        if (cast) {
-          u2 o;
-          o.x = f2h<PD>(pp[0]) | (f2h<PD>(pp[1]) << 16);
-          o.y = f2h<PD>(pp[2]) | (f2h<PD>(pp[3]) << 16);
-          o2[i] = o;
-        }
+        if (cast) o2[i] = pack4<PD>(pp);
       }
       done = nvec << 2;
     }
     for (int64_t e = done + threadIdx.x; e < len; e += kBlock) {
       float pe = p[e], me = m[e], ve = v[e];
-      adamw_elt(h2f<GD>(g[e]), pe, me, ve, s);
+      adamw_elt(G::one(g[e]), pe, me, ve, s);
       p[e] = pe; m[e] = me; v[e] = ve;
       if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
     }
@@ -482,16 +536,12 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __r
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-template <int GD, int U, bool NT>
-void launch_k1_u(const void* g, int64_t n, const DsxState* st, double* partials, int nparts, hipStream_t s) {
-  hipLaunchKernelGGL((k1_unscale_norm<GD, U, NT>), dim3(nparts), dim3(kBlock), 0, s,
-                     static_cast<const uint16_t*>(g), n, st, partials);
-}
-
 template <int GD>
 void launch_k1(const void* g, int64_t n, const DsxState* st, double* partials, int nparts, hipStream_t s) {
-  if (g_tune.nontemporal) launch_k1_u<GD, 4, true>(g, n, st, partials, nparts, s);
-  else launch_k1_u<GD, 4, false>(g, n, st, partials, nparts, s);
+  if (g_tune.nontemporal)
+    hipLaunchKernelGGL((k1_unscale_norm<GD, 4, true>), dim3(nparts), dim3(kBlock), 0, s, g, n, st, partials);
+  else
+    hipLaunchKernelGGL((k1_unscale_norm<GD, 4, false>), dim3(nparts), dim3(kBlock), 0, s, g, n, st, partials);
 }
 
 template <int GD, int PD, int U>
@@ -502,12 +552,13 @@ void launch_k2_u(float* p, float* m, float* v, void* p16, const void* g, int64_t
   const int64_t cap = (int64_t)cu_count() * g_tune.k2_blocks_per_cu;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
+  uint16_t* o = static_cast<uint16_t*>(p16);
   if (g_tune.nontemporal)
-    hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, true>), dim3((unsigned)blocks), dim3(kBlock), 0, s, p, m, v,
-                       static_cast<uint16_t*>(p16), static_cast<const uint16_t*>(g), n, sc);
+    hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, true>), dim3((unsigned)blocks), dim3(kBlock), 0, s, p, m, v, o, g,
+                       n, sc);
   else
-    hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, false>), dim3((unsigned)blocks), dim3(kBlock), 0, s, p, m, v,
-                       static_cast<uint16_t*>(p16), static_cast<const uint16_t*>(g), n, sc);
+    hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, false>), dim3((unsigned)blocks), dim3(kBlock), 0, s, p, m, v, o,
+                       g, n, sc);
 }
 
 template <int GD, int PD>
@@ -523,7 +574,7 @@ void launch_k2(float* p, float* m, float* v, void* p16, const void* g, int64_t n
 int check_flat(const float* master, const float* m, const float* v, const void* p16, int pdt, const void* g,
                int gdt, int64_t n) {
   if (n < 0) return fail(DSX_EINVAL, "n must be >= 0 (got %lld)", (long long)n);
-  if (!is16(gdt)) return fail(DSX_EINVAL, "grad dtype must be DSX_F16 or DSX_BF16 (got %d)", gdt);
+  if (!is_grad_dtype(gdt)) return fail(DSX_EINVAL, "grad dtype must be DSX_F16, DSX_BF16 or DSX_F32 (got %d)", gdt);
   if (p16 && !is16(pdt)) return fail(DSX_EINVAL, "param16 dtype must be DSX_F16 or DSX_BF16 (got %d)", pdt);
   if (n == 0) return DSX_OK;
   if (!master || !m || !v || !g) return fail(DSX_EINVAL, "null master/exp_avg/exp_avg_sq/grad pointer");
@@ -566,29 +617,55 @@ int check_parts(const double* partials, int32_t nparts) {
 
 int do_unscale_norm(const void* g, int gdt, int64_t n, const DsxState* st, double* partials, int32_t nparts,
                     hipStream_t s) {
-  if (gdt == DSX_BF16) launch_k1<DSX_BF16>(g, n, st, partials, nparts, s);
-  else launch_k1<DSX_F16>(g, n, st, partials, nparts, s);
+  switch (gdt) {
+    case DSX_BF16: launch_k1<DSX_BF16>(g, n, st, partials, nparts, s); break;
+    case DSX_F16: launch_k1<DSX_F16>(g, n, st, partials, nparts, s); break;
+    default: launch_k1<DSX_F32>(g, n, st, partials, nparts, s); break;
+  }
   return launch_status("dsx_unscale_norm");
 }
 
-int do_finalize(const double* partials, int32_t nparts, DsxState* st, const DsxScalerConfig& sc,
-                const DsxAdamwHyper& hp, const double* bc, int32_t bc_len, DsxStepScalars* out, hipStream_t s) {
-  hipLaunchKernelGGL(k0_finalize, dim3(1), dim3(kBlock), 0, s, partials, nparts, st, sc, hp, bc, bc_len, out);
+int do_finalize(const double* partials, int32_t nparts, DsxState* st, const DsxScalerConfig& sc, const Groups& grp,
+                int32_t bc_len, DsxStepScalars* out, hipStream_t s) {
+  hipLaunchKernelGGL(k0_finalize, dim3(1), dim3(kBlock), 0, s, partials, nparts, st, sc, grp, bc_len, out);
   return launch_status("dsx_finalize");
+}
+
+Groups one_group(const DsxAdamwHyper& hp, const double* bc) {
+  Groups g = {};
+  g.hyper[0] = hp;
+  g.bc[0] = bc;
+  g.t_offset[0] = 0;
+  g.n = 1;
+  return g;
+}
+
+template <int GD>
+void k2_by_param(int pd, float* p, float* m, float* v, void* p16, const void* g, int64_t n,
+                 const DsxStepScalars* sc, hipStream_t s) {
+  if (pd == DSX_BF16) launch_k2<GD, DSX_BF16>(p, m, v, p16, g, n, sc, s);
+  else launch_k2<GD, DSX_F16>(p, m, v, p16, g, n, sc, s);
 }
 
 int do_adamw_flat(float* p, float* m, float* v, void* p16, int pdt, const void* g, int gdt, int64_t n,
                   const DsxStepScalars* sc, hipStream_t s) {
   if (n == 0) return DSX_OK;
-  const int pd = p16 ? pdt : gdt;  // pd only selects the cast when p16 != NULL
-  if (gdt == DSX_BF16) {
-    if (pd == DSX_BF16) launch_k2<DSX_BF16, DSX_BF16>(p, m, v, p16, g, n, sc, s);
-    else launch_k2<DSX_BF16, DSX_F16>(p, m, v, p16, g, n, sc, s);
-  } else {
-    if (pd == DSX_BF16) launch_k2<DSX_F16, DSX_BF16>(p, m, v, p16, g, n, sc, s);
-    else launch_k2<DSX_F16, DSX_F16>(p, m, v, p16, g, n, sc, s);
+  const int pd = p16 ? pdt : DSX_F16;  // pd only selects the cast when p16 != NULL
+  switch (gdt) {
+    case DSX_BF16: k2_by_param<DSX_BF16>(pd, p, m, v, p16, g, n, sc, s); break;
+    case DSX_F16: k2_by_param<DSX_F16>(pd, p, m, v, p16, g, n, sc, s); break;
+    default: k2_by_param<DSX_F32>(pd, p, m, v, p16, g, n, sc, s); break;
   }
   return launch_status("dsx_adamw_flat");
+}
+
+template <int GD>
+void launch_k3(int pd, dim3 grid, const DsxTensorRef* t, const DsxChunk* c, int64_t nc, const DsxStepScalars* sc,
+               hipStream_t s) {
+  if (pd == DSX_BF16)
+    hipLaunchKernelGGL((k2_adamw_multi<GD, DSX_BF16>), grid, dim3(kBlock), 0, s, t, c, nc, sc);
+  else
+    hipLaunchKernelGGL((k2_adamw_multi<GD, DSX_F16>), grid, dim3(kBlock), 0, s, t, c, nc, sc);
 }
 
 }  // namespace
@@ -621,11 +698,16 @@ int32_t dsx_suggest_partials(int64_t n) {
 }
 
 int64_t dsx_count_chunks(const int64_t* numels, int32_t ntensors, int64_t chunk_elems) {
-  if (!numels || ntensors < 0 || chunk_elems < 8 || (chunk_elems & 7))
-    return fail(-1, "dsx_count_chunks: bad arguments"), -1;
+  if (!numels || ntensors < 0 || chunk_elems < 8 || (chunk_elems & 7)) {
+    fail(DSX_EINVAL, "dsx_count_chunks: bad arguments");
+    return -1;
+  }
   int64_t c = 0;
   for (int32_t i = 0; i < ntensors; ++i) {
-    if (numels[i] < 0) return fail(-1, "dsx_count_chunks: negative numel"), -1;
+    if (numels[i] < 0) {
+      fail(DSX_EINVAL, "dsx_count_chunks: negative numel");
+      return -1;
+    }
     c += ceil_div(numels[i], chunk_elems);
   }
   return c;
@@ -634,7 +716,10 @@ int64_t dsx_count_chunks(const int64_t* numels, int32_t ntensors, int64_t chunk_
 int64_t dsx_build_chunks(const int64_t* numels, int32_t ntensors, int64_t chunk_elems, DsxChunk* out, int64_t cap) {
   const int64_t need = dsx_count_chunks(numels, ntensors, chunk_elems);
   if (need < 0) return -1;
-  if (!out || cap < need) return fail(-1, "dsx_build_chunks: capacity %lld < %lld", (long long)cap, (long long)need), -1;
+  if (!out || cap < need) {
+    fail(DSX_EINVAL, "dsx_build_chunks: capacity %lld < %lld", (long long)cap, (long long)need);
+    return -1;
+  }
   int64_t c = 0;
   for (int32_t i = 0; i < ntensors; ++i) {
     for (int64_t s = 0; s < numels[i]; s += chunk_elems) {
@@ -659,7 +744,8 @@ int dsx_state_init(DsxState* state, float init_scale, int32_t hysteresis, void* 
 
 int dsx_unscale_norm(const void* grad, int grad_dtype, int64_t n, const DsxState* state, double* partials,
                      int32_t nparts, void* stream) {
-  if (!is16(grad_dtype)) return fail(DSX_EINVAL, "grad dtype must be DSX_F16 or DSX_BF16 (got %d)", grad_dtype);
+  if (!is_grad_dtype(grad_dtype))
+    return fail(DSX_EINVAL, "grad dtype must be DSX_F16, DSX_BF16 or DSX_F32 (got %d)", grad_dtype);
   if (n < 0) return fail(DSX_EINVAL, "n must be >= 0");
   if (n > 0 && (!grad || !aligned16(grad))) return fail(DSX_EINVAL, "grad must be non-null and 16-byte aligned");
   if (!state) return fail(DSX_EINVAL, "null state");
@@ -676,7 +762,32 @@ int dsx_finalize(const double* partials, int32_t nparts, DsxState* state, DsxSca
   if (rc) return rc;
   if (!state || !out) return fail(DSX_EINVAL, "null state or scalars");
   if (bc_len < 0 || (bc_len > 0 && !bc_table)) return fail(DSX_EINVAL, "bad bias-correction table");
-  return do_finalize(partials, nparts, state, scaler, hyper, bc_table, bc_len, out, as_stream(stream));
+  return do_finalize(partials, nparts, state, scaler, one_group(hyper, bc_table), bc_len, out, as_stream(stream));
+}
+
+int dsx_finalize_groups(const double* partials, int32_t nparts, DsxState* state, DsxScalerConfig scaler,
+                        const DsxAdamwHyper* hypers, const double* const* bc_tables, const int32_t* t_offsets,
+                        int32_t ngroups, int32_t bc_len, DsxStepScalars* out, void* stream) {
+  int rc = check_parts(partials, nparts);
+  if (!rc) rc = check_scaler(scaler);
+  if (rc) return rc;
+  if (ngroups < 1 || ngroups > DSX_MAX_GROUPS)
+    return fail(DSX_EINVAL, "ngroups must be in [1, %d] (got %d)", DSX_MAX_GROUPS, ngroups);
+  if (!hypers || !bc_tables || !t_offsets) return fail(DSX_EINVAL, "null group arrays");
+  if (!state || !out) return fail(DSX_EINVAL, "null state or scalars");
+  if (bc_len < 0) return fail(DSX_EINVAL, "bad bias-correction table length");
+  Groups grp = {};
+  grp.n = ngroups;
+  for (int k = 0; k < ngroups; ++k) {
+    rc = check_hyper(hypers[k]);
+    if (rc) return rc;
+    if (bc_len > 0 && !bc_tables[k]) return fail(DSX_EINVAL, "null bias-correction table for group %d", k);
+    if (t_offsets[k] < 0) return fail(DSX_EINVAL, "negative t_offset for group %d", k);
+    grp.hyper[k] = hypers[k];
+    grp.bc[k] = bc_tables[k];
+    grp.t_offset[k] = t_offsets[k];
+  }
+  return do_finalize(partials, nparts, state, scaler, grp, bc_len, out, as_stream(stream));
 }
 
 int dsx_adamw_flat(float* master, float* exp_avg, float* exp_avg_sq, void* param16, int param_dtype,
@@ -701,49 +812,54 @@ int dsx_zero_step_flat(float* master, float* exp_avg, float* exp_avg_sq, void* p
   if (bc_len < 0 || (bc_len > 0 && !bc_table)) return fail(DSX_EINVAL, "bad bias-correction table");
   hipStream_t s = as_stream(stream);
   rc = do_unscale_norm(grad, grad_dtype, n, state, partials, nparts, s);
-  if (!rc) rc = do_finalize(partials, nparts, state, scaler, hyper, bc_table, bc_len, out, s);
+  if (!rc) rc = do_finalize(partials, nparts, state, scaler, one_group(hyper, bc_table), bc_len, out, s);
   if (!rc) rc = do_adamw_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, out, s);
   return rc;
 }
 
 int dsx_unscale_norm_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int grad_dtype,
                            const DsxState* state, double* partials, int32_t nparts, void* stream) {
-  if (!is16(grad_dtype)) return fail(DSX_EINVAL, "grad dtype must be DSX_F16 or DSX_BF16 (got %d)", grad_dtype);
+  if (!is_grad_dtype(grad_dtype))
+    return fail(DSX_EINVAL, "grad dtype must be DSX_F16, DSX_BF16 or DSX_F32 (got %d)", grad_dtype);
   if (nchunks < 0 || (nchunks > 0 && (!tensors || !chunks))) return fail(DSX_EINVAL, "bad chunk table");
   if (!state) return fail(DSX_EINVAL, "null state");
   int rc = check_parts(partials, nparts);
   if (rc) return rc;
   hipStream_t s = as_stream(stream);
-  if (grad_dtype == DSX_BF16)
-    hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_BF16>), dim3(nparts), dim3(kBlock), 0, s, tensors, chunks, nchunks,
-                       state, partials);
-  else
-    hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_F16>), dim3(nparts), dim3(kBlock), 0, s, tensors, chunks, nchunks,
-                       state, partials);
+  const dim3 grid(nparts), blk(kBlock);
+  switch (grad_dtype) {
+    case DSX_BF16:
+      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_BF16>), grid, blk, 0, s, tensors, chunks, nchunks, state,
+                         partials);
+      break;
+    case DSX_F16:
+      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_F16>), grid, blk, 0, s, tensors, chunks, nchunks, state,
+                         partials);
+      break;
+    default:
+      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_F32>), grid, blk, 0, s, tensors, chunks, nchunks, state,
+                         partials);
+      break;
+  }
   return launch_status("dsx_unscale_norm_multi");
 }
 
 int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int param_dtype,
                     int grad_dtype, const DsxStepScalars* scalars, void* stream) {
-  if (!is16(grad_dtype)) return fail(DSX_EINVAL, "grad dtype must be DSX_F16 or DSX_BF16 (got %d)", grad_dtype);
+  if (!is_grad_dtype(grad_dtype))
+    return fail(DSX_EINVAL, "grad dtype must be DSX_F16, DSX_BF16 or DSX_F32 (got %d)", grad_dtype);
   if (!is16(param_dtype)) return fail(DSX_EINVAL, "param16 dtype must be DSX_F16 or DSX_BF16 (got %d)", param_dtype);
   if (nchunks < 0 || (nchunks > 0 && (!tensors || !chunks))) return fail(DSX_EINVAL, "bad chunk table");
   if (!scalars) return fail(DSX_EINVAL, "null scalars");
   if (nchunks == 0) return DSX_OK;
-  int64_t blocks = (int64_t)cu_count() * g_tune.k2_blocks_per_cu;
+  int64_t blocks = (int64_t)cu_count() * 8;
   if (blocks > nchunks) blocks = nchunks;
   hipStream_t s = as_stream(stream);
-  const dim3 grid((unsigned)blocks), blk(kBlock);
-  if (grad_dtype == DSX_BF16) {
-    if (param_dtype == DSX_BF16)
-      hipLaunchKernelGGL((k2_adamw_multi<DSX_BF16, DSX_BF16>), grid, blk, 0, s, tensors, chunks, nchunks, scalars);
-    else
-      hipLaunchKernelGGL((k2_adamw_multi<DSX_BF16, DSX_F16>), grid, blk, 0, s, tensors, chunks, nchunks, scalars);
-  } else {
-    if (param_dtype == DSX_BF16)
-      hipLaunchKernelGGL((k2_adamw_multi<DSX_F16, DSX_BF16>), grid, blk, 0, s, tensors, chunks, nchunks, scalars);
-    else
-      hipLaunchKernelGGL((k2_adamw_multi<DSX_F16, DSX_F16>), grid, blk, 0, s, tensors, chunks, nchunks, scalars);
+  const dim3 grid((unsigned)blocks);
+  switch (grad_dtype) {
+    case DSX_BF16: launch_k3<DSX_BF16>(param_dtype, grid, tensors, chunks, nchunks, scalars, s); break;
+    case DSX_F16: launch_k3<DSX_F16>(param_dtype, grid, tensors, chunks, nchunks, scalars, s); break;
+    default: launch_k3<DSX_F32>(param_dtype, grid, tensors, chunks, nchunks, scalars, s); break;
   }
   return launch_status("dsx_adamw_multi");
 }

@@ -1,0 +1,122 @@
+"""One flat partition holding every trainable parameter of a rank.
+
+The reference packs per-parameter grads into fp32 flat buffers every step
+(OptimizedGradientBucket, Src/zero/stage1.py:109-151; AdvancedGradientPartitioner
+with per-parameter views, Src/zero/stage2.py:108-193) and computes partition
+bounds element-granular (Src/zero/partition.py:102-141). Here the layout is
+built once and the copies disappear:
+
+  param16  n x fp16/bf16   the model's parameters (param.data are views)
+  grad     n x fp16/bf16   the model's grads (param.grad are views; autograd
+                           accumulates into them in place)
+  master   n x fp32        the optimizer's master weights
+  exp_avg, exp_avg_sq      n x fp32
+
+With fp32 training there is no param16: param.data are views of master and
+grads are fp32. Parameters are laid out group by group in model order; every
+parameter (and so every group) starts on an 8-element boundary, so each
+group's range is 16-byte aligned in every buffer. Padding elements have zero
+grad and zero master and stay zero under AdamW.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+ALIGN = 8
+
+
+def _round_up(x: int, a: int) -> int:
+    return (x + a - 1) // a * a
+
+
+@dataclass
+class Slot:
+    offset: int
+    numel: int
+    shape: torch.Size
+    group: int
+    name: str
+
+
+class FlatPartition:
+    def __init__(self, groups: list[list[torch.nn.Parameter]], device: torch.device,
+                 param_dtype: torch.dtype | None, names: dict | None = None):
+        """groups: parameter lists (one per optimizer param group).
+        param_dtype: torch.float16 / torch.bfloat16 for mixed precision, None
+        for fp32 training."""
+        if param_dtype not in (None, torch.float16, torch.bfloat16):
+            raise ValueError(f"param_dtype must be float16, bfloat16 or None, got {param_dtype}")
+        names = names or {}
+        self.device = torch.device(device)
+        self.param_dtype = param_dtype
+        self.grad_dtype = param_dtype or torch.float32
+        self.slots: list[Slot] = []
+        self.params: list[torch.nn.Parameter] = []
+        self.group_ranges: list[tuple[int, int]] = []
+        seen = set()
+        off = 0
+        for gi, plist in enumerate(groups):
+            start = off
+            for p in plist:
+                if id(p) in seen:
+                    raise ValueError("a parameter appears in more than one group")
+                seen.add(id(p))
+                n = p.numel()
+                self.slots.append(Slot(off, n, p.shape, gi, names.get(id(p), f"param{len(self.params)}")))
+                self.params.append(p)
+                off = _round_up(off + n, ALIGN)
+            self.group_ranges.append((start, off))
+        self.numel = off
+        dev = self.device
+        self.master = torch.zeros(self.numel, dtype=torch.float32, device=dev)
+        self.exp_avg = torch.zeros(self.numel, dtype=torch.float32, device=dev)
+        self.exp_avg_sq = torch.zeros(self.numel, dtype=torch.float32, device=dev)
+        self.grad = torch.zeros(self.numel, dtype=self.grad_dtype, device=dev)
+        self.param16 = torch.zeros(self.numel, dtype=param_dtype, device=dev) if param_dtype else None
+        with torch.no_grad():
+            for s, p in zip(self.slots, self.params):
+                self.master[s.offset:s.offset + s.numel].copy_(p.detach().reshape(-1).to(dev, torch.float32))
+            if self.param16 is not None:
+                self.param16.copy_(self.master)  # round to nearest even
+        self.rebind()
+
+    def rebind(self) -> None:
+        """Point every param.data / param.grad at its view of the flat buffers."""
+        home = self.param16 if self.param16 is not None else self.master
+        for s, p in zip(self.slots, self.params):
+            p.data = home[s.offset:s.offset + s.numel].view(s.shape)
+            p.grad = self.grad[s.offset:s.offset + s.numel].view(s.shape)
+
+    def check_grads_bound(self) -> None:
+        """Autograd accumulates into an existing .grad in place; if something
+        replaced a param's .grad with a new tensor, copy it into the flat
+        buffer and restore the view."""
+        for s, p in zip(self.slots, self.params):
+            g = p.grad
+            view = self.grad[s.offset:s.offset + s.numel]
+            if g is None:
+                view.zero_()
+                p.grad = view.view(s.shape)
+            elif g.data_ptr() != view.data_ptr():
+                view.copy_(g.reshape(-1))
+                p.grad = view.view(s.shape)
+
+    def group_views(self, gi: int):
+        a, b = self.group_ranges[gi]
+        return (self.master[a:b], self.exp_avg[a:b], self.exp_avg_sq[a:b],
+                self.param16[a:b] if self.param16 is not None else None, self.grad[a:b])
+
+    def views_of(self, i: int) -> dict:
+        s = self.slots[i]
+        sl = slice(s.offset, s.offset + s.numel)
+        return {"master": self.master[sl].view(s.shape), "exp_avg": self.exp_avg[sl].view(s.shape),
+                "exp_avg_sq": self.exp_avg_sq[sl].view(s.shape)}
+
+    def zero_grad(self) -> None:
+        self.grad.zero_()
+
+    def layout(self) -> list[dict]:
+        return [{"name": s.name, "offset": s.offset, "numel": s.numel, "shape": list(s.shape), "group": s.group}
+                for s in self.slots]

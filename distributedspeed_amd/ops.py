@@ -11,19 +11,30 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import (DSX_BF16, DSX_F16, DsxAdamwHyper, DsxScalerConfig, DsxStepScalars, DsxState)
+from ._lib import (DSX_BF16, DSX_F16, DSX_F32, DSX_MAX_GROUPS, DsxAdamwHyper, DsxScalerConfig, DsxStepScalars,
+                   DsxState)
 
 _DT = {torch.float16: DSX_F16, torch.bfloat16: DSX_BF16}
+_GDT = {torch.float16: DSX_F16, torch.bfloat16: DSX_BF16, torch.float32: DSX_F32}
 
 STATE_BYTES = ctypes.sizeof(DsxState)
 SCALARS_BYTES = ctypes.sizeof(DsxStepScalars)
 
 
 def dtype_code(dt: torch.dtype) -> int:
+    """Code of a 16-bit parameter dtype."""
     try:
         return _DT[dt]
     except KeyError:
         raise TypeError(f"expected a float16 or bfloat16 tensor, got {dt}") from None
+
+
+def grad_code(dt: torch.dtype) -> int:
+    """Code of a grad dtype (fp16, bf16 or fp32)."""
+    try:
+        return _GDT[dt]
+    except KeyError:
+        raise TypeError(f"expected a float16, bfloat16 or float32 grad, got {dt}") from None
 
 
 def _stream(device: torch.device) -> ctypes.c_void_p:
@@ -95,7 +106,7 @@ def unscale_norm(grad: torch.Tensor, state: torch.Tensor, partials: torch.Tensor
     """K1: partials[:nparts] = per-block fp64 sums of (grad * inv_scale)^2."""
     dev = _device(grad)
     _need(grad, "grad", None, None, dev)
-    gdt = dtype_code(grad.dtype)
+    gdt = grad_code(grad.dtype)
     _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
     nparts = nparts or partials.numel()
     _need(partials, "partials", torch.float64, None, dev, 8)
@@ -127,8 +138,8 @@ def adamw_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Te
     for name, t in (("master", master), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
         _need(t, name, torch.float32, n, dev)
     _need(grad, "grad", None, n, dev)
-    gdt = dtype_code(grad.dtype)
-    pdt = gdt
+    gdt = grad_code(grad.dtype)
+    pdt = DSX_F16
     if param16 is not None:
         _need(param16, "param16", None, n, dev)
         pdt = dtype_code(param16.dtype)
@@ -147,8 +158,8 @@ def zero_step_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torc
     for name, t in (("master", master), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
         _need(t, name, torch.float32, n, dev)
     _need(grad, "grad", None, n, dev)
-    gdt = dtype_code(grad.dtype)
-    pdt = gdt
+    gdt = grad_code(grad.dtype)
+    pdt = DSX_F16
     if param16 is not None:
         _need(param16, "param16", None, n, dev)
         pdt = dtype_code(param16.dtype)
@@ -165,35 +176,68 @@ def zero_step_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torc
               _stream(dev))
 
 
+# ---- parameter groups ---------------------------------------------------------------
+
+def finalize_groups(partials: torch.Tensor, nparts: int, state: torch.Tensor, scaler: DsxScalerConfig,
+                    hypers: list[DsxAdamwHyper], bc_tables: list[torch.Tensor], t_offsets: list[int], bc_len: int,
+                    out: torch.Tensor) -> None:
+    """K0 for several parameter groups: out holds len(hypers) DsxStepScalars."""
+    dev = _device(state)
+    k = len(hypers)
+    if not 1 <= k <= DSX_MAX_GROUPS or len(bc_tables) != k or len(t_offsets) != k:
+        raise ValueError(f"need 1..{DSX_MAX_GROUPS} groups with one table and offset each")
+    _need(partials, "partials", torch.float64, None, dev, 8)
+    _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
+    _need(out, "scalars", torch.uint8, SCALARS_BYTES * k, dev, 8)
+    for i, t in enumerate(bc_tables):
+        _need(t, f"bc_table[{i}]", torch.float64, None, dev, 8)
+        if t.numel() < 2 * bc_len:
+            raise ValueError("bc_table shorter than bc_len")
+    hy = (DsxAdamwHyper * k)(*hypers)
+    tabs = (ctypes.c_void_p * k)(*[t.data_ptr() for t in bc_tables])
+    offs = (ctypes.c_int32 * k)(*[int(x) for x in t_offsets])
+    _lib.call("dsx_finalize_groups", _ptr(partials), int(nparts), _ptr(state), scaler, hy, tabs, offs, k,
+              int(bc_len), _ptr(out), _stream(dev))
+
+
 # ---- ragged lists (K3) --------------------------------------------------------------
 
 class ChunkTable:
     """Device-resident tensor and chunk tables of a ragged list (built once;
-    the pointers must stay valid while the table is used)."""
+    the tensors must stay alive and in place while the table is used).
 
-    def __init__(self, masters, exp_avgs, exp_avg_sqs, params16, grads, chunk_elems: int = 65536):
+    masters/exp_avgs/exp_avg_sqs are fp32; grads share one dtype (fp16, bf16
+    or fp32); params16 (optional) share one 16-bit dtype; groups[i] is the
+    parameter group of tensor i (indexes the scalars array)."""
+
+    def __init__(self, masters, exp_avgs, exp_avg_sqs, params16, grads, groups=None, chunk_elems: int = 65536):
         k = len(masters)
         if not (len(exp_avgs) == len(exp_avg_sqs) == len(grads) == k) or (params16 is not None and len(params16) != k):
             raise ValueError("tensor lists must have equal lengths")
         if k == 0:
             raise ValueError("empty tensor list")
+        groups = list(groups) if groups is not None else [0] * k
+        if len(groups) != k or min(groups) < 0 or max(groups) >= DSX_MAX_GROUPS:
+            raise ValueError("groups must give one index in [0, DSX_MAX_GROUPS) per tensor")
         dev = _device(masters[0])
         self.device = dev
-        self.gdt = dtype_code(grads[0].dtype)
-        self.pdt = dtype_code(params16[0].dtype) if params16 is not None else self.gdt
+        self.gdt = grad_code(grads[0].dtype)
+        self.pdt = dtype_code(params16[0].dtype) if params16 is not None else DSX_F16
+        self.ngroups = max(groups) + 1
         refs = (_lib.DsxTensorRef * k)()
         numels = (ctypes.c_int64 * k)()
         for i in range(k):
             n = masters[i].numel()
             for name, t in (("master", masters[i]), ("exp_avg", exp_avgs[i]), ("exp_avg_sq", exp_avg_sqs[i])):
                 _need(t, f"{name}[{i}]", torch.float32, n, dev, 4)
-            _need(grads[i], f"grad[{i}]", grads[0].dtype, n, dev, 2)
+            _need(grads[i], f"grad[{i}]", grads[0].dtype, n, dev, grads[0].element_size())
             p16 = None
             if params16 is not None:
                 p16 = params16[i]
                 _need(p16, f"param16[{i}]", params16[0].dtype, n, dev, 2)
             refs[i] = _lib.DsxTensorRef(masters[i].data_ptr(), exp_avgs[i].data_ptr(), exp_avg_sqs[i].data_ptr(),
-                                        p16.data_ptr() if p16 is not None else None, grads[i].data_ptr(), n)
+                                        p16.data_ptr() if p16 is not None else None, grads[i].data_ptr(), n,
+                                        int(groups[i]), 0)
             numels[i] = n
         L = _lib.load()
         cnt = L.dsx_count_chunks(numels, k, int(chunk_elems))
@@ -220,7 +264,10 @@ def unscale_norm_multi(table: ChunkTable, state: torch.Tensor, partials: torch.T
 
 
 def adamw_multi(table: ChunkTable, scalars: torch.Tensor) -> None:
+    """K3: AdamW + cast over the list; scalars holds table.ngroups entries."""
     dev = table.device
-    _need(scalars, "scalars", torch.uint8, SCALARS_BYTES, dev, 8)
+    _need(scalars, "scalars", torch.uint8, None, dev, 8)
+    if scalars.numel() < SCALARS_BYTES * table.ngroups:
+        raise ValueError(f"scalars must hold {table.ngroups} DsxStepScalars")
     _lib.call("dsx_adamw_multi", _ptr(table.tensors), _ptr(table.chunks), table.nchunks, table.pdt, table.gdt,
               _ptr(scalars), _stream(dev))

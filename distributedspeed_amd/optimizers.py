@@ -1,0 +1,240 @@
+"""AdamWOptimizer: the fused ZeRO optimizer step behind torch's Optimizer API.
+
+The reference's stages call `optimizer.step_fused()` when the optimizer has
+one and `optimizer.step()` otherwise (Src/zero/stage1.py:522-525,
+Src/zero/stage2.py:609-612); its public name for a fused AdamW is
+`optimizers.AdamWOptimizer` (Src/__init__.py:109-114). This class is that
+optimizer: torch.optim.AdamW's constructor arguments, param_groups,
+state[p] (exp_avg / exp_avg_sq / master / step as live views), zero_grad,
+state_dict / load_state_dict, and a step that runs entirely on the GPU:
+
+    K1 unscale + inf/NaN + norm partials   over the whole flat grad buffer
+    K0 finalize                            skip, norm, clip, t, per-group
+                                           scalars, loss-scaler update
+    K2 AdamW + 16-bit cast                 one launch per parameter group
+
+with no host synchronisation. Parameters are re-homed into one
+FlatPartition at construction (param.data / param.grad become views).
+"""
+from __future__ import annotations
+
+import math
+from typing import Iterable
+
+import torch
+
+from . import ops
+from ._lib import DSX_MAX_GROUPS, DsxAdamwHyper
+from .flat import FlatPartition
+from .flat_step import BiasCorrectionTable, ScalerConfig
+
+
+class AdamWOptimizer(torch.optim.Optimizer):
+    def __init__(self, params: Iterable, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
+                 weight_decay: float = 1e-2, *, max_grad_norm: float = 0.0, param_dtype: torch.dtype | None = None,
+                 loss_scaler: ScalerConfig | None = None, device: torch.device | None = None,
+                 param_names: dict | None = None):
+        if not 0.0 <= lr:
+            raise ValueError(f"Invalid learning rate: {lr}")
+        if not 0.0 <= eps:
+            raise ValueError(f"Invalid epsilon value: {eps}")
+        if not 0.0 <= betas[0] < 1.0:
+            raise ValueError(f"Invalid beta parameter at index 0: {betas[0]}")
+        if not 0.0 <= betas[1] < 1.0:
+            raise ValueError(f"Invalid beta parameter at index 1: {betas[1]}")
+        if not 0.0 <= weight_decay:
+            raise ValueError(f"Invalid weight_decay value: {weight_decay}")
+        if math.isnan(max_grad_norm) or max_grad_norm < 0:
+            raise ValueError(f"Invalid max_grad_norm: {max_grad_norm}")
+        defaults = dict(lr=lr, betas=tuple(betas), eps=eps, weight_decay=weight_decay)
+        super().__init__(params, defaults)
+        if len(self.param_groups) > DSX_MAX_GROUPS:
+            raise ValueError(f"at most {DSX_MAX_GROUPS} parameter groups are supported")
+        plist = [p for g in self.param_groups for p in g["params"]]
+        if not plist:
+            raise ValueError("optimizer got an empty parameter list")
+        if device is None:
+            device = plist[0].device if plist[0].is_cuda else torch.device("cuda", torch.cuda.current_device())
+        self.device = torch.device(device)
+        if param_dtype is None and plist[0].dtype in (torch.float16, torch.bfloat16):
+            param_dtype = plist[0].dtype
+        self.max_grad_norm = float(max_grad_norm)
+        self.clip_eps = 1e-6
+        self.scaler = loss_scaler or ScalerConfig(mode="none")
+        self.scaler.validate()
+        self.flat = FlatPartition([g["params"] for g in self.param_groups], self.device, param_dtype, param_names)
+        self.nparts = ops.suggest_partials(self.flat.numel)
+        self.partials = torch.zeros(self.nparts, dtype=torch.float64, device=self.device)
+        self.dstate = ops.new_state(self.device, self.scaler.init_scale if self.scaler.mode != "none" else 1.0,
+                                    self.scaler.hysteresis if self.scaler.mode == "dynamic" else 1)
+        self.scalars = torch.zeros(ops.SCALARS_BYTES * len(self.param_groups), dtype=torch.uint8, device=self.device)
+        self._bc: dict[tuple[float, float], BiasCorrectionTable] = {}
+        self._t_offsets = [0] * len(self.param_groups)
+        self.steps_issued = 0
+        self._bind_state()
+
+    # ---- torch.optim.Optimizer protocol ---------------------------------------------
+
+    def _bind_state(self) -> None:
+        t_view = self.dstate[12:16].view(torch.int32)  # DsxState.t
+        for i, p in enumerate(self.flat.params):
+            st = self.flat.views_of(i)
+            st["step"] = t_view
+            self.state[p] = st
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        """Zero the flat grad buffer. The grads are views into it, so they are
+        zeroed rather than set to None whatever set_to_none says."""
+        self.flat.zero_grad()
+
+    def add_param_group(self, param_group: dict) -> None:
+        if getattr(self, "flat", None) is not None:
+            raise NotImplementedError("add_param_group after construction would move the flat partition; "
+                                      "build the optimizer with all groups")
+        super().add_param_group(param_group)
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        self.step_fused()
+        return loss
+
+    # ---- the fused step -------------------------------------------------------------------
+
+    def _hypers(self):
+        hs, tabs = [], []
+        for g in self.param_groups:
+            b1, b2 = float(g["betas"][0]), float(g["betas"][1])
+            hs.append(DsxAdamwHyper(float(g["lr"]), b1, b2, float(g["eps"]), float(g["weight_decay"]),
+                                    self.max_grad_norm, self.clip_eps))
+            key = (b1, b2)
+            if key not in self._bc:
+                self._bc[key] = BiasCorrectionTable(self.device, b1, b2)
+            self._bc[key].ensure(self.steps_issued)
+            tabs.append(self._bc[key])
+        bc_len = min(t.length for t in tabs)
+        return hs, [t.table for t in tabs], bc_len
+
+    def step_fused(self) -> None:
+        """K1 -> K0 -> K2 on the current stream; no host synchronisation."""
+        self.flat.check_grads_bound()
+        self.steps_issued += 1
+        hs, tables, bc_len = self._hypers()
+        ops.unscale_norm(self.flat.grad, self.dstate, self.partials, self.nparts)
+        ops.finalize_groups(self.partials, self.nparts, self.dstate, self.scaler.to_c(), hs, tables,
+                            self._t_offsets, bc_len, self.scalars)
+        for gi in range(len(self.param_groups)):
+            master, m, v, p16, g = self.flat.group_views(gi)
+            if master.numel() == 0:
+                continue
+            sc = self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
+            ops.adamw_flat(master, m, v, p16, g, sc)
+
+    # ---- device-side values, read on demand --------------------------------------------------
+
+    def loss_scale_tensor(self) -> torch.Tensor:
+        """The loss scale as a one-element fp32 device tensor (no sync)."""
+        return ops.scale_view(self.dstate)
+
+    def read_state(self):
+        """DsxState on the host (synchronises)."""
+        return ops.read_state(self.dstate)
+
+    def last_scalars(self, group: int = 0):
+        return ops.read_scalars(self.scalars[group * ops.SCALARS_BYTES:(group + 1) * ops.SCALARS_BYTES])
+
+    def grad_norm_tensor(self) -> torch.Tensor:
+        """Norm seen by the last step, as an fp64 device tensor (no sync)."""
+        return self.dstate[40:48].view(torch.float64)
+
+    # ---- checkpoints ----------------------------------------------------------------------------
+
+    def state_dict(self) -> dict:
+        """torch-compatible layout (state keyed by parameter index with
+        exp_avg / exp_avg_sq / step) plus the fp32 master and the device
+        scaler state; tensors are host copies."""
+        s = self.read_state()
+        groups = []
+        idx = 0
+        for g in self.param_groups:
+            gd = {k: v for k, v in g.items() if k != "params"}
+            gd["params"] = list(range(idx, idx + len(g["params"])))
+            idx += len(g["params"])
+            groups.append(gd)
+        state = {}
+        for i in range(len(self.flat.params)):
+            v = self.flat.views_of(i)
+            state[i] = {"step": torch.tensor(float(s.t)), "exp_avg": v["exp_avg"].detach().cpu().clone(),
+                        "exp_avg_sq": v["exp_avg_sq"].detach().cpu().clone(),
+                        "master": v["master"].detach().cpu().clone()}
+        return {"state": state, "param_groups": groups,
+                "dsx": {"scale": s.scale, "good_steps": s.good_steps, "hyst_left": s.hyst_left, "t": s.t,
+                        "iter": s.iter, "overflow_count": s.overflow_count, "steps_issued": self.steps_issued,
+                        "layout": self.flat.layout(), "scaler": dict(vars(self.scaler))}}
+
+    def load_state_dict(self, state_dict: dict) -> None:
+        groups = state_dict["param_groups"]
+        if len(groups) != len(self.param_groups):
+            raise ValueError("loaded state dict has a different number of parameter groups")
+        for g, sg in zip(self.param_groups, groups):
+            if len(g["params"]) != len(sg["params"]):
+                raise ValueError("loaded state dict contains a parameter group that doesn't match the size "
+                                 "of optimizer's group")
+            for k, v in sg.items():
+                if k != "params":
+                    g[k] = tuple(v) if k == "betas" else v
+        st = state_dict["state"]
+        with torch.no_grad():
+            for i in range(len(self.flat.params)):
+                if i not in st:
+                    continue
+                views = self.flat.views_of(i)
+                for key in ("exp_avg", "exp_avg_sq", "master"):
+                    if key in st[i]:
+                        src = st[i][key]
+                        if src.shape != views[key].shape:
+                            raise ValueError(f"state for parameter {i} has shape {tuple(src.shape)}, "
+                                             f"expected {tuple(views[key].shape)}")
+                        views[key].copy_(src.to(self.device, torch.float32))
+            if self.flat.param16 is not None:
+                self.flat.param16.copy_(self.flat.master)
+        dsx = state_dict.get("dsx")
+        t = int(dsx["t"]) if dsx else int(max((float(v["step"]) for v in st.values()), default=0))
+        from ._lib import DsxState
+        hs = DsxState()
+        hs.scale = float(dsx["scale"]) if dsx else (self.scaler.init_scale if self.scaler.mode != "none" else 1.0)
+        hs.good_steps = int(dsx["good_steps"]) if dsx else 0
+        hs.hyst_left = int(dsx["hyst_left"]) if dsx else max(1, self.scaler.hysteresis)
+        hs.t = t
+        hs.iter = int(dsx["iter"]) if dsx else t
+        hs.overflow_count = int(dsx["overflow_count"]) if dsx else 0
+        self.dstate.copy_(torch.frombuffer(bytearray(bytes(hs)), dtype=torch.uint8).to(self.device))
+        self.steps_issued = int(dsx["steps_issued"]) if dsx else t
+        self._bind_state()
+
+
+def adopt_torch_optimizer(opt: torch.optim.Optimizer, **kwargs) -> AdamWOptimizer:
+    """torch.optim.AdamW (or Adam without weight decay, where Adam and AdamW
+    coincide) -> AdamWOptimizer over the same param groups and
+    hyper-parameters. Anything else is refused rather than silently changed
+    into a different update rule."""
+    if not isinstance(opt, torch.optim.Optimizer):
+        raise TypeError(f"expected a torch.optim.Optimizer, got {type(opt).__name__}")
+    if isinstance(opt, AdamWOptimizer):
+        return opt
+    is_adamw = isinstance(opt, torch.optim.AdamW) or (isinstance(opt, torch.optim.Adam)
+                                                      and opt.defaults.get("decoupled_weight_decay", False))
+    plain_adam_no_wd = isinstance(opt, torch.optim.Adam) and all(g.get("weight_decay", 0) == 0
+                                                                 for g in opt.param_groups)
+    if not (is_adamw or plain_adam_no_wd):
+        raise NotImplementedError(f"{type(opt).__name__} is not supported by the fused step; use AdamW")
+    if any(g.get("amsgrad") or g.get("maximize") for g in opt.param_groups):
+        raise NotImplementedError("amsgrad / maximize are not supported by the fused step")
+    groups = [{k: v for k, v in g.items() if k in ("params", "lr", "betas", "eps", "weight_decay")}
+              for g in opt.param_groups]
+    d = opt.defaults
+    return AdamWOptimizer(groups, lr=float(d["lr"]), betas=d["betas"], eps=d["eps"], weight_decay=d["weight_decay"],
+                          **kwargs)

@@ -22,6 +22,8 @@
  *     scratch (the fp64 partials) is passed in by the caller.
  *   - Element counts are int64_t. Flat buffers must be 16-byte aligned; any n
  *     is accepted (the n % 8 tail is handled in-kernel).
+ *   - Grads are DSX_F16, DSX_BF16 or DSX_F32 (fp32 training: the grad is
+ *     read as is); param16 is DSX_F16 or DSX_BF16.
  *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL means
  *     the null stream). No call synchronises the host with the device.
  *   - Return value: 0 on success; DSX_EINVAL (== hipErrorInvalidValue) for a
@@ -68,6 +70,9 @@ extern "C" {
 
 /* upper bound on the partials one K1 launch may write */
 #define DSX_MAX_PARTIALS 8192
+
+/* upper bound on the parameter groups of one dsx_finalize_groups call */
+#define DSX_MAX_GROUPS 16
 
 /* Device-resident optimizer + loss-scaler state (64 bytes). */
 typedef struct DsxState {
@@ -125,8 +130,8 @@ typedef struct DsxStepScalars {
 } DsxStepScalars;
 
 /* One tensor of a ragged list (K3). master/exp_avg/exp_avg_sq fp32;
- * param16 and grad are 16-bit of the dtype given to the call; param16 may be
- * NULL (no cast written). */
+ * grad of the call's grad dtype; param16 (16-bit, may be NULL: no cast
+ * written) of the call's param dtype. `group` selects scalars[group]. */
 typedef struct DsxTensorRef {
   float*      master;
   float*      exp_avg;
@@ -134,6 +139,8 @@ typedef struct DsxTensorRef {
   void*       param16;
   const void* grad;
   int64_t     numel;
+  int32_t     group;
+  int32_t     reserved;
 } DsxTensorRef;
 
 /* One chunk of a ragged list: elements [start, start+len) of tensor `tensor`. */
@@ -202,6 +209,20 @@ int dsx_finalize(const double* partials, int32_t nparts, DsxState* state,
                  DsxScalerConfig scaler, DsxAdamwHyper hyper,
                  const double* bc_table, int32_t bc_len, DsxStepScalars* out,
                  void* stream);
+
+/* The same for up to DSX_MAX_GROUPS parameter groups (torch param_groups
+ * with their own lr / betas / eps / weight_decay): one skip decision, norm,
+ * clip coefficient (from hypers[0].max_grad_norm) and scaler update; out[g]
+ * receives group g's scalars. hypers, bc_tables and t_offsets are HOST
+ * arrays of ngroups entries (bc_tables[g] is a device table as above; the
+ * tables share bc_len); group g steps with t - t_offsets[g] (a group added
+ * after k steps starts its own count at 1, as torch's per-parameter step
+ * does). Replaces the per-group loop of torch.optim.AdamW.step. */
+int dsx_finalize_groups(const double* partials, int32_t nparts, DsxState* state,
+                        DsxScalerConfig scaler, const DsxAdamwHyper* hypers,
+                        const double* const* bc_tables,
+                        const int32_t* t_offsets, int32_t ngroups,
+                        int32_t bc_len, DsxStepScalars* out, void* stream);
 
 /* ---- K2: AdamW + cast over a flat partition -------------------------- */
 

@@ -35,6 +35,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#define DSXO_F32 0
 #define DSXO_F16 1
 #define DSXO_BF16 2
 
@@ -98,19 +99,21 @@ uint16_t dsxo_f32_to_bf16(float x) {
   return (uint16_t)r;
 }
 
-static inline float load16(const uint16_t* g, int64_t i, int dt) {
-  return dt == DSXO_BF16 ? dsxo_bf16_to_f32(g[i]) : dsxo_f16_to_f32(g[i]);
+/* Grad element i as fp32: 16-bit storage widened exactly, or fp32 as is. */
+static inline float load_grad(const void* g, int64_t i, int dt) {
+  if (dt == DSXO_F32) return ((const float*)g)[i];
+  const uint16_t h = ((const uint16_t*)g)[i];
+  return dt == DSXO_BF16 ? dsxo_bf16_to_f32(h) : dsxo_f16_to_f32(h);
 }
-
 /* Sum over i of (double)(f32(g[i]) * inv_scale)^2 in index order, with
  * Neumaier's compensated summation so that the result is accurate to a few
  * ulp of fp64 even over 10^9 terms (a plain running sum drifts ~1e-10
  * relative there). Each square is exact in fp64. Non-finite iff some unscaled
  * grad is inf or NaN. */
-double dsxo_sumsq(const uint16_t* g, int dt, int64_t n, float inv_scale) {
+double dsxo_sumsq(const void* g, int dt, int64_t n, float inv_scale) {
   double s = 0.0, c = 0.0;
   for (int64_t i = 0; i < n; ++i) {
-    const float a = load16(g, i, dt) * inv_scale;
+    const float a = load_grad(g, i, dt) * inv_scale;
     const double x = (double)a * (double)a;
     const double t = s + x;
     if (!isfinite(t)) { s = t; c = 0.0; continue; }
@@ -123,14 +126,15 @@ double dsxo_sumsq(const uint16_t* g, int dt, int64_t n, float inv_scale) {
 
 /* Same sum, split into `nblocks` contiguous blocks summed separately and then
  * added in block order -- a second summation order for cross-checks. */
-double dsxo_sumsq_blocked(const uint16_t* g, int dt, int64_t n, float inv_scale, int64_t nblocks) {
+double dsxo_sumsq_blocked(const void* g, int dt, int64_t n, float inv_scale, int64_t nblocks) {
   double total = 0.0;
   if (nblocks < 1) nblocks = 1;
   const int64_t per = (n + nblocks - 1) / nblocks;
   for (int64_t b = 0; b < nblocks; ++b) {
     const int64_t lo = b * per, hi = lo + per < n ? lo + per : n;
     if (lo >= n) break;
-    total += dsxo_sumsq(g + lo, dt, hi - lo, inv_scale);
+    const char* base = (const char*)g + lo * (dt == DSXO_F32 ? 4 : 2);
+    total += dsxo_sumsq(base, dt, hi - lo, inv_scale);
   }
   return total;
 }
@@ -151,12 +155,13 @@ static inline void step_elt(float graw, float* p, float* m, float* v, const Dsxo
 }
 
 /* One AdamW step over n elements, in place; p16 (may be NULL) receives the
- * cast master. Elements are independent, so the loop may run in parallel. */
-void dsxo_adamw(float* p, float* m, float* v, uint16_t* p16, int pdt, const uint16_t* g, int gdt, int64_t n,
+ * cast master. Grads are 16-bit storage (gdt F16/BF16) or fp32 (gdt F32).
+ * Elements are independent, so the loop may run in parallel. */
+void dsxo_adamw(float* p, float* m, float* v, uint16_t* p16, int pdt, const void* g, int gdt, int64_t n,
                 const DsxoScalars* s) {
 #pragma omp parallel for schedule(static)
   for (int64_t i = 0; i < n; ++i) {
-    step_elt(load16(g, i, gdt), p + i, m + i, v + i, s);
+    step_elt(load_grad(g, i, gdt), p + i, m + i, v + i, s);
     if (p16) p16[i] = pdt == DSXO_BF16 ? dsxo_f32_to_bf16(p[i]) : dsxo_f32_to_f16(p[i]);
   }
 }
@@ -167,7 +172,7 @@ void dsxo_cast_f32(const float* x, uint16_t* out, int dt, int64_t n) {
 }
 
 void dsxo_widen(const uint16_t* h, float* out, int dt, int64_t n) {
-  for (int64_t i = 0; i < n; ++i) out[i] = load16(h, i, dt);
+  for (int64_t i = 0; i < n; ++i) out[i] = load_grad(h, i, dt);
 }
 
 int dsxo_num_threads(void) {

@@ -32,6 +32,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
+F32 = 0
 F16 = 1
 BF16 = 2
 
@@ -112,8 +113,14 @@ def inv_scale_of(scale: float) -> float:
     return float(np.float32(1.0 / float(np.float32(scale))))
 
 
+def _gdtype(dt: int):
+    return np.float32 if dt == F32 else np.uint16
+
+
 def sumsq(g16: np.ndarray, dt: int, inv_scale: float, blocks: int = 0) -> float:
-    _check(g16, np.uint16)
+    """Sum of (f32(g) * inv_scale)^2 in fp64; g16 is uint16 storage for
+    F16/BF16 or a float32 array for F32."""
+    _check(g16, _gdtype(dt))
     if blocks:
         return lib().dsxo_sumsq_blocked(_ptr(g16), dt, g16.size, inv_scale, blocks)
     return lib().dsxo_sumsq(_ptr(g16), dt, g16.size, inv_scale)
@@ -171,7 +178,7 @@ def adamw(p: np.ndarray, m: np.ndarray, v: np.ndarray, p16: np.ndarray | None, p
     n = p.size
     for a in (p, m, v):
         _check(a, np.float32, n)
-    _check(g16, np.uint16, n)
+    _check(g16, _gdtype(gdt), n)
     if p16 is not None:
         _check(p16, np.uint16, n)
     lib().dsxo_adamw(_ptr(p), _ptr(m), _ptr(v), _ptr(p16), pdt, _ptr(g16), gdt, n, ctypes.byref(sc))

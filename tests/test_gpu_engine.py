@@ -1,0 +1,250 @@
+"""GPU tests of the drop-in API: initialize() -> engine(batch) ->
+engine.backward(loss) -> engine.step(), checked step by step against the CPU
+oracle fed the grads autograd produced (captured from the flat grad buffer
+before each step)."""
+from __future__ import annotations
+
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import BF16, F16, torch16_to_np
+
+pytestmark = pytest.mark.gpu
+
+F32 = 0
+
+
+def _say(msg):
+    print(f"[gpu-test] {msg}", file=sys.stderr, flush=True)
+
+
+def _mlp(seed=0):
+    import torch
+    torch.manual_seed(seed)
+    return torch.nn.Sequential(torch.nn.Linear(784, 1024), torch.nn.ReLU(), torch.nn.Linear(1024, 1024),
+                               torch.nn.ReLU(), torch.nn.Linear(1024, 10))
+
+
+def _grads_np(opt):
+    g = opt.flat.grad
+    if g.dtype == __import__("torch").float32:
+        return g.detach().cpu().numpy().copy(), F32
+    return torch16_to_np(g).copy(), (F16 if g.dtype == __import__("torch").float16 else BF16)
+
+
+class GroupOracle:
+    """The oracle over a flat partition with per-group hyper-parameters and
+    one global norm / skip / scaler."""
+
+    def __init__(self, O, opt, hypers, scaler):
+        self.O = O
+        self.p = opt.flat.master.detach().cpu().numpy().copy()
+        self.m = np.zeros_like(self.p)
+        self.v = np.zeros_like(self.p)
+        self.p16 = torch16_to_np(opt.flat.param16).copy() if opt.flat.param16 is not None else None
+        self.pdt = None if opt.flat.param16 is None else (F16 if opt.flat.param16.dtype == __import__("torch").float16
+                                                           else BF16)
+        self.ranges = opt.flat.group_ranges
+        self.hypers = hypers
+        self.scaler = scaler
+        self.t = 0
+
+    def step(self, g, gdt, max_norm):
+        O = self.O
+        scale = self.scaler.scale
+        inv = O.inv_scale_of(scale)
+        ss = O.sumsq(g, gdt, inv)
+        skipped = not math.isfinite(ss)
+        if not skipped:
+            self.t += 1
+            coef = O.clip_coef(math.sqrt(ss), max_norm)
+            for (a, b), h in zip(self.ranges, self.hypers):
+                sl = slice(a, b)
+                p16 = self.p16[sl] if self.p16 is not None else None
+                pv, mv, vv = self.p[sl], self.m[sl], self.v[sl]
+                # the oracle works on contiguous arrays: run on copies, write back
+                pc, mc, vc = pv.copy(), mv.copy(), vv.copy()
+                p16c = p16.copy() if p16 is not None else None
+                O.adamw(pc, mc, vc, p16c, self.pdt or F16, np.ascontiguousarray(g[sl]), gdt,
+                        O.step_scalars(h, self.t, inv, coef))
+                pv[:], mv[:], vv[:] = pc, mc, vc
+                if p16 is not None:
+                    p16[:] = p16c
+        self.scaler.update(skipped)
+        return skipped, ss
+
+    def compare(self, opt, tag):
+        for name, ref, got in (("master", self.p, opt.flat.master), ("exp_avg", self.m, opt.flat.exp_avg),
+                               ("exp_avg_sq", self.v, opt.flat.exp_avg_sq)):
+            g = got.detach().cpu().numpy()
+            assert np.array_equal(g.view(np.uint32), ref.view(np.uint32)), f"{tag}: {name} differs"
+        if self.p16 is not None:
+            assert np.array_equal(torch16_to_np(opt.flat.param16), self.p16), f"{tag}: param16 differs"
+
+
+def _run_training(gpu, oracle, ds_config, steps, seed=0, groups=None, scheduler=None, batch=32, check=True):
+    import torch
+    import distributedspeed_amd as ds
+    model = _mlp(seed)
+    params = groups(model) if groups else None
+    engine, opt, _, sched = ds.initialize(model, ds_config, model_parameters=params)
+    base = opt.base_optimizer
+    hyp = [oracle.Hyper(lr=g["lr"], beta1=g["betas"][0], beta2=g["betas"][1], eps=g["eps"],
+                        weight_decay=g["weight_decay"], max_grad_norm=base.max_grad_norm) for g in base.param_groups]
+    sc = base.scaler
+    spec = oracle.LossScalerSpec(scale=sc.init_scale if sc.mode != "none" else 1.0, window=sc.window,
+                                 hysteresis=sc.hysteresis if sc.mode == "dynamic" else 1, min_scale=sc.min_scale,
+                                 dynamic=sc.mode == "dynamic")
+    orc = GroupOracle(oracle, base, hyp, spec)
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(seed + 100)
+    log = []
+    for step in range(steps):
+        x = torch.randn(batch, 784, device=gpu, generator=gen)
+        y = torch.randint(0, 10, (batch,), device=gpu, generator=gen)
+        out = engine(x)
+        loss = torch.nn.functional.cross_entropy(out.float(), y)
+        engine.backward(loss)
+        if check:
+            g, gdt = _grads_np(base)
+            skipped, ss = orc.step(g, gdt, base.max_grad_norm)
+        engine.step()
+        if check:
+            st = base.read_state()
+            assert bool(st.last_skip) == skipped, f"step {step}: skip {st.last_skip} vs {skipped}"
+            assert st.scale == spec.scale, f"step {step}: scale {st.scale} vs {spec.scale}"
+            orc.compare(base, f"step {step}")
+            log.append((skipped, st.scale, float(loss)))
+    return engine, log
+
+
+def test_engine_fp16_mlp_matches_oracle(gpu, oracle):
+    _say("engine fp16 mlp")
+    cfg = {"train_batch_size": 32, "optimizer": {"type": "AdamW", "params": {"lr": 1e-4, "betas": [0.9, 0.999],
+                                                                             "eps": 1e-8, "weight_decay": 0.01}},
+           "fp16": {"enabled": True, "loss_scale": 0, "initial_scale_power": 16, "loss_scale_window": 1000,
+                    "hysteresis": 2, "min_loss_scale": 1},
+           "zero_optimization": {"stage": 2}, "max_grad_norm": 1.0}
+    engine, log = _run_training(gpu, oracle, cfg, steps=6)
+    assert engine.global_steps == 6
+    assert all(math.isfinite(l) for _, _, l in log)
+
+
+def test_engine_bf16_two_groups_with_scheduler(gpu, oracle):
+    import torch
+    _say("engine bf16 groups")
+
+    def groups(model):
+        decay = [p for n, p in model.named_parameters() if n.endswith("weight")]
+        no_decay = [p for n, p in model.named_parameters() if n.endswith("bias")]
+        return [{"params": decay, "weight_decay": 0.1}, {"params": no_decay, "weight_decay": 0.0, "lr": 5e-4}]
+
+    cfg = {"optimizer": {"type": "AdamW", "params": {"lr": 3e-4, "betas": [0.9, 0.95], "eps": 1e-8,
+                                                     "weight_decay": 0.1}},
+           "bf16": {"enabled": True}, "max_grad_norm": 0.5}
+    engine, log = _run_training(gpu, oracle, cfg, steps=5, groups=groups)
+    base = engine.optimizer.base_optimizer
+    assert len(base.param_groups) == 2 and base.param_groups[1]["lr"] == 5e-4
+    assert base.flat.param16.dtype == torch.bfloat16
+
+
+def test_engine_fp32_no_mixed_precision(gpu, oracle):
+    import torch
+    _say("engine fp32")
+    cfg = {"optimizer": {"type": "AdamW", "params": {"lr": 1e-3}}, "max_grad_norm": 0.0}
+    engine, _ = _run_training(gpu, oracle, cfg, steps=4)
+    base = engine.optimizer.base_optimizer
+    assert base.flat.param16 is None and base.flat.grad.dtype == torch.float32
+    # the model's parameters are the fp32 master itself
+    p0 = next(engine.module.parameters())
+    assert base.flat.master.data_ptr() <= p0.data_ptr() < base.flat.master.data_ptr() + 4 * base.flat.numel
+
+
+def test_autograd_accumulates_into_flat_grad_buffer(gpu):
+    import torch
+    import distributedspeed_amd as ds
+    model = _mlp(1)
+    engine, opt, _, _ = ds.initialize(model, {"fp16": {"enabled": True}})
+    flat = opt.base_optimizer.flat
+    x = torch.randn(8, 784, device=gpu)
+    engine.backward(engine(x).float().pow(2).mean())
+    lo, hi = flat.grad.data_ptr(), flat.grad.data_ptr() + 2 * flat.numel
+    for p in engine.module.parameters():
+        assert p.grad is not None and lo <= p.grad.data_ptr() < hi
+    assert float(flat.grad.float().abs().sum()) > 0
+
+
+def test_gradient_accumulation(gpu, oracle):
+    """Two micro-batches accumulate into the 16-bit grads; one step."""
+    import torch
+    import distributedspeed_amd as ds
+    cfg = {"bf16": {"enabled": True}, "gradient_accumulation_steps": 2, "max_grad_norm": 0.0,
+           "optimizer": {"params": {"lr": 1e-3}}}
+    engine, opt, _, _ = ds.initialize(_mlp(2), cfg)
+    base = opt.base_optimizer
+    p_before = base.flat.master.clone()
+    x1, x2 = torch.randn(16, 784, device=gpu), torch.randn(16, 784, device=gpu)
+    engine.backward(engine(x1).float().pow(2).mean())
+    engine.step()  # not a boundary: no update
+    assert torch.equal(base.flat.master, p_before) and engine.global_steps == 0
+    engine.backward(engine(x2).float().pow(2).mean())
+    g = torch16_to_np(base.flat.grad).copy()
+    engine.step()
+    assert engine.global_steps == 1
+    assert float(base.flat.grad.float().abs().sum()) == 0.0  # zeroed after the boundary step
+    p, m, v = p_before.cpu().numpy(), np.zeros(base.flat.numel, np.float32), np.zeros(base.flat.numel, np.float32)
+    h = oracle.Hyper(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01)
+    oracle.adamw(p, m, v, None, BF16, g, BF16, oracle.step_scalars(h, 1, 1.0, 1.0))
+    assert np.array_equal(base.flat.master.cpu().numpy().view(np.uint32), p.view(np.uint32))
+
+
+def test_torch_adamw_is_adopted(gpu):
+    import torch
+    import distributedspeed_amd as ds
+    model = _mlp(3)
+    topt = torch.optim.AdamW(model.parameters(), lr=2e-4, betas=(0.8, 0.9), weight_decay=0.05)
+    engine, opt, _, _ = ds.initialize(model.cuda(), {"bf16": {"enabled": True}}, optimizer=topt)
+    g = opt.param_groups[0]
+    assert (g["lr"], tuple(g["betas"]), g["weight_decay"]) == (2e-4, (0.8, 0.9), 0.05)
+    with pytest.raises(NotImplementedError):
+        ds.initialize(_mlp(4), {}, optimizer=torch.optim.SGD(_mlp(4).parameters(), lr=0.1))
+
+
+def test_checkpoint_round_trip_is_bit_exact(gpu, tmp_path):
+    import torch
+    import distributedspeed_amd as ds
+    cfg = {"fp16": {"enabled": True, "hysteresis": 1}, "max_grad_norm": 1.0}
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(9)
+    data = [(torch.randn(16, 784, device=gpu, generator=gen), torch.randint(0, 10, (16,), device=gpu, generator=gen))
+            for _ in range(5)]
+
+    def train(engine, batches):
+        for x, y in batches:
+            engine.backward(torch.nn.functional.cross_entropy(engine(x).float(), y))
+            engine.step()
+
+    e1, _, _, _ = ds.initialize(_mlp(5), cfg)
+    train(e1, data[:3])
+    e1.save_checkpoint(str(tmp_path), client_state={"epoch": 1})
+    train(e1, data[3:])
+    e2, _, _, _ = ds.initialize(_mlp(6), cfg)  # different init: everything must come from the checkpoint
+    _, client = e2.load_checkpoint(str(tmp_path))
+    assert client == {"epoch": 1} and e2.global_steps == 3
+    train(e2, data[3:])
+    b1, b2 = e1.optimizer.base_optimizer, e2.optimizer.base_optimizer
+    for name in ("master", "exp_avg", "exp_avg_sq", "param16"):
+        assert torch.equal(getattr(b1.flat, name), getattr(b2.flat, name)), name
+    s1, s2 = b1.read_state(), b2.read_state()
+    assert (s1.scale, s1.t, s1.good_steps, s1.overflow_count) == (s2.scale, s2.t, s2.good_steps, s2.overflow_count)
+
+
+def test_initialize_refuses_multi_rank(gpu, monkeypatch):
+    import distributedspeed_amd as ds
+    monkeypatch.setenv("WORLD_SIZE", "2")
+    with pytest.raises(NotImplementedError):
+        ds.initialize(_mlp(7), {})

@@ -359,3 +359,102 @@ def test_host_rejects_bad_arguments(gpu):
     with pytest.raises(_lib.DsxError):  # the C layer's own check, reached directly
         _lib.call("dsx_adamw_flat", buf[1:].data_ptr(), tm.data_ptr(), tv.data_ptr(), None, 2, tg.data_ptr(), 2,
                   n, sc.data_ptr(), None)
+
+
+def test_k2_fp32_grads_bit_exact(gpu, oracle):
+    """fp32 training: fp32 grads, no 16-bit cast (the master is the param)."""
+    import torch
+    O = oracle
+    n = 100_003
+    rng = np.random.default_rng(31)
+    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    m = (rng.standard_normal(n) * 1e-4).astype(np.float32)
+    v = (np.abs(rng.standard_normal(n)) * 1e-6).astype(np.float32)
+    g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    g[:4] = [0.0, -0.0, 1e-40, 3.0e38]
+    sc = O.step_scalars(O.Hyper(lr=1e-3, weight_decay=0.02), 4, 1.0, 0.25)
+    from distributedspeed_amd import _lib, ops
+    c = _lib.DsxStepScalars()
+    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss"):
+        setattr(c, k, getattr(sc, k))
+    tp, tm, tv, tg = (f32_to_torch(a, gpu) for a in (p, m, v, g))
+    ops.adamw_flat(tp, tm, tv, None, tg, ops.scalars_from_host(c, gpu))
+    st = ops.new_state(gpu, 1.0, 1)
+    parts = torch.zeros(ops.suggest_partials(n), dtype=torch.float64, device=gpu)
+    ops.unscale_norm(tg, st, parts)
+    O.adamw(p, m, v, None, F16, g, O.F32, sc)
+    for a, b in ((tp, p), (tm, m), (tv, v)):
+        assert np.array_equal(a.cpu().numpy().view(np.uint32), b.view(np.uint32))
+    assert float(parts.sum().item()) == pytest.approx(O.sumsq(g, O.F32, 1.0), rel=1e-12)
+
+
+def test_finalize_groups_matches_oracle(gpu, oracle):
+    """Per-group scalars (lr, betas, eps, weight decay, t offset) from one
+    K0 launch; global norm, clip and scaler. Group 2 joined after step 2, so
+    it steps with t - 2."""
+    import torch
+    from distributedspeed_amd import _lib, ops
+    from distributedspeed_amd.flat_step import BiasCorrectionTable, ScalerConfig
+    O = oracle
+    hyps = [O.Hyper(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0),
+            O.Hyper(lr=5e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, max_grad_norm=1.0),
+            O.Hyper(lr=2e-4, beta1=0.8, beta2=0.95, eps=1e-6, weight_decay=0.05, max_grad_norm=1.0)]
+    offs = [0, 0, 2]
+    host = _lib.DsxState()
+    host.scale, host.hyst_left, host.t = 8.0, 1, 2
+    st = torch.frombuffer(bytearray(bytes(host)), dtype=torch.uint8).to(gpu)
+    tabs = [BiasCorrectionTable(gpu, h.beta1, h.beta2) for h in hyps]
+    out = torch.zeros(ops.SCALARS_BYTES * 3, dtype=torch.uint8, device=gpu)
+    parts = torch.tensor([4.0, 5.0, 7.0], dtype=torch.float64, device=gpu)  # sumsq 16 -> norm 4 -> clipped
+    cfg = ScalerConfig(mode="static", init_scale=8.0).to_c()
+    hc = [_lib.DsxAdamwHyper(h.lr, h.beta1, h.beta2, h.eps, h.weight_decay, h.max_grad_norm, h.clip_eps)
+          for h in hyps]
+    for t in range(3, 7):
+        ops.finalize_groups(parts, 3, st, cfg, hc, [x.table for x in tabs], offs, tabs[0].length, out)
+        s = ops.read_state(st)
+        assert s.error == 0 and s.t == t and s.scale == 8.0
+        for k, h in enumerate(hyps):
+            got = ops.read_scalars(out[k * ops.SCALARS_BYTES:(k + 1) * ops.SCALARS_BYTES])
+            ref = O.step_scalars(h, t - offs[k], O.inv_scale_of(8.0), O.clip_coef(4.0, 1.0))
+            assert got.skip == 0 and got.t == t - offs[k]
+            assert got.norm == 4.0
+            for name in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss"):
+                assert np.float32(getattr(got, name)) == np.float32(getattr(ref, name)), (t, k, name)
+    # an offset beyond the current step is an error: the step is skipped and flagged
+    ops.finalize_groups(parts, 3, st, cfg, hc, [x.table for x in tabs], [0, 0, 7], tabs[0].length, out)
+    s = ops.read_state(st)
+    assert s.error & _lib.DSX_STATE_ERR_BC_TABLE and s.t == 6
+    assert ops.read_scalars(out[:ops.SCALARS_BYTES]).skip == 1
+
+
+def test_multi_tensor_groups(gpu, oracle):
+    """K3 with two parameter groups: each tensor uses its group's scalars."""
+    import torch
+    from distributedspeed_amd import _lib, ops
+    O = oracle
+    sizes = [1000, 4096, 7, 20000]
+    groups = [0, 1, 0, 1]
+    hyps = [O.Hyper(lr=1e-3, weight_decay=0.1), O.Hyper(lr=3e-3, beta1=0.5, beta2=0.9, weight_decay=0.0)]
+    t = 2
+    arrs = [make_state(s, 40 + i, BF16, 1e-3, edges=False) for i, s in enumerate(sizes)]
+    tens = [[f32_to_torch(a[j], gpu) for j in range(3)] for a in arrs]
+    tg = [np16_to_torch(a[3], BF16, gpu) for a in arrs]
+    tp16 = [torch.empty(s, dtype=torch.bfloat16, device=gpu) for s in sizes]
+    table = ops.ChunkTable([x[0] for x in tens], [x[1] for x in tens], [x[2] for x in tens], tp16, tg,
+                           groups=groups, chunk_elems=1024)
+    scal = torch.zeros(2 * ops.SCALARS_BYTES, dtype=torch.uint8, device=gpu)
+    for k, h in enumerate(hyps):
+        sc = O.step_scalars(h, t, 1.0, 1.0)
+        c = _lib.DsxStepScalars()
+        for f in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss"):
+            setattr(c, f, getattr(sc, f))
+        scal[k * ops.SCALARS_BYTES:(k + 1) * ops.SCALARS_BYTES] = ops.scalars_from_host(c, gpu)
+    ops.adamw_multi(table, scal)
+    torch.cuda.synchronize()
+    for i, (p, m, v, g16) in enumerate(arrs):
+        p16 = np.empty(p.size, np.uint16)
+        O.adamw(p, m, v, p16, BF16, g16, BF16, O.step_scalars(hyps[groups[i]], t, 1.0, 1.0))
+        assert np.array_equal(tens[i][0].cpu().numpy().view(np.uint32), p.view(np.uint32)), i
+        assert np.array_equal(tens[i][1].cpu().numpy().view(np.uint32), m.view(np.uint32)), i
+        assert np.array_equal(tens[i][2].cpu().numpy().view(np.uint32), v.view(np.uint32)), i
+        assert np.array_equal(torch16_to_np(tp16[i]), p16), i
