@@ -355,7 +355,7 @@ def test_host_rejects_bad_arguments(gpu):
     with pytest.raises(ValueError):
         ops.adamw_flat(torch.zeros(n + 1, device=gpu), tm, tv, None, tg, sc)
     with pytest.raises(TypeError):
-        ops.adamw_flat(buf[:n], tm, tv, None, tg.float(), sc)
+        ops.adamw_flat(buf[:n], tm, tv, None, tg.to(torch.int16), sc)
     with pytest.raises(_lib.DsxError):  # the C layer's own check, reached directly
         _lib.call("dsx_adamw_flat", buf[1:].data_ptr(), tm.data_ptr(), tv.data_ptr(), None, 2, tg.data_ptr(), 2,
                   n, sc.data_ptr(), None)
