@@ -40,6 +40,9 @@ def _args():
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                       "k2_adamw_flat_llama8b_shard_traffic.json"))
     ap.add_argument("--tuning", default="", help="k1_bpc,k2_bpc,k2_unroll,nt (library launch-shape override)")
+    ap.add_argument("--workload", default="llama8b-shard", choices=["llama8b-shard", "llama-ragged"],
+                    help="llama8b-shard: the headline flat step (K1/K0/K2); llama-ragged: configs[3]'s 289-tensor "
+                         "list through K3 (a secondary line, not the headline)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="for rocprofv3 --pmc runs: launch K1, K0, K2 three times each and one 1 GiB fp32 "
                          "copy (the byte-counter calibration), then exit without timing")
@@ -94,6 +97,91 @@ def make_inputs(n: int, seed: int, device):
     exp_avg_sq = torch.zeros(n, dtype=torch.float32, device=device)
     p16 = master.to(torch.bfloat16)
     return master, exp_avg, exp_avg_sq, p16, grad
+
+
+def llama_ragged_shapes():
+    """32 x (4096^2 x4, 4096x14336 x2, 14336x4096, 4096 x2) +
+    128256x4096 -- 289 tensors, 8,310,226,944 elements."""
+    shapes = []
+    for _ in range(32):
+        shapes += [(4096, 4096)] * 4 + [(4096, 14336)] * 2 + [(14336, 4096)] + [(4096,)] * 2
+    shapes.append((128256, 4096))
+    return shapes
+
+
+def bench_ragged(a, dev) -> int:
+    """configs[3] through K3: fp16 grads N(0, 1e-3^2) x 2^16, dynamic scaler
+    (init 2^16, window 1000, hysteresis 2, min 1), AdamW defaults, clip 1.0.
+    One step = K1 over the chunk table, K0, K3 (three launches)."""
+    import math
+
+    import torch
+    from distributedspeed_amd import ops
+    from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
+    sizes = [math.prod(s) for s in llama_ragged_shapes()]
+    n = sum(sizes)
+    _progress(f"allocating {len(sizes)} tensors / {n} elements")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    ts = []
+    for k in sizes:
+        p = torch.empty(k, device=dev).normal_(0.0, 0.02, generator=gen)
+        g = torch.empty(k, device=dev).normal_(0.0, 1e-3, generator=gen).mul_(2.0 ** 16).to(torch.float16)
+        ts.append((p, torch.zeros(k, device=dev), torch.zeros(k, device=dev), p.to(torch.float16), g))
+    table = ops.ChunkTable(*[[t[j] for t in ts] for j in range(5)])
+    hyper = AdamWHyper(lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, max_grad_norm=1.0)
+    scfg = ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, window=1000, hysteresis=2, min_scale=1.0)
+    bc = BiasCorrectionTable(dev, hyper.beta1, hyper.beta2, capacity=a.warmup + 3 * a.steps + 8)
+    st = ops.new_state(dev, scfg.init_scale, scfg.hysteresis)
+    nparts = ops.suggest_partials(n)
+    parts = torch.zeros(nparts, dtype=torch.float64, device=dev)
+    out = ops.new_scalars(dev)
+    hc, sc = hyper.to_c(), scfg.to_c()
+
+    def step(ev=None):
+        if ev:
+            ev[0].record()
+        ops.unscale_norm_multi(table, st, parts, nparts)
+        if ev:
+            ev[1].record()
+        ops.finalize(parts, nparts, st, sc, hc, bc.table, bc.length, out)
+        if ev:
+            ev[2].record()
+        ops.adamw_multi(table, out)
+        if ev:
+            ev[3].record()
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record()
+    for _ in range(a.steps):
+        step()
+    s1.record()
+    torch.cuda.synchronize()
+    ms = s0.elapsed_time(s1) / a.steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    k1 = sum(e[0].elapsed_time(e[1]) for e in evs) / a.steps
+    k3 = sum(e[2].elapsed_time(e[3]) for e in evs) / a.steps
+    s = ops.read_state(st)
+    if s.error or s.last_skip:
+        print(json.dumps({"error": f"state error={s.error} skip={s.last_skip}"}))
+        return 1
+    print(json.dumps({
+        "metric": "ragged multi-tensor ZeRO step Gparam/s (configs[3], K3)", "value": round(n / ms / 1e6, 3),
+        "unit": "Gparam/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "dtype": "f32 state / fp16 grads+params", "data": "synthetic",
+        "config": {"workload": "llama ragged list (BASELINE configs[3])", "tensors": len(sizes), "numel": n,
+                   "chunks": table.nchunks},
+        "achieved_tbps_end_to_end": round(30 * n / ms / 1e9, 4),
+        "kernels_ms": {"k1_unscale_norm_multi": round(k1, 4), "k2_adamw_multi": round(k3, 4)},
+        "k3_gbs": round(28 * n / k3 / 1e6, 1), "k3_frac_of_8tbs": round(28 * n / k3 / 1e6 / HBM_PEAK_GBS, 4),
+    }), flush=True)
+    return 0
 
 
 def cpu_baseline(n_sample: int, hyper) -> dict | None:
@@ -181,6 +269,8 @@ def main() -> int:
     n = int(a.numel)
     if a.profile_kernels:
         return profile_kernels(n, dev)
+    if a.workload == "llama-ragged":
+        return bench_ragged(a, dev)
     hyper = AdamWHyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     _progress(f"generating {n} elements")
     master, exp_avg, exp_avg_sq, p16, grad = make_inputs(n, 2, dev)
