@@ -40,7 +40,7 @@ def _args():
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                       "k2_adamw_flat_llama8b_shard_traffic.json"))
     ap.add_argument("--tuning", default="", help="k1_bpc,k2_bpc,k2_unroll,nt (library launch-shape override)")
-    ap.add_argument("--workload", default="llama8b-shard", choices=["llama8b-shard", "llama-ragged"],
+    ap.add_argument("--workload", default="llama8b-shard", choices=["llama8b-shard", "llama-ragged", "llama70b-offload"],
                     help="llama8b-shard: the headline flat step (K1/K0/K2); llama-ragged: configs[3]'s 289-tensor "
                          "list through K3 (a secondary line, not the headline)")
     ap.add_argument("--profile-kernels", action="store_true",
@@ -184,6 +184,79 @@ def bench_ragged(a, dev) -> int:
     return 0
 
 
+def bench_offload(a, dev) -> int:
+    """Llama-3-70B ZeRO-3 one-rank shard, 8,819,213,312 elements,
+    fp32 master/m/v in pinned host memory (105.8 GB) streamed through HBM in
+    64 Mi-element chunks, bf16 grads N(0, 3e-4^2) and params in HBM; AdamW lr
+    1.5e-4, betas (0.9, 0.95), wd 0.1. Bound by the host link (12 B/elt each
+    way), so the figure of merit is link GB/s against the measured link
+    ceiling, not HBM TB/s."""
+    import torch
+    from distributedspeed_amd import ops
+    from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
+    from distributedspeed_amd.offload import HostStateStreamer, measure_link, pinned_zeros
+    n = int(a.numel) if a.numel != HEADLINE_NUMEL else 8_819_213_312
+    chunk = 64 << 20
+    _progress("measuring the host link")
+    link = measure_link(dev)
+    _progress(f"link {link}; allocating {n} elements of pinned state")
+    master, m, v = pinned_zeros(n), pinned_zeros(n), pinned_zeros(n)
+    grad = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    p16 = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    tmp = torch.empty(chunk, device=dev)
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        tmp[:e - s].normal_(0.0, 0.02, generator=gen)
+        master[s:e].copy_(tmp[:e - s])
+        p16[s:e].copy_(tmp[:e - s])
+        grad[s:e].copy_(tmp[:e - s].normal_(0.0, 3e-4, generator=gen))
+        if (s // chunk) % 16 == 0:
+            _progress(f"filled {e}/{n}")
+    del tmp
+    torch.cuda.synchronize()
+    hyper = AdamWHyper(lr=1.5e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    scfg = ScalerConfig(mode="none")
+    bc = BiasCorrectionTable(dev, hyper.beta1, hyper.beta2)
+    st = ops.new_state(dev, 1.0, 1)
+    nparts = ops.suggest_partials(n)
+    parts = torch.zeros(nparts, dtype=torch.float64, device=dev)
+    out = ops.new_scalars(dev)
+    streamer = HostStateStreamer(dev, chunk)
+    steps = max(1, min(a.steps, 3))
+
+    def step():
+        ops.unscale_norm(grad, st, parts, nparts)
+        ops.finalize(parts, nparts, st, scfg.to_c(), hyper.to_c(), bc.table, bc.length, out)
+        streamer.run((master, m, v), p16, grad, [(0, n, out)])
+
+    _progress("warmup step")
+    step()
+    torch.cuda.synchronize()
+    times = []
+    for i in range(steps):
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        _progress(f"step {i + 1}: {times[-1]:.3f} s")
+    s = ops.read_state(st)
+    sec = sorted(times)[len(times) // 2]
+    each_way = 12 * n / sec / 1e9
+    print(json.dumps({
+        "metric": "offloaded ZeRO step (configs[4]): Gparam/s and host-link GB/s each way",
+        "value": round(n / sec / 1e9, 4), "unit": "Gparam/s", "n_gpus": 1, "steps": steps, "warmup": 1,
+        "ms_per_step": round(sec * 1e3, 1), "higher_is_better": True, "dtype": "f32 state (host) / bf16 grads+params",
+        "data": "synthetic", "config": {"workload": "llama3-70b zero3 one-rank shard, state offloaded "
+                                                    "(BASELINE configs[4])", "numel": n, "chunk_elems": chunk},
+        "link_gbs_each_way": round(each_way, 2), "link_ceiling_gbs": {k: round(x, 2) for k, x in link.items()},
+        "frac_of_measured_bidirectional_link": round(each_way / link["both_each_way"], 4),
+        "state_t": s.t, "skipped": s.last_skip,
+    }), flush=True)
+    return 0
+
+
 def cpu_baseline(n_sample: int, hyper) -> dict | None:
     """The C oracle (a CPU port of the step) on a bounded sample, on this
     host's cores; plus torch.optim.AdamW on CPU (the reference's cpu_offload
@@ -271,6 +344,8 @@ def main() -> int:
         return profile_kernels(n, dev)
     if a.workload == "llama-ragged":
         return bench_ragged(a, dev)
+    if a.workload == "llama70b-offload":
+        return bench_offload(a, dev)
     hyper = AdamWHyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     _progress(f"generating {n} elements")
     master, exp_avg, exp_avg_sq, p16, grad = make_inputs(n, 2, dev)

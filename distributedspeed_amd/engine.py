@@ -45,9 +45,6 @@ class DistributedSpeedEngine(torch.nn.Module):
                  optimizer: Optional[torch.optim.Optimizer] = None, lr_scheduler=None,
                  model_parameters=None, device: Optional[torch.device] = None):
         super().__init__()
-        if config.zero_optimization.cpu_offload:
-            raise NotImplementedError("zero_optimization.cpu_offload: the host-resident optimizer state path is "
-                                      "not built in this version; run with optimizer state in HBM")
         self.config = config
         self.device = device or torch.device("cuda", torch.cuda.current_device())
         self.module = model.to(self.device)
@@ -56,7 +53,8 @@ class DistributedSpeedEngine(torch.nn.Module):
         scaler = ScalerConfig(**config.loss_scaler())
         names = {id(p): n for n, p in self.module.named_parameters()}
         common = dict(max_grad_norm=float(config.max_grad_norm or 0), param_dtype=self.param_dtype,
-                      loss_scaler=scaler, device=self.device, param_names=names)
+                      loss_scaler=scaler, device=self.device, param_names=names,
+                      offload=bool(config.zero_optimization.cpu_offload))
         if optimizer is not None:
             if not isinstance(optimizer, AdamWOptimizer):
                 optimizer = adopt_torch_optimizer(optimizer, **common)

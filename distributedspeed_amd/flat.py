@@ -13,7 +13,11 @@ built once and the copies disappear:
   exp_avg, exp_avg_sq      n x fp32
 
 With fp32 training there is no param16: param.data are views of master and
-grads are fp32. Parameters are laid out group by group in model order; every
+grads are fp32. With `offload=True` master / exp_avg / exp_avg_sq are pinned
+host tensors instead (the step streams them through HBM; param16 and grad
+stay in HBM), which needs a 16-bit param dtype.
+
+Parameters are laid out group by group in model order; every
 parameter (and so every group) starts on an 8-element boundary, so each
 group's range is 16-byte aligned in every buffer. Padding elements have zero
 grad and zero master and stay zero under AdamW.
@@ -42,13 +46,17 @@ class Slot:
 
 class FlatPartition:
     def __init__(self, groups: list[list[torch.nn.Parameter]], device: torch.device,
-                 param_dtype: torch.dtype | None, names: dict | None = None):
+                 param_dtype: torch.dtype | None, names: dict | None = None, offload: bool = False):
         """groups: parameter lists (one per optimizer param group).
         param_dtype: torch.float16 / torch.bfloat16 for mixed precision, None
         for fp32 training."""
         if param_dtype not in (None, torch.float16, torch.bfloat16):
             raise ValueError(f"param_dtype must be float16, bfloat16 or None, got {param_dtype}")
+        if offload and param_dtype is None:
+            raise ValueError("offloaded optimizer state needs fp16 or bf16 parameters (fp32 params would have to "
+                             "live in host memory)")
         names = names or {}
+        self.offload = bool(offload)
         self.device = torch.device(device)
         self.param_dtype = param_dtype
         self.grad_dtype = param_dtype or torch.float32
@@ -70,38 +78,48 @@ class FlatPartition:
             self.group_ranges.append((start, off))
         self.numel = off
         dev = self.device
-        self.master = torch.zeros(self.numel, dtype=torch.float32, device=dev)
-        self.exp_avg = torch.zeros(self.numel, dtype=torch.float32, device=dev)
-        self.exp_avg_sq = torch.zeros(self.numel, dtype=torch.float32, device=dev)
+        if self.offload:
+            self.master, self.exp_avg, self.exp_avg_sq = (
+                torch.zeros(self.numel, dtype=torch.float32, pin_memory=True) for _ in range(3))
+        else:
+            self.master, self.exp_avg, self.exp_avg_sq = (
+                torch.zeros(self.numel, dtype=torch.float32, device=dev) for _ in range(3))
         self.grad = torch.zeros(self.numel, dtype=self.grad_dtype, device=dev)
         self.param16 = torch.zeros(self.numel, dtype=param_dtype, device=dev) if param_dtype else None
         with torch.no_grad():
             for s, p in zip(self.slots, self.params):
-                self.master[s.offset:s.offset + s.numel].copy_(p.detach().reshape(-1).to(dev, torch.float32))
-            if self.param16 is not None:
+                src = p.detach().reshape(-1)
+                self.master[s.offset:s.offset + s.numel].copy_(src.to(self.master.device, torch.float32))
+                if self.offload:
+                    self.param16[s.offset:s.offset + s.numel].copy_(src.to(dev, torch.float32))
+            if self.param16 is not None and not self.offload:
                 self.param16.copy_(self.master)  # round to nearest even
         self.rebind()
 
     def rebind(self) -> None:
         """Point every param.data / param.grad at its view of the flat buffers."""
         home = self.param16 if self.param16 is not None else self.master
+        self._grad_views = []
         for s, p in zip(self.slots, self.params):
             p.data = home[s.offset:s.offset + s.numel].view(s.shape)
-            p.grad = self.grad[s.offset:s.offset + s.numel].view(s.shape)
+            gv = self.grad[s.offset:s.offset + s.numel].view(s.shape)
+            p.grad = gv
+            self._grad_views.append(gv)
 
     def check_grads_bound(self) -> None:
-        """Autograd accumulates into an existing .grad in place; if something
-        replaced a param's .grad with a new tensor, copy it into the flat
-        buffer and restore the view."""
-        for s, p in zip(self.slots, self.params):
+        """Autograd accumulates into an existing .grad in place, so p.grad stays
+        the view rebind() set. If something replaced it (set it to None or to
+        a new tensor), copy that into the flat buffer and restore the view."""
+        for i, (s, p) in enumerate(zip(self.slots, self.params)):
             g = p.grad
-            view = self.grad[s.offset:s.offset + s.numel]
+            view = self._grad_views[i]
+            if g is view:
+                continue
             if g is None:
                 view.zero_()
-                p.grad = view.view(s.shape)
             elif g.data_ptr() != view.data_ptr():
-                view.copy_(g.reshape(-1))
-                p.grad = view.view(s.shape)
+                view.copy_(g)
+            p.grad = view
 
     def group_views(self, gi: int):
         a, b = self.group_ranges[gi]

@@ -1,0 +1,118 @@
+"""Optimizer state offloaded to pinned host memory.
+
+The reference's `cpu_offload` parks optimizer state on the host and copies
+all of it back to the GPU before stepping (Src/zero/stage1.py:376-398,
+482-498; Src/zero/stage2.py:432-454, 563-582), and ZeRO-3 keeps a pinned-host
+tier (Src/zero/stage3.py:881-898, 1189-1207). Here the fp32 master /
+exp_avg / exp_avg_sq live in pinned host memory for good; the 16-bit params
+and grads stay in HBM. A step is
+
+    K1 over the device grads -> K0 -> (host reads the skip flag: one sync)
+    for each chunk k of every parameter group's range:
+        copy stream in :  state[k] host -> staging[k % nbuf]     (hipMemcpyAsync)
+        compute stream :  K2 on staging[k % nbuf] + grad/param16 views
+        copy stream out:  staging[k % nbuf] -> state[k] host
+
+with events so that chunk k+1 is copied in and chunk k-1 copied out while
+chunk k computes. The host link, not HBM, bounds it: 12 B/elt each way.
+All streams have the default priority.
+"""
+from __future__ import annotations
+
+import time
+
+import torch
+
+from . import ops
+
+
+class HostStateStreamer:
+    def __init__(self, device: torch.device, chunk_elems: int = 64 << 20, nbuf: int = 3):
+        if chunk_elems <= 0 or chunk_elems % 8:
+            raise ValueError("chunk_elems must be a positive multiple of 8")
+        if nbuf < 2:
+            raise ValueError("nbuf must be >= 2")
+        self.device = torch.device(device)
+        self.chunk = int(chunk_elems)
+        self.nbuf = int(nbuf)
+        self.stage = [[torch.empty(self.chunk, dtype=torch.float32, device=self.device) for _ in range(3)]
+                      for _ in range(self.nbuf)]
+        self.s_in = torch.cuda.Stream(self.device)
+        self.s_out = torch.cuda.Stream(self.device)
+        self.ev_in = [torch.cuda.Event() for _ in range(self.nbuf)]
+        self.ev_done = [torch.cuda.Event() for _ in range(self.nbuf)]
+        self.ev_out = [torch.cuda.Event() for _ in range(self.nbuf)]
+        self.last_bytes = 0
+        self.last_seconds = 0.0
+
+    def run(self, host_state: tuple[torch.Tensor, torch.Tensor, torch.Tensor], param16: torch.Tensor | None,
+            grad: torch.Tensor, pieces: list[tuple[int, int, torch.Tensor]]) -> None:
+        """pieces: (start, end, scalars) ranges of the flat partition, each
+        with the DsxStepScalars (device uint8[64]) of its parameter group."""
+        compute = torch.cuda.current_stream(self.device)
+        # Everything earlier on the compute stream (K0, the previous step's
+        # K2s) and every earlier copy out is ordered before this step's copies.
+        self.s_in.wait_stream(compute)
+        self.s_in.wait_stream(self.s_out)
+        k = 0
+        moved = 0
+        for a, b, scal in pieces:
+            for s in range(a, b, self.chunk):
+                e = min(b, s + self.chunk)
+                n = e - s
+                slot = k % self.nbuf
+                st = [t[:n] for t in self.stage[slot]]
+                with torch.cuda.stream(self.s_in):
+                    if k >= self.nbuf:
+                        self.s_in.wait_event(self.ev_out[slot])
+                    for dst, src in zip(st, host_state):
+                        dst.copy_(src[s:e], non_blocking=True)
+                    self.ev_in[slot].record(self.s_in)
+                compute.wait_event(self.ev_in[slot])
+                ops.adamw_flat(st[0], st[1], st[2], param16[s:e] if param16 is not None else None, grad[s:e], scal)
+                self.ev_done[slot].record(compute)
+                with torch.cuda.stream(self.s_out):
+                    self.s_out.wait_event(self.ev_done[slot])
+                    for dst, src in zip(host_state, st):
+                        dst[s:e].copy_(src, non_blocking=True)
+                    self.ev_out[slot].record(self.s_out)
+                moved += 24 * n
+                k += 1
+        # the step is complete, in stream order, once the last copy out is
+        compute.wait_stream(self.s_out)
+        self.last_bytes = moved
+
+
+def pinned_zeros(n: int) -> torch.Tensor:
+    return torch.zeros(n, dtype=torch.float32, pin_memory=True)
+
+
+def measure_link(device: torch.device, nbytes: int = 1 << 30) -> dict:
+    """Plain pinned-host <-> HBM copy bandwidth (GB/s), one direction at a
+    time and both at once: the ceiling the streamed step is compared to."""
+    n = nbytes // 4
+    h1 = torch.empty(n, dtype=torch.float32, pin_memory=True)
+    h2 = torch.empty(n, dtype=torch.float32, pin_memory=True)
+    d1 = torch.empty(n, dtype=torch.float32, device=device)
+    d2 = torch.empty(n, dtype=torch.float32, device=device)
+    s1, s2 = torch.cuda.Stream(device), torch.cuda.Stream(device)
+    out = {}
+    for name, fn in (("h2d", lambda: d1.copy_(h1, non_blocking=True)),
+                     ("d2h", lambda: h2.copy_(d2, non_blocking=True))):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        out[name] = 3 * nbytes / (time.perf_counter() - t0) / 1e9
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            d1.copy_(h1, non_blocking=True)
+        with torch.cuda.stream(s2):
+            h2.copy_(d2, non_blocking=True)
+    torch.cuda.synchronize()
+    out["both_each_way"] = 3 * nbytes / (time.perf_counter() - t0) / 1e9
+    return out

@@ -27,13 +27,14 @@ from . import ops
 from ._lib import DSX_MAX_GROUPS, DsxAdamwHyper
 from .flat import FlatPartition
 from .flat_step import BiasCorrectionTable, ScalerConfig
+from .offload import HostStateStreamer
 
 
 class AdamWOptimizer(torch.optim.Optimizer):
     def __init__(self, params: Iterable, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
                  weight_decay: float = 1e-2, *, max_grad_norm: float = 0.0, param_dtype: torch.dtype | None = None,
                  loss_scaler: ScalerConfig | None = None, device: torch.device | None = None,
-                 param_names: dict | None = None):
+                 param_names: dict | None = None, offload: bool = False, offload_chunk_elems: int = 64 << 20):
         if not 0.0 <= lr:
             raise ValueError(f"Invalid learning rate: {lr}")
         if not 0.0 <= eps:
@@ -62,7 +63,9 @@ class AdamWOptimizer(torch.optim.Optimizer):
         self.clip_eps = 1e-6
         self.scaler = loss_scaler or ScalerConfig(mode="none")
         self.scaler.validate()
-        self.flat = FlatPartition([g["params"] for g in self.param_groups], self.device, param_dtype, param_names)
+        self.flat = FlatPartition([g["params"] for g in self.param_groups], self.device, param_dtype, param_names,
+                                  offload=offload)
+        self.streamer = HostStateStreamer(self.device, offload_chunk_elems) if offload else None
         self.nparts = ops.suggest_partials(self.flat.numel)
         self.partials = torch.zeros(self.nparts, dtype=torch.float64, device=self.device)
         self.dstate = ops.new_state(self.device, self.scaler.init_scale if self.scaler.mode != "none" else 1.0,
@@ -126,6 +129,15 @@ class AdamWOptimizer(torch.optim.Optimizer):
         ops.unscale_norm(self.flat.grad, self.dstate, self.partials, self.nparts)
         ops.finalize_groups(self.partials, self.nparts, self.dstate, self.scaler.to_c(), hs, tables,
                             self._t_offsets, bc_len, self.scalars)
+        if self.streamer is not None:
+            # State in pinned host memory: stream it through HBM chunk by chunk.
+            # A skipped step streams too (K2 leaves the chunks unchanged), which
+            # keeps the host free of any wait on the device.
+            pieces = [(a, b, self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES])
+                      for gi, (a, b) in enumerate(self.flat.group_ranges) if b > a]
+            self.streamer.run((self.flat.master, self.flat.exp_avg, self.flat.exp_avg_sq), self.flat.param16,
+                              self.flat.grad, pieces)
+            return
         for gi in range(len(self.param_groups)):
             master, m, v, p16, g = self.flat.group_views(gi)
             if master.numel() == 0:
@@ -198,9 +210,9 @@ class AdamWOptimizer(torch.optim.Optimizer):
                         if src.shape != views[key].shape:
                             raise ValueError(f"state for parameter {i} has shape {tuple(src.shape)}, "
                                              f"expected {tuple(views[key].shape)}")
-                        views[key].copy_(src.to(self.device, torch.float32))
+                        views[key].copy_(src.to(views[key].device, torch.float32))
             if self.flat.param16 is not None:
-                self.flat.param16.copy_(self.flat.master)
+                self.flat.param16.copy_(self.flat.master.to(self.device))
         dsx = state_dict.get("dsx")
         t = int(dsx["t"]) if dsx else int(max((float(v["step"]) for v in st.values()), default=0))
         from ._lib import DsxState
