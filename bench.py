@@ -195,12 +195,22 @@ def bench_offload(a, dev) -> int:
     from distributedspeed_amd import ops
     from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
     from distributedspeed_amd.offload import HostStateStreamer, measure_link, pinned_zeros
-    n = int(a.numel) if a.numel != HEADLINE_NUMEL else 8_819_213_312
+    full = int(a.numel) if a.numel != HEADLINE_NUMEL else 8_819_213_312
     chunk = 64 << 20
     _progress("measuring the host link")
     link = measure_link(dev)
-    _progress(f"link {link}; allocating {n} elements of pinned state")
-    master, m, v = pinned_zeros(n), pinned_zeros(n), pinned_zeros(n)
+    n = full
+    while True:
+        _progress(f"link {link}; allocating {n} elements of pinned state")
+        try:
+            master, m, v = pinned_zeros(n), pinned_zeros(n), pinned_zeros(n)
+            break
+        except MemoryError as e:
+            master = m = v = None
+            if n <= chunk:
+                raise
+            _progress(f"{e}; halving the shard")
+            n = (n // 2) // chunk * chunk
     grad = torch.empty(n, dtype=torch.bfloat16, device=dev)
     p16 = torch.empty(n, dtype=torch.bfloat16, device=dev)
     gen = torch.Generator(device=dev)
@@ -252,6 +262,9 @@ def bench_offload(a, dev) -> int:
                                                     "(BASELINE configs[4])", "numel": n, "chunk_elems": chunk},
         "link_gbs_each_way": round(each_way, 2), "link_ceiling_gbs": {k: round(x, 2) for k, x in link.items()},
         "frac_of_measured_bidirectional_link": round(each_way / link["both_each_way"], 4),
+        "reduced_from_numel": full if n != full else None,
+        "reduction_reason": ("pinned host memory on this machine is capped (hipHostMalloc fails beyond ~64 GiB in "
+                             "total); the full shard needs 12 B/elt pinned") if n != full else None,
         "state_t": s.t, "skipped": s.last_skip,
     }), flush=True)
     return 0

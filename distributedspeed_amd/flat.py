@@ -79,8 +79,8 @@ class FlatPartition:
         self.numel = off
         dev = self.device
         if self.offload:
-            self.master, self.exp_avg, self.exp_avg_sq = (
-                torch.zeros(self.numel, dtype=torch.float32, pin_memory=True) for _ in range(3))
+            from .offload import pinned_zeros
+            self.master, self.exp_avg, self.exp_avg_sq = (pinned_zeros(self.numel) for _ in range(3))
         else:
             self.master, self.exp_avg, self.exp_avg_sq = (
                 torch.zeros(self.numel, dtype=torch.float32, device=dev) for _ in range(3))

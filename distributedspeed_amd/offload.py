@@ -7,23 +7,66 @@ tier (Src/zero/stage3.py:881-898, 1189-1207). Here the fp32 master /
 exp_avg / exp_avg_sq live in pinned host memory for good; the 16-bit params
 and grads stay in HBM. A step is
 
-    K1 over the device grads -> K0 -> (host reads the skip flag: one sync)
+    K1 over the device grads -> K0 (skip decision stays on the device)
     for each chunk k of every parameter group's range:
         copy stream in :  state[k] host -> staging[k % nbuf]     (hipMemcpyAsync)
         compute stream :  K2 on staging[k % nbuf] + grad/param16 views
         copy stream out:  staging[k % nbuf] -> state[k] host
 
 with events so that chunk k+1 is copied in and chunk k-1 copied out while
-chunk k computes. The host link, not HBM, bounds it: 12 B/elt each way.
+chunk k computes; on a skipped step K2 leaves each chunk unchanged. The host
+link, not HBM, bounds it: 12 B/elt each way.
 All streams have the default priority.
 """
 from __future__ import annotations
 
+import ctypes
 import time
+import weakref
 
 import torch
 
 from . import ops
+
+_hip = None
+
+
+def _hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime torch already loaded (same soname, so the same copy)."""
+    global _hip
+    if _hip is None:
+        torch.cuda.init()
+        _hip = ctypes.CDLL("libamdhip64.so.7")
+        _hip.hipHostMalloc.restype = ctypes.c_int
+        _hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+        _hip.hipHostFree.restype = ctypes.c_int
+        _hip.hipHostFree.argtypes = [ctypes.c_void_p]
+    return _hip
+
+
+def pinned_empty(n: int) -> torch.Tensor:
+    """An fp32 CPU tensor of exactly n elements in pinned host memory from
+    hipHostMalloc, freed with hipHostFree when the last tensor or view using
+    it is released. (torch's pinned allocator rounds every request up to a
+    power of two, which doubles the footprint of a 35 GB state array.) Raises
+    MemoryError when the machine's pinned-memory limit is reached.
+
+    Lifetime: torch.from_numpy keeps the ndarray alive for as long as the
+    storage lives, the ndarray keeps the ctypes array alive, and the
+    finalizer on the ctypes array frees the memory."""
+    n = int(n)
+    if n == 0:
+        return torch.empty(0, dtype=torch.float32)
+    import numpy as np
+    hip = _hip_runtime()
+    ptr = ctypes.c_void_p()
+    rc = hip.hipHostMalloc(ctypes.byref(ptr), 4 * n, 0)
+    if rc != 0 or not ptr.value:
+        raise MemoryError(f"hipHostMalloc of {4 * n / 2**30:.1f} GiB failed (status {rc}): the pinned host memory "
+                          "this machine allows is exhausted")
+    buf = (ctypes.c_float * n).from_address(ptr.value)
+    weakref.finalize(buf, hip.hipHostFree, ptr.value)
+    return torch.from_numpy(np.ctypeslib.as_array(buf))
 
 
 class HostStateStreamer:
@@ -84,15 +127,17 @@ class HostStateStreamer:
 
 
 def pinned_zeros(n: int) -> torch.Tensor:
-    return torch.zeros(n, dtype=torch.float32, pin_memory=True)
+    t = pinned_empty(n)
+    t.zero_()
+    return t
 
 
 def measure_link(device: torch.device, nbytes: int = 1 << 30) -> dict:
     """Plain pinned-host <-> HBM copy bandwidth (GB/s), one direction at a
     time and both at once: the ceiling the streamed step is compared to."""
     n = nbytes // 4
-    h1 = torch.empty(n, dtype=torch.float32, pin_memory=True)
-    h2 = torch.empty(n, dtype=torch.float32, pin_memory=True)
+    h1 = pinned_empty(n)
+    h2 = pinned_empty(n)
     d1 = torch.empty(n, dtype=torch.float32, device=device)
     d2 = torch.empty(n, dtype=torch.float32, device=device)
     s1, s2 = torch.cuda.Stream(device), torch.cuda.Stream(device)
