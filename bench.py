@@ -259,6 +259,7 @@ def bench_offload(a, dev) -> int:
                                                     "(BASELINE configs[4])", "numel": n, "chunk_elems": chunk},
         "link_gbs_each_way": round(each_way, 2), "link_ceiling_gbs": {k: round(x, 2) for k, x in link.items()},
         "frac_of_measured_bidirectional_link": round(each_way / link["both_each_way"], 4),
+        "frac_of_one_direction_link": round(each_way / min(link["h2d"], link["d2h"]), 4),
         "reduced_from_numel": full if n != full else None,
         "reduction_reason": (f"pinned budget {a.pinned_budget_gib} GiB: this machine caps GPU-visible pinned host "
                              "memory (no single hipHostMalloc above 32 GiB, ~64 GiB in total); the full shard needs "
