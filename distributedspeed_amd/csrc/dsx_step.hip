@@ -468,9 +468,20 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorR
     const int64_t len = ch.len;
     int64_t done = 0;
     if (aligned16(g)) {
+      // four 16-byte nontemporal loads in flight per thread before any use
+      constexpr int U = 4;
       const u4* g16 = reinterpret_cast<const u4*>(g);
       const int64_t nvec = len / G::per16;
-      for (int64_t i = threadIdx.x; i < nvec; i += kBlock) acc = G::sumsq16(g16[i], inv, acc);
+      for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += kBlock * U) {
+        u4 S[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t i = i0 + (int64_t)u * kBlock;
+          S[u] = (i < nvec) ? ld<true>(g16 + i) : u4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc = G::sumsq16(S[u], inv, acc);
+      }
       done = nvec * G::per16;
     }
     for (int64_t e = done + threadIdx.x; e < len; e += kBlock) {
@@ -513,6 +524,8 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __r
       u2* o2 = reinterpret_cast<u2*>(p16);
       const GS* g4 = reinterpret_cast<const GS*>(g);
       const int64_t nvec = len >> 2;
+      // plain loads/stores: on the 8.3e9-element ragged list nontemporal
+      // hints measured ~5% slower here
       for (int64_t i = threadIdx.x; i < nvec; i += kBlock) {
         float gf[4];
         G::four(g4[i], gf);
