@@ -1,0 +1,207 @@
+"""Host-side logic without a GPU: ds_config parsing (mirroring
+Src/config.py's defaults, deep merge, unknown-key TypeError, validation
+messages and env overrides), the flat partition layout (on CPU tensors), the
+bias-correction table, the loss-scaler mapping and the ops' argument checks."""
+from __future__ import annotations
+
+import json
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from distributedspeed_amd import config as C
+from distributedspeed_amd.flat import ALIGN, FlatPartition
+from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
+
+
+# ---- ds_config ------------------------------------------------------------------------
+
+def test_defaults_match_reference():
+    c = C.DistributedSpeedConfig()
+    assert c.max_grad_norm == 1.0 and c.gradient_accumulation_steps == 1 and c.train_batch_size == 32
+    assert c.adamw_params() == {"lr": 1e-4, "betas": (0.9, 0.999), "eps": 1e-8, "weight_decay": 0.01}
+    assert (c.fp16.loss_scale, c.fp16.initial_scale_power, c.fp16.loss_scale_window, c.fp16.hysteresis,
+            c.fp16.min_loss_scale) == (0.0, 16, 1000, 2, 1.0)
+    assert c.zero_optimization.stage == 0 and c.zero_optimization.contiguous_gradients
+    assert c.precision == "fp32" and c.loss_scaler() == {"mode": "none", "init_scale": 1.0}
+
+
+def test_deep_merge_keeps_unspecified_params():
+    c = C.DistributedSpeedConfig({"optimizer": {"params": {"lr": 3e-4, "betas": [0.9, 0.95]}}})
+    assert c.adamw_params() == {"lr": 3e-4, "betas": (0.9, 0.95), "eps": 1e-8, "weight_decay": 0.01}
+
+
+def test_loss_scaler_mapping():
+    dyn = C.DistributedSpeedConfig(C.fp16_config()).loss_scaler()
+    assert dyn == {"mode": "dynamic", "init_scale": 65536.0, "window": 1000, "hysteresis": 2, "min_scale": 1.0}
+    static = C.DistributedSpeedConfig({"fp16": {"enabled": True, "loss_scale": 128}}).loss_scaler()
+    assert static == {"mode": "static", "init_scale": 128.0}
+    assert C.DistributedSpeedConfig(C.bf16_config()).loss_scaler()["mode"] == "none"
+    ScalerConfig(**dyn).validate()
+
+
+def test_unknown_key_raises_typeerror_like_the_reference():
+    with pytest.raises(TypeError):
+        C.DistributedSpeedConfig({"fp16": {"enabled": True, "not_a_key": 1}})
+    with pytest.raises(TypeError):
+        C.DistributedSpeedConfig({"zero_optimization": {"stagee": 2}})
+
+
+@pytest.mark.parametrize("cfg,msg", [
+    ({"fp16": {"enabled": True}, "bf16": {"enabled": True}}, "Cannot enable both FP16 and BF16"),
+    ({"zero_optimization": {"stage": 4}}, "ZeRO stage must be 0, 1, 2, or 3"),
+    ({"gradient_accumulation_steps": 0}, "gradient_accumulation_steps must be positive"),
+    ({"fp16": {"enabled": True, "hysteresis": 0}}, "hysteresis must be >= 1"),
+])
+def test_validation_messages(cfg, msg):
+    with pytest.raises(ValueError, match="Configuration validation failed") as e:
+        C.DistributedSpeedConfig(cfg)
+    assert msg in str(e.value)
+
+
+def test_gradient_clipping_alias_and_extra_sections():
+    c = C.DistributedSpeedConfig({"gradient_clipping": 0.5, "scheduler": {"type": "WarmupLR"}})
+    assert c.max_grad_norm == 0.5 and c.extra["scheduler"] == {"type": "WarmupLR"}
+    assert c["scheduler"]["type"] == "WarmupLR" and c.get("nope", 7) == 7
+
+
+def test_env_overrides(monkeypatch):
+    monkeypatch.setenv("DISTRIBUTEDSPEED_LEARNING_RATE", "0.005")
+    monkeypatch.setenv("DISTRIBUTEDSPEED_BF16_ENABLED", "true")
+    monkeypatch.setenv("DISTRIBUTEDSPEED_ZERO_STAGE", "2")
+    c = C.DistributedSpeedConfig({})
+    assert c.adamw_params()["lr"] == 0.005 and c.bf16.enabled and c.zero_optimization.stage == 2
+
+
+def test_load_config_json_and_yaml(tmp_path):
+    d = {"fp16": {"enabled": True}, "gradient_accumulation_steps": 4}
+    j = tmp_path / "ds.json"
+    j.write_text(json.dumps(d))
+    y = tmp_path / "ds.yaml"
+    y.write_text("fp16:\n  enabled: true\ngradient_accumulation_steps: 4\n")
+    for path in (j, y):
+        c = C.load_config(str(path))
+        assert c.fp16.enabled and c.gradient_accumulation_steps == 4
+    with pytest.raises(FileNotFoundError):
+        C.load_config(str(tmp_path / "missing.json"))
+    with pytest.raises(TypeError):
+        C.load_config(3.0)
+
+
+# ---- flat partition (CPU tensors) ----------------------------------------------------------
+
+def _params(shapes, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for s in shapes]
+
+
+def test_flat_layout_alignment_and_views():
+    ps = _params([(3, 5), (7,), (4, 4), (1,), (10,)])
+    orig = [p.detach().clone() for p in ps]
+    fp = FlatPartition([ps[:2], ps[2:]], torch.device("cpu"), torch.bfloat16)
+    offs = [s.offset for s in fp.slots]
+    assert offs == [0, 16, 24, 40, 48] and all(o % ALIGN == 0 for o in offs)
+    assert fp.group_ranges == [(0, 24), (24, 64)] and fp.numel == 64
+    for s, p, o in zip(fp.slots, ps, orig):
+        assert p.dtype == torch.bfloat16 and p.grad is not None and p.grad.dtype == torch.bfloat16
+        assert torch.equal(fp.master[s.offset:s.offset + s.numel], o.reshape(-1))  # master keeps fp32 values
+        assert torch.equal(p.detach().float().reshape(-1), o.reshape(-1).to(torch.bfloat16).float())
+        assert p.data_ptr() == fp.param16[s.offset:].data_ptr()
+    # padding is zero everywhere
+    used = torch.zeros(fp.numel, dtype=torch.bool)
+    for s in fp.slots:
+        used[s.offset:s.offset + s.numel] = True
+    assert (fp.master[~used] == 0).all() and (fp.param16[~used].float() == 0).all()
+
+
+def test_autograd_accumulates_into_flat_views_on_cpu():
+    lin = torch.nn.Linear(6, 3)
+    fp = FlatPartition([list(lin.parameters())], torch.device("cpu"), None)
+    x = torch.randn(4, 6)
+    lin(x).sum().backward()
+    lin(x).sum().backward()  # accumulates in place
+    for s, p in zip(fp.slots, fp.params):
+        assert p.grad.data_ptr() == fp.grad[s.offset:].data_ptr()
+    assert torch.allclose(fp.grad[fp.slots[1].offset:fp.slots[1].offset + 3], torch.full((3,), 8.0))
+    fp.check_grads_bound()
+    # a replaced grad is copied back into the flat buffer and the view restored
+    lin.bias.grad = torch.ones(3)
+    fp.check_grads_bound()
+    assert torch.equal(fp.grad[fp.slots[1].offset:fp.slots[1].offset + 3], torch.ones(3))
+    assert lin.bias.grad.data_ptr() == fp.grad[fp.slots[1].offset:].data_ptr()
+    lin.weight.grad = None
+    fp.check_grads_bound()
+    assert lin.weight.grad is not None and float(lin.weight.grad.abs().sum()) == 0.0
+    fp.zero_grad()
+    assert float(fp.grad.abs().sum()) == 0.0
+
+
+def test_flat_rejects_duplicates_and_bad_dtype():
+    p = torch.nn.Parameter(torch.zeros(3))
+    with pytest.raises(ValueError):
+        FlatPartition([[p], [p]], torch.device("cpu"), None)
+    with pytest.raises(ValueError):
+        FlatPartition([[torch.nn.Parameter(torch.zeros(3))]], torch.device("cpu"), torch.float64)
+    with pytest.raises(ValueError):
+        FlatPartition([[torch.nn.Parameter(torch.zeros(3))]], torch.device("cpu"), None, offload=True)
+
+
+def test_layout_manifest_names():
+    lin = torch.nn.Linear(2, 2)
+    names = {id(p): n for n, p in lin.named_parameters()}
+    fp = FlatPartition([list(lin.parameters())], torch.device("cpu"), None, names)
+    assert [e["name"] for e in fp.layout()] == ["weight", "bias"]
+
+
+# ---- bias corrections, hyper-parameters ----------------------------------------------------
+
+def test_bias_correction_table_matches_torch_expression():
+    tab = BiasCorrectionTable(torch.device("cpu"), 0.9, 0.95, capacity=8)
+    assert tab.length >= 8
+    t = tab.table.numpy()
+    for step in range(1, 9):
+        assert t[2 * (step - 1)] == 1 - 0.9 ** float(step)
+        assert t[2 * (step - 1) + 1] == (1 - 0.95 ** float(step)) ** 0.5
+    tab.ensure(5000)
+    assert tab.length >= 5000 and tab.table.numel() == 2 * tab.length
+    tab.ensure(10, betas=(0.8, 0.99))
+    assert tab.table[0].item() == 1 - 0.8 ** 1.0
+
+
+def test_hyper_validation_messages():
+    for kw, msg in ((dict(lr=-1), "Invalid learning rate"), (dict(eps=-1), "Invalid epsilon"),
+                    (dict(beta1=1.0), "index 0"), (dict(beta2=-0.1), "index 1"),
+                    (dict(weight_decay=-1), "Invalid weight_decay"), (dict(max_grad_norm=math.nan), "NaN")):
+        with pytest.raises(ValueError, match=msg):
+            AdamWHyper(**kw).validate()
+    c = AdamWHyper(lr=1e-3).to_c()
+    assert (c.lr, c.beta1, c.clip_eps) == (1e-3, 0.9, 1e-6)
+
+
+def test_ops_reject_cpu_tensors():
+    from distributedspeed_amd import ops
+    t = torch.zeros(16)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.adamw_flat(t, t, t, None, t, torch.zeros(64, dtype=torch.uint8))
+    with pytest.raises(TypeError):
+        ops.grad_code(torch.int32)
+    assert ops.grad_code(torch.float32) == 0 and ops.dtype_code(torch.bfloat16) == 2
+
+
+def test_initialize_fails_loudly_without_gpu():
+    import distributedspeed_amd as ds
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    with pytest.raises(RuntimeError, match="GPU"):
+        ds.initialize(torch.nn.Linear(2, 2), {})
+
+
+def test_oracle_not_imported_by_product():
+    import pathlib
+    root = pathlib.Path(__file__).resolve().parents[1] / "distributedspeed_amd"
+    for f in root.rglob("*.py"):
+        text = f.read_text()
+        assert "import oracle" not in text and "from oracle" not in text, f
+    assert np.__version__  # numpy is the only array dependency of the oracle
