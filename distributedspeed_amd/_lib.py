@@ -19,6 +19,7 @@ DSX_F32, DSX_F16, DSX_BF16 = 0, 1, 2
 DSX_SCALE_NONE, DSX_SCALE_STATIC, DSX_SCALE_DYNAMIC = 0, 1, 2
 DSX_EINVAL = 1
 DSX_STATE_ERR_BC_TABLE = 1
+DSX_STATE_ERR_GROUPS = 2
 DSX_MAX_PARTIALS = 8192
 DSX_MAX_GROUPS = 16
 ABI_VERSION = 1
@@ -61,8 +62,13 @@ class DsxChunk(_c.Structure):
     _fields_ = [("tensor", _c.c_int32), ("reserved", _c.c_int32), ("start", _c.c_int64), ("len", _c.c_int64)]
 
 
+class DsxGroupsDev(_c.Structure):
+    _fields_ = [("hyper", DsxAdamwHyper * 16), ("bc_table", _P * 16), ("t_offset", _c.c_int32 * 16),
+                ("ngroups", _c.c_int32), ("bc_len", _c.c_int32), ("reserved", _c.c_int64 * 2)]
+
+
 for _s, _n in ((DsxState, 64), (DsxScalerConfig, 32), (DsxAdamwHyper, 56), (DsxStepScalars, 64),
-               (DsxTensorRef, 56), (DsxChunk, 24)):
+               (DsxTensorRef, 56), (DsxChunk, 24), (DsxGroupsDev, 1112)):
     assert _c.sizeof(_s) == _n, (_s.__name__, _c.sizeof(_s))
 
 # name -> (restype, argtypes); every symbol include/dsx.h declares.
@@ -78,6 +84,7 @@ SIGNATURES = {
     "dsx_finalize": (_c.c_int, [_P, _c.c_int32, _P, DsxScalerConfig, DsxAdamwHyper, _P, _c.c_int32, _P, _P]),
     "dsx_finalize_groups": (_c.c_int, [_P, _c.c_int32, _P, DsxScalerConfig, _P, _P, _P, _c.c_int32, _c.c_int32,
                                        _P, _P]),
+    "dsx_finalize_dev": (_c.c_int, [_P, _c.c_int32, _P, DsxScalerConfig, _P, _c.c_int32, _P, _P]),
     "dsx_adamw_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, _P]),
     "dsx_zero_step_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, DsxScalerConfig,
                                       DsxAdamwHyper, _P, _c.c_int32, _P, _c.c_int32, _P, _P]),

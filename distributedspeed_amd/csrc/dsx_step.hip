@@ -33,6 +33,7 @@ static_assert(sizeof(DsxAdamwHyper) == 56, "DsxAdamwHyper layout");
 static_assert(sizeof(DsxStepScalars) == 64, "DsxStepScalars layout");
 static_assert(sizeof(DsxTensorRef) == 56, "DsxTensorRef layout");
 static_assert(sizeof(DsxChunk) == 24, "DsxChunk layout");
+static_assert(sizeof(DsxGroupsDev) == 1112, "DsxGroupsDev layout");
 
 namespace {
 
@@ -289,59 +290,60 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm(const void* __restrict
 
 // ---- K0: finalize ------------------------------------------------------------
 
-struct Groups {
-  DsxAdamwHyper hyper[DSX_MAX_GROUPS];
-  const double* bc[DSX_MAX_GROUPS];
-  int32_t t_offset[DSX_MAX_GROUPS];
-  int32_t n;
-};
+// Hyper-parameters a device-resident group block may hold: the admissible
+// ranges of torch.optim.Adam's constructor, checked again on the device for
+// the graph path (where the host cannot see the values at launch).
+__device__ __forceinline__ bool hyper_ok(const DsxAdamwHyper& h) {
+  return h.lr >= 0.0 && h.eps >= 0.0 && h.beta1 >= 0.0 && h.beta1 < 1.0 && h.beta2 >= 0.0 && h.beta2 < 1.0 &&
+         h.weight_decay >= 0.0 && h.clip_eps >= 0.0 && h.max_grad_norm == h.max_grad_norm;
+}
 
-// Global part of a step (norm, skip, clip, t, scaler) once; per-group fp32
-// scalars for each parameter group.
-__global__ __launch_bounds__(kBlock) void k0_finalize(const double* __restrict__ partials, int32_t nparts,
-                                                      DsxState* __restrict__ state, DsxScalerConfig scfg,
-                                                      Groups grp, int32_t bc_len,
-                                                      DsxStepScalars* __restrict__ out) {
-  double x = 0.0;
-  for (int i = threadIdx.x; i < nparts; i += kBlock) x += partials[i];
-  const double sumsq = block_sum(x);
-  if (threadIdx.x != 0) return;
-
+// Thread 0 only. Global part of a step (norm, skip, clip, t, scaler) once;
+// per-group fp32 scalars into out[0..nout). Slots at or past grp.ngroups (and
+// every slot when groups_bad) get skip = 1, so a K2 launched for them leaves
+// its group unchanged rather than reusing an older step's scalars.
+__device__ void finalize_body(double sumsq, DsxState* __restrict__ state, const DsxScalerConfig& scfg,
+                              const DsxGroupsDev& grp, bool groups_bad, int nout,
+                              DsxStepScalars* __restrict__ out) {
   DsxState s = *state;
   const double norm = sqrt(sumsq);
   const float inv = inv_of(s.scale);
   const bool found_inf = !__builtin_isfinite(sumsq);
   const bool dynamic = scfg.mode == DSX_SCALE_DYNAMIC;
   const int32_t t = s.t + 1;
-  bool skip = found_inf;
-  if (!found_inf) {
-    for (int k = 0; k < grp.n; ++k) {
+  bool skip = found_inf || groups_bad;
+  if (groups_bad) s.error |= DSX_STATE_ERR_GROUPS;
+  const int ng = groups_bad ? 0 : grp.ngroups;
+  if (!skip) {
+    for (int k = 0; k < ng; ++k) {
       const int32_t tk = t - grp.t_offset[k];
-      if (tk < 1 || tk > bc_len) {
+      if (tk < 1 || tk > grp.bc_len) {
         skip = true;
         s.error |= DSX_STATE_ERR_BC_TABLE;
       }
     }
   }
   float coef = 1.0f;
-  const DsxAdamwHyper& h0 = grp.hyper[0];
-  if (!skip && h0.max_grad_norm > 0.0 && norm > h0.max_grad_norm)
-    coef = (float)(h0.max_grad_norm / (norm + h0.clip_eps));
-
-  for (int k = 0; k < grp.n; ++k) {
-    const DsxAdamwHyper& hp = grp.hyper[k];
+  if (ng > 0) {
+    const DsxAdamwHyper& h0 = grp.hyper[0];
+    if (!skip && h0.max_grad_norm > 0.0 && norm > h0.max_grad_norm)
+      coef = (float)(h0.max_grad_norm / (norm + h0.clip_eps));
+  }
+  for (int k = 0; k < nout; ++k) {
+    const bool live = k < ng;
     DsxStepScalars o = {};
     o.sumsq = sumsq;
     o.norm = norm;
     o.inv_scale = inv;
     o.clip_coef = coef;
     o.decay = 1.0f;
-    o.skip = skip ? 1 : 0;
-    o.t = (skip ? s.t : t) - grp.t_offset[k];
-    if (!skip) {
+    o.skip = (skip || !live) ? 1 : 0;
+    o.t = (skip ? s.t : t) - (live ? grp.t_offset[k] : 0);
+    if (!skip && live) {
+      const DsxAdamwHyper& hp = grp.hyper[k];
       const int32_t tk = t - grp.t_offset[k];
-      const double bc1 = grp.bc[k][2 * (int64_t)(tk - 1)];
-      const double bc2s = grp.bc[k][2 * (int64_t)(tk - 1) + 1];
+      const double bc1 = grp.bc_table[k][2 * (int64_t)(tk - 1)];
+      const double bc2s = grp.bc_table[k][2 * (int64_t)(tk - 1) + 1];
       if (hp.weight_decay != 0.0) o.decay = (float)(1.0 - hp.lr * hp.weight_decay);
       o.w1 = (float)(1.0 - hp.beta1);
       o.w1m1 = o.w1 - 1.0f;
@@ -381,6 +383,34 @@ __global__ __launch_bounds__(kBlock) void k0_finalize(const double* __restrict__
   s.last_skip = skip ? 1 : 0;
   s.last_norm = norm;
   *state = s;
+}
+
+__device__ __forceinline__ double reduce_partials(const double* __restrict__ partials, int32_t nparts) {
+  double x = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += kBlock) x += partials[i];
+  return block_sum(x);
+}
+
+// Group inputs as a kernel argument (validated on the host).
+__global__ __launch_bounds__(kBlock) void k0_finalize(const double* __restrict__ partials, int32_t nparts,
+                                                      DsxState* __restrict__ state, DsxScalerConfig scfg,
+                                                      DsxGroupsDev grp, DsxStepScalars* __restrict__ out) {
+  const double sumsq = reduce_partials(partials, nparts);
+  if (threadIdx.x == 0) finalize_body(sumsq, state, scfg, grp, false, grp.ngroups, out);
+}
+
+// Group inputs from device memory (the graph path); validated here.
+__global__ __launch_bounds__(kBlock) void k0_finalize_dev(const double* __restrict__ partials, int32_t nparts,
+                                                          DsxState* __restrict__ state, DsxScalerConfig scfg,
+                                                          const DsxGroupsDev* __restrict__ gp, int32_t max_groups,
+                                                          DsxStepScalars* __restrict__ out) {
+  const double sumsq = reduce_partials(partials, nparts);
+  if (threadIdx.x != 0) return;
+  const DsxGroupsDev grp = *gp;
+  bool bad = grp.ngroups < 1 || grp.ngroups > max_groups || grp.ngroups > DSX_MAX_GROUPS || grp.bc_len < 0;
+  for (int k = 0; !bad && k < grp.ngroups; ++k)
+    bad = !hyper_ok(grp.hyper[k]) || grp.t_offset[k] < 0 || (grp.bc_len > 0 && grp.bc_table[k] == nullptr);
+  finalize_body(sumsq, state, scfg, grp, bad, max_groups, out);
 }
 
 __global__ void k_state_init(DsxState* state, float scale, int32_t hysteresis) {
@@ -638,18 +668,19 @@ int do_unscale_norm(const void* g, int gdt, int64_t n, const DsxState* st, doubl
   return launch_status("dsx_unscale_norm");
 }
 
-int do_finalize(const double* partials, int32_t nparts, DsxState* st, const DsxScalerConfig& sc, const Groups& grp,
-                int32_t bc_len, DsxStepScalars* out, hipStream_t s) {
-  hipLaunchKernelGGL(k0_finalize, dim3(1), dim3(kBlock), 0, s, partials, nparts, st, sc, grp, bc_len, out);
+int do_finalize(const double* partials, int32_t nparts, DsxState* st, const DsxScalerConfig& sc,
+                const DsxGroupsDev& grp, DsxStepScalars* out, hipStream_t s) {
+  hipLaunchKernelGGL(k0_finalize, dim3(1), dim3(kBlock), 0, s, partials, nparts, st, sc, grp, out);
   return launch_status("dsx_finalize");
 }
 
-Groups one_group(const DsxAdamwHyper& hp, const double* bc) {
-  Groups g = {};
+DsxGroupsDev one_group(const DsxAdamwHyper& hp, const double* bc, int32_t bc_len) {
+  DsxGroupsDev g = {};
   g.hyper[0] = hp;
-  g.bc[0] = bc;
+  g.bc_table[0] = bc;
   g.t_offset[0] = 0;
-  g.n = 1;
+  g.ngroups = 1;
+  g.bc_len = bc_len;
   return g;
 }
 
@@ -775,7 +806,7 @@ int dsx_finalize(const double* partials, int32_t nparts, DsxState* state, DsxSca
   if (rc) return rc;
   if (!state || !out) return fail(DSX_EINVAL, "null state or scalars");
   if (bc_len < 0 || (bc_len > 0 && !bc_table)) return fail(DSX_EINVAL, "bad bias-correction table");
-  return do_finalize(partials, nparts, state, scaler, one_group(hyper, bc_table), bc_len, out, as_stream(stream));
+  return do_finalize(partials, nparts, state, scaler, one_group(hyper, bc_table, bc_len), out, as_stream(stream));
 }
 
 int dsx_finalize_groups(const double* partials, int32_t nparts, DsxState* state, DsxScalerConfig scaler,
@@ -789,18 +820,32 @@ int dsx_finalize_groups(const double* partials, int32_t nparts, DsxState* state,
   if (!hypers || !bc_tables || !t_offsets) return fail(DSX_EINVAL, "null group arrays");
   if (!state || !out) return fail(DSX_EINVAL, "null state or scalars");
   if (bc_len < 0) return fail(DSX_EINVAL, "bad bias-correction table length");
-  Groups grp = {};
-  grp.n = ngroups;
+  DsxGroupsDev grp = {};
+  grp.ngroups = ngroups;
+  grp.bc_len = bc_len;
   for (int k = 0; k < ngroups; ++k) {
     rc = check_hyper(hypers[k]);
     if (rc) return rc;
     if (bc_len > 0 && !bc_tables[k]) return fail(DSX_EINVAL, "null bias-correction table for group %d", k);
     if (t_offsets[k] < 0) return fail(DSX_EINVAL, "negative t_offset for group %d", k);
     grp.hyper[k] = hypers[k];
-    grp.bc[k] = bc_tables[k];
+    grp.bc_table[k] = bc_tables[k];
     grp.t_offset[k] = t_offsets[k];
   }
-  return do_finalize(partials, nparts, state, scaler, grp, bc_len, out, as_stream(stream));
+  return do_finalize(partials, nparts, state, scaler, grp, out, as_stream(stream));
+}
+
+int dsx_finalize_dev(const double* partials, int32_t nparts, DsxState* state, DsxScalerConfig scaler,
+                     const DsxGroupsDev* groups, int32_t max_groups, DsxStepScalars* out, void* stream) {
+  int rc = check_parts(partials, nparts);
+  if (!rc) rc = check_scaler(scaler);
+  if (rc) return rc;
+  if (!state || !out || !groups) return fail(DSX_EINVAL, "null state, scalars or groups");
+  if (max_groups < 1 || max_groups > DSX_MAX_GROUPS)
+    return fail(DSX_EINVAL, "max_groups must be in [1, %d] (got %d)", DSX_MAX_GROUPS, max_groups);
+  hipLaunchKernelGGL(k0_finalize_dev, dim3(1), dim3(kBlock), 0, as_stream(stream), partials, nparts, state, scaler,
+                     groups, max_groups, out);
+  return launch_status("dsx_finalize_dev");
 }
 
 int dsx_adamw_flat(float* master, float* exp_avg, float* exp_avg_sq, void* param16, int param_dtype,
@@ -825,7 +870,7 @@ int dsx_zero_step_flat(float* master, float* exp_avg, float* exp_avg_sq, void* p
   if (bc_len < 0 || (bc_len > 0 && !bc_table)) return fail(DSX_EINVAL, "bad bias-correction table");
   hipStream_t s = as_stream(stream);
   rc = do_unscale_norm(grad, grad_dtype, n, state, partials, nparts, s);
-  if (!rc) rc = do_finalize(partials, nparts, state, scaler, one_group(hyper, bc_table), bc_len, out, s);
+  if (!rc) rc = do_finalize(partials, nparts, state, scaler, one_group(hyper, bc_table, bc_len), out, s);
   if (!rc) rc = do_adamw_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, out, s);
   return rc;
 }

@@ -54,7 +54,8 @@ class DistributedSpeedEngine(torch.nn.Module):
         names = {id(p): n for n, p in self.module.named_parameters()}
         common = dict(max_grad_norm=float(config.max_grad_norm or 0), param_dtype=self.param_dtype,
                       loss_scaler=scaler, device=self.device, param_names=names,
-                      offload=bool(config.zero_optimization.cpu_offload))
+                      offload=bool(config.zero_optimization.cpu_offload),
+                      graph=bool(config.get("hip_graph", False)))
         if optimizer is not None:
             if not isinstance(optimizer, AdamWOptimizer):
                 optimizer = adopt_torch_optimizer(optimizer, **common)

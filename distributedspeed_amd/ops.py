@@ -200,6 +200,55 @@ def finalize_groups(partials: torch.Tensor, nparts: int, state: torch.Tensor, sc
               int(bc_len), _ptr(out), _stream(dev))
 
 
+GROUPS_BYTES = ctypes.sizeof(_lib.DsxGroupsDev)
+
+
+def pack_groups(hypers: list[DsxAdamwHyper], bc_tables: list[torch.Tensor], t_offsets: list[int],
+                bc_len: int) -> bytes:
+    """A DsxGroupsDev image (for dsx_finalize_dev) with the host-side checks
+    dsx_finalize_groups makes, so a bad value raises here as it does eagerly."""
+    k = len(hypers)
+    if not 1 <= k <= DSX_MAX_GROUPS or len(bc_tables) != k or len(t_offsets) != k:
+        raise ValueError(f"need 1..{DSX_MAX_GROUPS} groups with one table and offset each")
+    from .flat_step import AdamWHyper
+    g = _lib.DsxGroupsDev()
+    for i in range(k):
+        h = hypers[i]
+        try:
+            AdamWHyper(h.lr, h.beta1, h.beta2, h.eps, h.weight_decay, h.max_grad_norm, h.clip_eps).validate()
+        except ValueError as e:  # the error type and wording dsx_finalize_groups reports
+            raise _lib.DsxError("dsx_finalize_dev", _lib.DSX_EINVAL, str(e)) from None
+        t = bc_tables[i]
+        if t.dtype != torch.float64 or t.device.type != "cuda" or t.numel() < 2 * bc_len:
+            raise ValueError(f"bc_table[{i}] must be a float64 GPU tensor of at least {2 * bc_len} entries")
+        if int(t_offsets[i]) < 0:
+            raise ValueError(f"negative t_offset for group {i}")
+        g.hyper[i] = h
+        g.bc_table[i] = t.data_ptr()
+        g.t_offset[i] = int(t_offsets[i])
+    g.ngroups = k
+    g.bc_len = int(bc_len)
+    return bytes(g)
+
+
+def finalize_dev(partials: torch.Tensor, nparts: int, state: torch.Tensor, scaler: DsxScalerConfig,
+                 groups_dev: torch.Tensor, max_groups: int, out: torch.Tensor) -> None:
+    """K0 reading its per-group inputs from `groups_dev` (a DsxGroupsDev in
+    device memory), the form a captured graph replays; `out` holds max_groups
+    DsxStepScalars, all written."""
+    dev = _device(state)
+    if not 1 <= max_groups <= DSX_MAX_GROUPS:
+        raise ValueError(f"max_groups must be in [1, {DSX_MAX_GROUPS}]")
+    _need(partials, "partials", torch.float64, None, dev, 8)
+    if nparts > partials.numel():
+        raise ValueError("nparts exceeds the partials buffer")
+    _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
+    _need(groups_dev, "groups", torch.uint8, GROUPS_BYTES, dev, 8)
+    _need(out, "scalars", torch.uint8, SCALARS_BYTES * max_groups, dev, 8)
+    _lib.call("dsx_finalize_dev", _ptr(partials), int(nparts), _ptr(state), scaler, _ptr(groups_dev),
+              int(max_groups), _ptr(out), _stream(dev))
+
+
 # ---- ragged lists (K3) --------------------------------------------------------------
 
 class ChunkTable:

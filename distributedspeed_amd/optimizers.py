@@ -15,6 +15,9 @@ state_dict / load_state_dict, and a step that runs entirely on the GPU:
 
 with no host synchronisation. Parameters are re-homed into one
 FlatPartition at construction (param.data / param.grad become views).
+With graph=True the three stages are captured into one HIP graph at the
+first step and replayed afterwards (K0 then reads the per-group values from
+device memory; see graph.py).
 """
 from __future__ import annotations
 
@@ -34,7 +37,8 @@ class AdamWOptimizer(torch.optim.Optimizer):
     def __init__(self, params: Iterable, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
                  weight_decay: float = 1e-2, *, max_grad_norm: float = 0.0, param_dtype: torch.dtype | None = None,
                  loss_scaler: ScalerConfig | None = None, device: torch.device | None = None,
-                 param_names: dict | None = None, offload: bool = False, offload_chunk_elems: int = 64 << 20):
+                 param_names: dict | None = None, offload: bool = False, offload_chunk_elems: int = 64 << 20,
+                 graph: bool = False):
         if not 0.0 <= lr:
             raise ValueError(f"Invalid learning rate: {lr}")
         if not 0.0 <= eps:
@@ -74,6 +78,10 @@ class AdamWOptimizer(torch.optim.Optimizer):
         self._bc: dict[tuple[float, float], BiasCorrectionTable] = {}
         self._t_offsets = [0] * len(self.param_groups)
         self.steps_issued = 0
+        if graph and offload:
+            raise ValueError("graph=True needs HBM-resident state (offload=False)")
+        self.use_graph = bool(graph)
+        self._graph = None
         self._bind_state()
 
     # ---- torch.optim.Optimizer protocol ---------------------------------------------
@@ -126,6 +134,14 @@ class AdamWOptimizer(torch.optim.Optimizer):
         self.flat.check_grads_bound()
         self.steps_issued += 1
         hs, tables, bc_len = self._hypers()
+        if self.use_graph:
+            # Captured once (first step), replayed after uploading this step's
+            # per-group block; the same kernels, buffers and order as below.
+            if self._graph is None:
+                from .graph import GraphedStep
+                self._graph = GraphedStep(self)
+            self._graph.replay(hs, tables, bc_len)
+            return
         ops.unscale_norm(self.flat.grad, self.dstate, self.partials, self.nparts)
         ops.finalize_groups(self.partials, self.nparts, self.dstate, self.scaler.to_c(), hs, tables,
                             self._t_offsets, bc_len, self.scalars)

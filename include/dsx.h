@@ -67,6 +67,7 @@ extern "C" {
 
 /* state error bits (DsxState.error) */
 #define DSX_STATE_ERR_BC_TABLE 1 /* bias-correction table shorter than t */
+#define DSX_STATE_ERR_GROUPS   2 /* device-side group inputs out of range */
 
 /* upper bound on the partials one K1 launch may write */
 #define DSX_MAX_PARTIALS 8192
@@ -223,6 +224,29 @@ int dsx_finalize_groups(const double* partials, int32_t nparts, DsxState* state,
                         const double* const* bc_tables,
                         const int32_t* t_offsets, int32_t ngroups,
                         int32_t bc_len, DsxStepScalars* out, void* stream);
+
+/* Per-step inputs of dsx_finalize_dev, held in DEVICE memory so that a
+ * captured graph reads the current values at every replay (1112 bytes). */
+typedef struct DsxGroupsDev {
+  DsxAdamwHyper  hyper[DSX_MAX_GROUPS];
+  const double*  bc_table[DSX_MAX_GROUPS];  /* device tables, as dsx_finalize */
+  int32_t        t_offset[DSX_MAX_GROUPS];
+  int32_t        ngroups;
+  int32_t        bc_len;
+  int64_t        reserved[2];
+} DsxGroupsDev;
+
+/* dsx_finalize_groups with its per-group inputs read from `groups` (device
+ * memory) instead of kernel arguments: the form to capture in a HIP graph
+ * (the host updates `groups` with an async copy before each replay). `out`
+ * has room for max_groups scalars and all of them are written: slots at or
+ * past groups->ngroups get skip = 1. A groups->ngroups outside
+ * [1, max_groups] or an invalid hyper-parameter sets DSX_STATE_ERR_GROUPS and
+ * skips the step (every slot). No counterpart in the reference (it has no
+ * graph path). */
+int dsx_finalize_dev(const double* partials, int32_t nparts, DsxState* state,
+                     DsxScalerConfig scaler, const DsxGroupsDev* groups,
+                     int32_t max_groups, DsxStepScalars* out, void* stream);
 
 /* ---- K2: AdamW + cast over a flat partition -------------------------- */
 

@@ -38,10 +38,11 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 def test_struct_layouts_match_header(lib):
     from distributedspeed_amd import _lib
     text = open(HEADER).read()
-    for struct in ("DsxState", "DsxScalerConfig", "DsxAdamwHyper", "DsxStepScalars", "DsxTensorRef", "DsxChunk"):
+    for struct in ("DsxState", "DsxScalerConfig", "DsxAdamwHyper", "DsxStepScalars", "DsxTensorRef", "DsxChunk",
+                   "DsxGroupsDev"):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
-        fields = re.findall(r"([A-Za-z_][A-Za-z0-9_\s\*]*?)\s+\*?([a-z0-9_]+)(\[\d+\])?\s*;", body)
+        fields = re.findall(r"([A-Za-z_][A-Za-z0-9_\s\*]*?)\s+\*?([a-z0-9_]+)(\[[A-Z0-9_]+\])?\s*;", body)
         cls = getattr(_lib, struct)
         assert [f[1] for f in fields] == [f[0] for f in cls._fields_], struct
 

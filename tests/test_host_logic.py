@@ -205,3 +205,17 @@ def test_oracle_not_imported_by_product():
         text = f.read_text()
         assert "import oracle" not in text and "from oracle" not in text, f
     assert np.__version__  # numpy is the only array dependency of the oracle
+
+
+def test_pack_groups_checks_on_host():
+    """The graph path's per-step group block is checked on the host with the
+    eager path's error type and wording."""
+    from distributedspeed_amd import _lib, ops
+    t = torch.zeros(8, dtype=torch.float64)
+    with pytest.raises(_lib.DsxError, match="Invalid learning rate"):
+        ops.pack_groups([AdamWHyper(lr=-1).to_c()], [t], [0], 4)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.pack_groups([AdamWHyper().to_c()], [t], [0], 4)
+    with pytest.raises(ValueError, match="groups"):
+        ops.pack_groups([], [], [], 4)
+    assert ops.GROUPS_BYTES == 1112
