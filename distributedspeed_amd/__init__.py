@@ -88,9 +88,9 @@ def __getattr__(name: str):
     if name in ("ZeROOptimizer",):
         from .zero import ZeROOptimizer
         return ZeROOptimizer
-    if name in ("AdamWOptimizer",):
-        from .optimizers import AdamWOptimizer
-        return AdamWOptimizer
+    if name in ("AdamWOptimizer", "MultiTensorAdamWOptimizer"):
+        from . import optimizers as _o
+        return getattr(_o, name)
     if name in ("DistributedSpeedConfig", "load_config", "fp16_config", "bf16_config", "zero_config"):
         from . import config as _c
         return getattr(_c, name)
@@ -98,5 +98,5 @@ def __getattr__(name: str):
 
 
 __all__ = ["initialize", "is_initialized", "get_config", "get_rank", "get_world_size", "get_local_rank", "destroy",
-           "DistributedSpeedEngine", "ZeROOptimizer", "AdamWOptimizer", "DistributedSpeedConfig", "load_config",
+           "DistributedSpeedEngine", "ZeROOptimizer", "AdamWOptimizer", "MultiTensorAdamWOptimizer", "DistributedSpeedConfig", "load_config",
            "fp16_config", "bf16_config", "zero_config"]

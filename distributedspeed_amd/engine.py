@@ -26,7 +26,7 @@ import torch
 
 from .config import DistributedSpeedConfig
 from .flat_step import ScalerConfig
-from .optimizers import AdamWOptimizer, adopt_torch_optimizer
+from .optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer, _FusedAdamWBase, adopt_torch_optimizer
 from .zero import ZeROOptimizer
 
 
@@ -56,9 +56,10 @@ class DistributedSpeedEngine(torch.nn.Module):
                       loss_scaler=scaler, device=self.device, param_names=names,
                       offload=bool(config.zero_optimization.cpu_offload),
                       graph=bool(config.get("hip_graph", False)))
+        contiguous = bool(config.zero_optimization.contiguous_gradients)
         if optimizer is not None:
-            if not isinstance(optimizer, AdamWOptimizer):
-                optimizer = adopt_torch_optimizer(optimizer, **common)
+            if not isinstance(optimizer, _FusedAdamWBase):
+                optimizer = adopt_torch_optimizer(optimizer, contiguous=contiguous, **common)
         else:
             if config.optimizer.type.lower() not in ("adamw", "adam"):
                 raise NotImplementedError(f"optimizer.type {config.optimizer.type!r}: the fused step is AdamW")
@@ -68,11 +69,12 @@ class DistributedSpeedEngine(torch.nn.Module):
             else:
                 groups = [p for p in params if p.requires_grad]
             hp = config.adamw_params()
-            optimizer = AdamWOptimizer(groups, lr=hp["lr"], betas=hp["betas"], eps=hp["eps"],
-                                       weight_decay=hp["weight_decay"], **common)
+            cls = AdamWOptimizer if contiguous else MultiTensorAdamWOptimizer
+            optimizer = cls(groups, lr=hp["lr"], betas=hp["betas"], eps=hp["eps"], weight_decay=hp["weight_decay"],
+                            **common)
         zcfg = {"stage": config.zero_optimization.stage,
                 "gradient_accumulation_steps": config.gradient_accumulation_steps}
-        self.optimizer = ZeROOptimizer(optimizer, zcfg, list(optimizer.flat.params))
+        self.optimizer = ZeROOptimizer(optimizer, zcfg, list(optimizer.dsx_params))
         self.lr_scheduler = lr_scheduler
         self.global_steps = 0
         self.micro_steps = 0
@@ -134,7 +136,7 @@ class DistributedSpeedEngine(torch.nn.Module):
                     "client_state": client_state or {}}, os.path.join(path, "model_states.pt"))
         torch.save(self.optimizer.state_dict(), os.path.join(path, "optim_states.pt"))
         with open(os.path.join(path, "layout.json"), "w") as f:
-            json.dump({"numel": opt.flat.numel, "precision": self.config.precision, "params": opt.flat.layout()}, f)
+            json.dump({"numel": opt.numel, "precision": self.config.precision, "params": opt.layout()}, f)
         with open(os.path.join(save_dir, "latest"), "w") as f:
             f.write(tag)
         return path
@@ -146,7 +148,7 @@ class DistributedSpeedEngine(torch.nn.Module):
         path = os.path.join(load_dir, tag)
         with open(os.path.join(path, "layout.json")) as f:
             layout = json.load(f)
-        mine = self.optimizer.base_optimizer.flat.layout()
+        mine = self.optimizer.base_optimizer.layout()
         if [(p["name"], p["numel"]) for p in layout["params"]] != [(p["name"], p["numel"]) for p in mine]:
             raise ValueError("checkpoint parameter layout does not match this model")
         ms = torch.load(os.path.join(path, "model_states.pt"), weights_only=True)

@@ -135,6 +135,12 @@ class FlatPartition:
     def zero_grad(self) -> None:
         self.grad.zero_()
 
+    def refresh_params16(self) -> None:
+        """param16 <- master (RNE), after the master was loaded."""
+        if self.param16 is not None:
+            with torch.no_grad():
+                self.param16.copy_(self.master.to(self.device))
+
     def layout(self) -> list[dict]:
         return [{"name": s.name, "offset": s.offset, "numel": s.numel, "shape": list(s.shape), "group": s.group}
                 for s in self.slots]

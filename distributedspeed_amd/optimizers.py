@@ -15,6 +15,9 @@ state_dict / load_state_dict, and a step that runs entirely on the GPU:
 
 with no host synchronisation. Parameters are re-homed into one
 FlatPartition at construction (param.data / param.grad become views).
+MultiTensorAdamWOptimizer is the same optimizer over parameters left in
+their own storage (K1 and K3 over a chunk table instead of K1 and K2 over
+one buffer), for zero_optimization.contiguous_gradients = false.
 With graph=True the three stages are captured into one HIP graph at the
 first step and replayed afterwards (K0 then reads the per-group values from
 device memory; see graph.py).
@@ -31,26 +34,34 @@ from ._lib import DSX_MAX_GROUPS, DsxAdamwHyper
 from .flat import FlatPartition
 from .flat_step import BiasCorrectionTable, ScalerConfig
 from .offload import HostStateStreamer
+from .ragged import RaggedParams
 
 
-class AdamWOptimizer(torch.optim.Optimizer):
-    def __init__(self, params: Iterable, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
-                 weight_decay: float = 1e-2, *, max_grad_norm: float = 0.0, param_dtype: torch.dtype | None = None,
-                 loss_scaler: ScalerConfig | None = None, device: torch.device | None = None,
-                 param_names: dict | None = None, offload: bool = False, offload_chunk_elems: int = 64 << 20,
-                 graph: bool = False):
-        if not 0.0 <= lr:
-            raise ValueError(f"Invalid learning rate: {lr}")
-        if not 0.0 <= eps:
-            raise ValueError(f"Invalid epsilon value: {eps}")
-        if not 0.0 <= betas[0] < 1.0:
-            raise ValueError(f"Invalid beta parameter at index 0: {betas[0]}")
-        if not 0.0 <= betas[1] < 1.0:
-            raise ValueError(f"Invalid beta parameter at index 1: {betas[1]}")
-        if not 0.0 <= weight_decay:
-            raise ValueError(f"Invalid weight_decay value: {weight_decay}")
-        if math.isnan(max_grad_norm) or max_grad_norm < 0:
-            raise ValueError(f"Invalid max_grad_norm: {max_grad_norm}")
+def _check_hyper(lr, betas, eps, weight_decay, max_grad_norm) -> None:
+    if not 0.0 <= lr:
+        raise ValueError(f"Invalid learning rate: {lr}")
+    if not 0.0 <= eps:
+        raise ValueError(f"Invalid epsilon value: {eps}")
+    if not 0.0 <= betas[0] < 1.0:
+        raise ValueError(f"Invalid beta parameter at index 0: {betas[0]}")
+    if not 0.0 <= betas[1] < 1.0:
+        raise ValueError(f"Invalid beta parameter at index 1: {betas[1]}")
+    if not 0.0 <= weight_decay:
+        raise ValueError(f"Invalid weight_decay value: {weight_decay}")
+    if math.isnan(max_grad_norm) or max_grad_norm < 0:
+        raise ValueError(f"Invalid max_grad_norm: {max_grad_norm}")
+
+
+class _FusedAdamWBase(torch.optim.Optimizer):
+    """What both storage forms share: torch.optim.AdamW's constructor
+    checks and param_groups, the device-resident DsxState / partials /
+    per-group scalars, the bias-correction tables, the readers and the
+    checkpoint format. A subclass provides `store` (the parameter storage:
+    params, numel, views_of, refresh_params16, layout, zero_grad) and
+    step_fused()."""
+
+    def _init_common(self, params, lr, betas, eps, weight_decay, max_grad_norm, loss_scaler, device):
+        _check_hyper(lr, betas, eps, weight_decay, max_grad_norm)
         defaults = dict(lr=lr, betas=tuple(betas), eps=eps, weight_decay=weight_decay)
         super().__init__(params, defaults)
         if len(self.param_groups) > DSX_MAX_GROUPS:
@@ -61,16 +72,14 @@ class AdamWOptimizer(torch.optim.Optimizer):
         if device is None:
             device = plist[0].device if plist[0].is_cuda else torch.device("cuda", torch.cuda.current_device())
         self.device = torch.device(device)
-        if param_dtype is None and plist[0].dtype in (torch.float16, torch.bfloat16):
-            param_dtype = plist[0].dtype
         self.max_grad_norm = float(max_grad_norm)
         self.clip_eps = 1e-6
         self.scaler = loss_scaler or ScalerConfig(mode="none")
         self.scaler.validate()
-        self.flat = FlatPartition([g["params"] for g in self.param_groups], self.device, param_dtype, param_names,
-                                  offload=offload)
-        self.streamer = HostStateStreamer(self.device, offload_chunk_elems) if offload else None
-        self.nparts = ops.suggest_partials(self.flat.numel)
+        return plist
+
+    def _init_device(self, numel: int) -> None:
+        self.nparts = ops.suggest_partials(numel)
         self.partials = torch.zeros(self.nparts, dtype=torch.float64, device=self.device)
         self.dstate = ops.new_state(self.device, self.scaler.init_scale if self.scaler.mode != "none" else 1.0,
                                     self.scaler.hysteresis if self.scaler.mode == "dynamic" else 1)
@@ -78,29 +87,37 @@ class AdamWOptimizer(torch.optim.Optimizer):
         self._bc: dict[tuple[float, float], BiasCorrectionTable] = {}
         self._t_offsets = [0] * len(self.param_groups)
         self.steps_issued = 0
-        if graph and offload:
-            raise ValueError("graph=True needs HBM-resident state (offload=False)")
-        self.use_graph = bool(graph)
-        self._graph = None
-        self._bind_state()
 
     # ---- torch.optim.Optimizer protocol ---------------------------------------------
 
+    @property
+    def dsx_params(self) -> list:
+        """The parameters in step order."""
+        return self.store.params
+
+    @property
+    def numel(self) -> int:
+        return self.store.numel
+
+    def layout(self) -> list[dict]:
+        return self.store.layout()
+
     def _bind_state(self) -> None:
         t_view = self.dstate[12:16].view(torch.int32)  # DsxState.t
-        for i, p in enumerate(self.flat.params):
-            st = self.flat.views_of(i)
+        for i, p in enumerate(self.store.params):
+            st = dict(self.store.views_of(i))
             st["step"] = t_view
             self.state[p] = st
 
     def zero_grad(self, set_to_none: bool = True) -> None:
-        """Zero the flat grad buffer. The grads are views into it, so they are
-        zeroed rather than set to None whatever set_to_none says."""
-        self.flat.zero_grad()
+        """Zero the grads in place. Their storage is what the step reads (flat
+        views, or the addresses in the chunk table), so they are zeroed
+        rather than set to None whatever set_to_none says."""
+        self.store.zero_grad()
 
     def add_param_group(self, param_group: dict) -> None:
-        if getattr(self, "flat", None) is not None:
-            raise NotImplementedError("add_param_group after construction would move the flat partition; "
+        if getattr(self, "store", None) is not None:
+            raise NotImplementedError("add_param_group after construction would move the parameter storage; "
                                       "build the optimizer with all groups")
         super().add_param_group(param_group)
 
@@ -112,8 +129,6 @@ class AdamWOptimizer(torch.optim.Optimizer):
                 loss = closure()
         self.step_fused()
         return loss
-
-    # ---- the fused step -------------------------------------------------------------------
 
     def _hypers(self):
         hs, tabs = [], []
@@ -128,38 +143,6 @@ class AdamWOptimizer(torch.optim.Optimizer):
             tabs.append(self._bc[key])
         bc_len = min(t.length for t in tabs)
         return hs, [t.table for t in tabs], bc_len
-
-    def step_fused(self) -> None:
-        """K1 -> K0 -> K2 on the current stream; no host synchronisation."""
-        self.flat.check_grads_bound()
-        self.steps_issued += 1
-        hs, tables, bc_len = self._hypers()
-        if self.use_graph:
-            # Captured once (first step), replayed after uploading this step's
-            # per-group block; the same kernels, buffers and order as below.
-            if self._graph is None:
-                from .graph import GraphedStep
-                self._graph = GraphedStep(self)
-            self._graph.replay(hs, tables, bc_len)
-            return
-        ops.unscale_norm(self.flat.grad, self.dstate, self.partials, self.nparts)
-        ops.finalize_groups(self.partials, self.nparts, self.dstate, self.scaler.to_c(), hs, tables,
-                            self._t_offsets, bc_len, self.scalars)
-        if self.streamer is not None:
-            # State in pinned host memory: stream it through HBM chunk by chunk.
-            # A skipped step streams too (K2 leaves the chunks unchanged), which
-            # keeps the host free of any wait on the device.
-            pieces = [(a, b, self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES])
-                      for gi, (a, b) in enumerate(self.flat.group_ranges) if b > a]
-            self.streamer.run((self.flat.master, self.flat.exp_avg, self.flat.exp_avg_sq), self.flat.param16,
-                              self.flat.grad, pieces)
-            return
-        for gi in range(len(self.param_groups)):
-            master, m, v, p16, g = self.flat.group_views(gi)
-            if master.numel() == 0:
-                continue
-            sc = self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
-            ops.adamw_flat(master, m, v, p16, g, sc)
 
     # ---- device-side values, read on demand --------------------------------------------------
 
@@ -193,15 +176,15 @@ class AdamWOptimizer(torch.optim.Optimizer):
             idx += len(g["params"])
             groups.append(gd)
         state = {}
-        for i in range(len(self.flat.params)):
-            v = self.flat.views_of(i)
+        for i in range(len(self.store.params)):
+            v = self.store.views_of(i)
             state[i] = {"step": torch.tensor(float(s.t)), "exp_avg": v["exp_avg"].detach().cpu().clone(),
                         "exp_avg_sq": v["exp_avg_sq"].detach().cpu().clone(),
                         "master": v["master"].detach().cpu().clone()}
         return {"state": state, "param_groups": groups,
                 "dsx": {"scale": s.scale, "good_steps": s.good_steps, "hyst_left": s.hyst_left, "t": s.t,
                         "iter": s.iter, "overflow_count": s.overflow_count, "steps_issued": self.steps_issued,
-                        "layout": self.flat.layout(), "scaler": dict(vars(self.scaler))}}
+                        "layout": self.store.layout(), "scaler": dict(vars(self.scaler))}}
 
     def load_state_dict(self, state_dict: dict) -> None:
         groups = state_dict["param_groups"]
@@ -216,10 +199,10 @@ class AdamWOptimizer(torch.optim.Optimizer):
                     g[k] = tuple(v) if k == "betas" else v
         st = state_dict["state"]
         with torch.no_grad():
-            for i in range(len(self.flat.params)):
+            for i in range(len(self.store.params)):
                 if i not in st:
                     continue
-                views = self.flat.views_of(i)
+                views = self.store.views_of(i)
                 for key in ("exp_avg", "exp_avg_sq", "master"):
                     if key in st[i]:
                         src = st[i][key]
@@ -227,8 +210,7 @@ class AdamWOptimizer(torch.optim.Optimizer):
                             raise ValueError(f"state for parameter {i} has shape {tuple(src.shape)}, "
                                              f"expected {tuple(views[key].shape)}")
                         views[key].copy_(src.to(views[key].device, torch.float32))
-            if self.flat.param16 is not None:
-                self.flat.param16.copy_(self.flat.master.to(self.device))
+            self.store.refresh_params16()
         dsx = state_dict.get("dsx")
         t = int(dsx["t"]) if dsx else int(max((float(v["step"]) for v in st.values()), default=0))
         from ._lib import DsxState
@@ -244,14 +226,115 @@ class AdamWOptimizer(torch.optim.Optimizer):
         self._bind_state()
 
 
-def adopt_torch_optimizer(opt: torch.optim.Optimizer, **kwargs) -> AdamWOptimizer:
+class AdamWOptimizer(_FusedAdamWBase):
+    """The flat form: every parameter re-homed into one FlatPartition (the
+    reference's contiguous_gradients layout, Src/zero/stage2.py:108-193)."""
+
+    def __init__(self, params: Iterable, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
+                 weight_decay: float = 1e-2, *, max_grad_norm: float = 0.0, param_dtype: torch.dtype | None = None,
+                 loss_scaler: ScalerConfig | None = None, device: torch.device | None = None,
+                 param_names: dict | None = None, offload: bool = False, offload_chunk_elems: int = 64 << 20,
+                 graph: bool = False):
+        plist = self._init_common(params, lr, betas, eps, weight_decay, max_grad_norm, loss_scaler, device)
+        if param_dtype is None and plist[0].dtype in (torch.float16, torch.bfloat16):
+            param_dtype = plist[0].dtype
+        if graph and offload:
+            raise ValueError("graph=True needs HBM-resident state (offload=False)")
+        self.flat = FlatPartition([g["params"] for g in self.param_groups], self.device, param_dtype, param_names,
+                                  offload=offload)
+        self.store = self.flat
+        self.streamer = HostStateStreamer(self.device, offload_chunk_elems) if offload else None
+        self._init_device(self.flat.numel)
+        self.use_graph = bool(graph)
+        self._graph = None
+        self._bind_state()
+
+    def launch_norm(self) -> None:
+        """K1 alone over the current grads (partials <- squared norms)."""
+        self.flat.check_grads_bound()
+        ops.unscale_norm(self.flat.grad, self.dstate, self.partials, self.nparts)
+
+    def step_fused(self) -> None:
+        """K1 -> K0 -> K2 on the current stream; no host synchronisation."""
+        self.flat.check_grads_bound()
+        self.steps_issued += 1
+        hs, tables, bc_len = self._hypers()
+        if self.use_graph:
+            # Captured once (first step), replayed after uploading this step's
+            # per-group block; the same kernels, buffers and order as below.
+            if self._graph is None:
+                from .graph import GraphedStep
+                self._graph = GraphedStep(self)
+            self._graph.replay(hs, tables, bc_len)
+            return
+        ops.unscale_norm(self.flat.grad, self.dstate, self.partials, self.nparts)
+        ops.finalize_groups(self.partials, self.nparts, self.dstate, self.scaler.to_c(), hs, tables,
+                            self._t_offsets, bc_len, self.scalars)
+        if self.streamer is not None:
+            # State in pinned host memory: stream it through HBM chunk by chunk.
+            # A skipped step streams too (K2 leaves the chunks unchanged), which
+            # keeps the host free of any wait on the device.
+            pieces = [(a, b, self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES])
+                      for gi, (a, b) in enumerate(self.flat.group_ranges) if b > a]
+            self.streamer.run((self.flat.master, self.flat.exp_avg, self.flat.exp_avg_sq), self.flat.param16,
+                              self.flat.grad, pieces)
+            return
+        for gi in range(len(self.param_groups)):
+            master, m, v, p16, g = self.flat.group_views(gi)
+            if master.numel() == 0:
+                continue
+            sc = self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
+            ops.adamw_flat(master, m, v, p16, g, sc)
+
+
+
+class MultiTensorAdamWOptimizer(_FusedAdamWBase):
+    """The ragged form: parameters keep their own storage and autograd's
+    grads; the step runs over the tensor list through a chunk table (K1 over
+    the list, K0, K3), two streaming launches whatever the number of tensors.
+    Chosen by zero_optimization.contiguous_gradients = false."""
+
+    def __init__(self, params: Iterable, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
+                 weight_decay: float = 1e-2, *, max_grad_norm: float = 0.0, param_dtype: torch.dtype | None = None,
+                 loss_scaler: ScalerConfig | None = None, device: torch.device | None = None,
+                 param_names: dict | None = None, chunk_elems: int = 65536, offload: bool = False,
+                 graph: bool = False):
+        if offload or graph:
+            raise ValueError("offload and graph capture need the flat form (contiguous_gradients = true)")
+        plist = self._init_common(params, lr, betas, eps, weight_decay, max_grad_norm, loss_scaler, device)
+        if param_dtype is None and plist[0].dtype in (torch.float16, torch.bfloat16):
+            param_dtype = plist[0].dtype
+        self.store = RaggedParams([g["params"] for g in self.param_groups], self.device, param_dtype, param_names,
+                                  chunk_elems)
+        self.streamer = None
+        self.use_graph = False
+        self._graph = None
+        self._init_device(self.store.numel)
+        self._bind_state()
+
+    def launch_norm(self) -> None:
+        ops.unscale_norm_multi(self.store.table(), self.dstate, self.partials, self.nparts)
+
+    def step_fused(self) -> None:
+        """K1 (list) -> K0 -> K3 on the current stream; no host synchronisation
+        (a chunk-table rebuild, after storage moved, uploads the new table)."""
+        table = self.store.table()
+        self.steps_issued += 1
+        hs, tables, bc_len = self._hypers()
+        ops.unscale_norm_multi(table, self.dstate, self.partials, self.nparts)
+        ops.finalize_groups(self.partials, self.nparts, self.dstate, self.scaler.to_c(), hs, tables,
+                            self._t_offsets, bc_len, self.scalars)
+        ops.adamw_multi(table, self.scalars)
+
+
+def adopt_torch_optimizer(opt: torch.optim.Optimizer, contiguous: bool = True, **kwargs) -> _FusedAdamWBase:
     """torch.optim.AdamW (or Adam without weight decay, where Adam and AdamW
     coincide) -> AdamWOptimizer over the same param groups and
     hyper-parameters. Anything else is refused rather than silently changed
     into a different update rule."""
     if not isinstance(opt, torch.optim.Optimizer):
         raise TypeError(f"expected a torch.optim.Optimizer, got {type(opt).__name__}")
-    if isinstance(opt, AdamWOptimizer):
+    if isinstance(opt, _FusedAdamWBase):
         return opt
     is_adamw = isinstance(opt, torch.optim.AdamW) or (isinstance(opt, torch.optim.Adam)
                                                       and opt.defaults.get("decoupled_weight_decay", False))
@@ -264,5 +347,5 @@ def adopt_torch_optimizer(opt: torch.optim.Optimizer, **kwargs) -> AdamWOptimize
     groups = [{k: v for k, v in g.items() if k in ("params", "lr", "betas", "eps", "weight_decay")}
               for g in opt.param_groups]
     d = opt.defaults
-    return AdamWOptimizer(groups, lr=float(d["lr"]), betas=d["betas"], eps=d["eps"], weight_decay=d["weight_decay"],
-                          **kwargs)
+    cls = AdamWOptimizer if contiguous else MultiTensorAdamWOptimizer
+    return cls(groups, lr=float(d["lr"]), betas=d["betas"], eps=d["eps"], weight_decay=d["weight_decay"], **kwargs)

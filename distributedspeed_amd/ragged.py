@@ -1,0 +1,119 @@
+"""Parameters left where they lie: the ragged-list form of the step (K3).
+
+With `zero_optimization.contiguous_gradients: false` the reference keeps each
+parameter's grad as its own tensor and steps them one by one (torch
+AdamW's per-tensor loop, Src/zero/stage1.py:522-525); here every parameter
+keeps its own storage and its own autograd-allocated grad, and the step runs
+over the list through a device chunk table (dsx_unscale_norm_multi /
+dsx_adamw_multi): one launch each for the norm and the update whatever the
+number of tensors.
+
+Per parameter: master / exp_avg / exp_avg_sq are fp32 tensors of the
+parameter's shape owned here; with a 16-bit param dtype, param.data is the
+16-bit copy K3 writes, and with fp32 training param.data is the master
+itself. The chunk table holds raw addresses, so it is rebuilt whenever a
+param's or a grad's storage has moved (checked every step on the host).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+
+class RaggedParams:
+    def __init__(self, groups: list[list[torch.nn.Parameter]], device: torch.device,
+                 param_dtype: torch.dtype | None, names: dict | None = None, chunk_elems: int = 65536):
+        if param_dtype not in (None, torch.float16, torch.bfloat16):
+            raise ValueError(f"param_dtype must be float16, bfloat16 or None, got {param_dtype}")
+        names = names or {}
+        self.device = torch.device(device)
+        self.param_dtype = param_dtype
+        self.grad_dtype = param_dtype or torch.float32
+        self.chunk_elems = int(chunk_elems)
+        self.params: list[torch.nn.Parameter] = []
+        self.group_of: list[int] = []
+        self.names: list[str] = []
+        self.master: list[torch.Tensor] = []
+        self.exp_avg: list[torch.Tensor] = []
+        self.exp_avg_sq: list[torch.Tensor] = []
+        seen = set()
+        with torch.no_grad():
+            for gi, plist in enumerate(groups):
+                for p in plist:
+                    if id(p) in seen:
+                        raise ValueError("a parameter appears in more than one group")
+                    seen.add(id(p))
+                    src = p.detach()
+                    if param_dtype is None:
+                        if src.dtype != torch.float32:
+                            raise ValueError(f"fp32 training needs fp32 parameters, got {src.dtype}")
+                        master = src.to(self.device).contiguous().clone()
+                        p.data = master
+                    else:
+                        master = src.to(self.device, torch.float32).contiguous().clone()
+                        p.data = master.to(param_dtype)  # round to nearest even
+                    self.params.append(p)
+                    self.group_of.append(gi)
+                    self.names.append(names.get(id(p), f"param{len(self.params) - 1}"))
+                    self.master.append(master)
+                    self.exp_avg.append(torch.zeros_like(master))
+                    self.exp_avg_sq.append(torch.zeros_like(master))
+                    if p.grad is not None:
+                        p.grad = p.grad.to(self.device, self.grad_dtype).contiguous()
+        self.numel = sum(m.numel() for m in self.master)
+        self.ngroups = len(groups)
+        self._table = None
+        self._key = None
+
+    def ensure_grads(self) -> None:
+        """Give every param a contiguous grad of the grad dtype on the device
+        (zeros where autograd produced none, as the flat form does)."""
+        for p in self.params:
+            g = p.grad
+            if g is None:
+                p.grad = torch.zeros_like(p, dtype=self.grad_dtype)
+            elif g.dtype != self.grad_dtype or g.device != self.device or not g.is_contiguous():
+                p.grad = g.to(self.device, self.grad_dtype).contiguous()
+
+    def table(self) -> ops.ChunkTable:
+        """The device chunk table for the current storage (rebuilt only when
+        a param's or a grad's address changed)."""
+        self.ensure_grads()
+        key = tuple((p.data.data_ptr(), p.grad.data_ptr()) for p in self.params)
+        if key != self._key:
+            for p, m in zip(self.params, self.master):
+                if p.data.shape != m.shape or (self.param_dtype is None and p.data.data_ptr() != m.data_ptr()):
+                    raise RuntimeError("a parameter's storage was replaced after the optimizer was built")
+                if self.param_dtype is not None and (p.dtype != self.param_dtype or not p.data.is_contiguous()):
+                    raise RuntimeError("a parameter's dtype or layout was changed after the optimizer was built")
+            p16 = None if self.param_dtype is None else [p.data for p in self.params]
+            self._table = ops.ChunkTable(self.master, self.exp_avg, self.exp_avg_sq, p16,
+                                         [p.grad for p in self.params], self.group_of, self.chunk_elems)
+            self._key = key
+        return self._table
+
+    def zero_grad(self) -> None:
+        """Zero the grads in place (their addresses, and so the chunk table,
+        stay valid)."""
+        gs = [p.grad for p in self.params if p.grad is not None]
+        if gs:
+            torch._foreach_zero_(gs)
+
+    def views_of(self, i: int) -> dict:
+        return {"master": self.master[i], "exp_avg": self.exp_avg[i], "exp_avg_sq": self.exp_avg_sq[i]}
+
+    def refresh_params16(self) -> None:
+        """param.data <- master (RNE), after the master was loaded."""
+        if self.param_dtype is None:
+            return
+        with torch.no_grad():
+            for p, m in zip(self.params, self.master):
+                p.data.copy_(m)
+
+    def layout(self) -> list[dict]:
+        out, off = [], 0
+        for p, name, gi in zip(self.params, self.names, self.group_of):
+            out.append({"name": name, "offset": off, "numel": p.numel(), "shape": list(p.shape), "group": gi})
+            off += p.numel()
+        return out

@@ -25,7 +25,7 @@ from typing import Any, Dict, List, Optional
 import torch
 
 from .flat_step import ScalerConfig
-from .optimizers import AdamWOptimizer, adopt_torch_optimizer
+from .optimizers import _FusedAdamWBase, adopt_torch_optimizer
 
 logger = logging.getLogger(__name__)
 
@@ -52,19 +52,20 @@ class ZeROOptimizer:
         self.gradient_accumulation_steps = int(_config_get(config, "gradient_accumulation_steps", 1))
         if self.gradient_accumulation_steps <= 0:
             raise ValueError("gradient_accumulation_steps must be positive")
-        if not isinstance(optimizer, AdamWOptimizer):
+        if not isinstance(optimizer, _FusedAdamWBase):
             optimizer = self._adopt(optimizer, config)
         self.base_optimizer = optimizer
-        self.model_parameters = list(model_parameters) if model_parameters is not None else list(optimizer.flat.params)
+        self.model_parameters = list(model_parameters) if model_parameters is not None else list(optimizer.dsx_params)
         self.param_groups = optimizer.param_groups
         self.current_step = 0
         self.gradient_accumulation_count = 0
         self.timers = {"step_time": 0.0}
 
     @staticmethod
-    def _adopt(opt, config) -> AdamWOptimizer:
+    def _adopt(opt, config) -> _FusedAdamWBase:
         scaler = _config_get(config, "loss_scaler", None)
-        return adopt_torch_optimizer(opt, max_grad_norm=float(_config_get(config, "max_grad_norm", 0.0) or 0.0),
+        return adopt_torch_optimizer(opt, contiguous=bool(_config_get(config, "contiguous_gradients", True)),
+                                     max_grad_norm=float(_config_get(config, "max_grad_norm", 0.0) or 0.0),
                                      loss_scaler=ScalerConfig(**scaler) if isinstance(scaler, dict) else scaler)
 
     # ---- the step --------------------------------------------------------------------------
@@ -109,9 +110,8 @@ class ZeROOptimizer:
     def grad_norm(self) -> torch.Tensor:
         """sqrt(sum of squared unscaled grads) of the current grads, computed
         by K1 into a device tensor (no host sync)."""
-        from . import ops
         opt = self.base_optimizer
-        ops.unscale_norm(opt.flat.grad, opt.dstate, opt.partials, opt.nparts)
+        opt.launch_norm()
         return opt.partials[:opt.nparts].sum().sqrt()
 
     # ---- counters and properties --------------------------------------------------------------
@@ -156,7 +156,7 @@ class ZeROOptimizer:
 
     def __repr__(self) -> str:
         return (f"ZeROOptimizer(stage={self.stage}, world_size=1, parameters={len(self.model_parameters)}, "
-                f"numel={self.base_optimizer.flat.numel})")
+                f"numel={self.base_optimizer.numel})")
 
     def __getattr__(self, name: str):
         if name == "base_optimizer":

@@ -1,0 +1,131 @@
+"""GPU tests of the ragged form (MultiTensorAdamWOptimizer: K1 over a chunk
+table, K0, K3) against the flat form (K1, K0, K2 over one buffer), whose
+parity with the oracle is tested elsewhere. The update is elementwise, so
+the two must agree bit for bit on master / exp_avg / exp_avg_sq / 16-bit
+params and on every skip and loss-scale decision; only the fp64 norm may
+differ in its last bits (the partial sums are grouped differently)."""
+from __future__ import annotations
+
+import sys
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = ((257, 33), (1000,), (64, 64), (5,), (3, 7, 11))
+
+
+def _say(msg):
+    print(f"[gpu-test] {msg}", file=sys.stderr, flush=True)
+
+
+def _pair(gpu, dtype, scaler, shapes=SHAPES):
+    import torch
+    from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
+    out = []
+    for cls in (AdamWOptimizer, MultiTensorAdamWOptimizer):
+        g = torch.Generator().manual_seed(5)
+        ps = [torch.nn.Parameter((torch.randn(s, generator=g) * 0.05).to(gpu)) for s in shapes]
+        groups = [{"params": ps[:2]}, {"params": ps[2:], "lr": 3e-4, "weight_decay": 0.0, "betas": (0.8, 0.95)}]
+        out.append(cls(groups, lr=1e-3, weight_decay=0.01, max_grad_norm=1.0, param_dtype=dtype,
+                       loss_scaler=scaler, device=gpu))
+    return out
+
+
+def _check(flat, rag, tag):
+    import torch
+    for i, p in enumerate(rag.dsx_params):
+        fv, rv = flat.flat.views_of(i), rag.store.views_of(i)
+        for k in ("master", "exp_avg", "exp_avg_sq"):
+            assert torch.equal(fv[k].view(torch.int32), rv[k].view(torch.int32)), f"{tag}: {k}[{i}]"
+        fp = flat.dsx_params[i]
+        if p.dtype != torch.float32:
+            assert torch.equal(fp.detach().view(torch.int16), p.detach().view(torch.int16)), f"{tag}: param16[{i}]"
+    a, b = flat.read_state(), rag.read_state()
+    for k in ("scale", "good_steps", "hyst_left", "t", "iter", "overflow_count", "error", "last_skip"):
+        assert getattr(a, k) == getattr(b, k), f"{tag}: state.{k} {getattr(a, k)} vs {getattr(b, k)}"
+    assert abs(a.last_norm - b.last_norm) <= 1e-12 * max(a.last_norm, 1e-30) or a.last_norm == b.last_norm
+
+
+def _set_grads(flat, rag, gen, scale, dtype, inf_at=None):
+    import torch
+    for i, (pf, pr) in enumerate(zip(flat.dsx_params, rag.dsx_params)):
+        g = (torch.randn(pf.shape, generator=gen, device=pf.device) * 1e-2 * scale).to(dtype)
+        if inf_at == i:
+            g.view(-1)[g.numel() // 2] = float("inf")
+        pf.grad.copy_(g)  # the flat form's grads are views into its buffer
+        pr.grad = g.clone()  # the ragged form takes autograd-style fresh tensors
+
+
+@pytest.mark.parametrize("dtype_name", ["float16", "bfloat16", "float32"])
+def test_ragged_matches_flat(gpu, dtype_name):
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    dtype = getattr(torch, dtype_name)
+    _say(f"ragged vs flat {dtype_name}")
+    sc = (ScalerConfig(mode="dynamic", init_scale=2.0 ** 12, window=4, hysteresis=2)
+          if dtype == torch.float16 else ScalerConfig(mode="none"))
+    flat, rag = _pair(gpu, None if dtype == torch.float32 else dtype, sc)
+    gen = torch.Generator(device=gpu).manual_seed(2)
+    for step in range(12):
+        scale = float(flat.read_state().scale)
+        inf_at = (step % 5) if (dtype == torch.float16 and step in (3, 4, 8)) else None
+        _set_grads(flat, rag, gen, scale if dtype == torch.float16 else 1.0, flat.flat.grad.dtype, inf_at)
+        for o in (flat, rag):
+            o.param_groups[1]["lr"] = 3e-4 * (1 + step)
+            o.step()
+        _check(flat, rag, f"step {step}")
+    st = rag.read_state()
+    assert st.t == (9 if dtype == torch.float16 else 12)
+
+
+def test_ragged_misaligned_grads_and_table_rebuild(gpu):
+    """Grads at odd element offsets take the kernels' unaligned paths; a
+    grad replaced between steps moves storage and rebuilds the table."""
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    _say("ragged misaligned + rebuild")
+    flat, rag = _pair(gpu, torch.bfloat16, ScalerConfig(mode="none"))
+    gen = torch.Generator(device=gpu).manual_seed(9)
+    keys = set()
+    for step in range(4):
+        _set_grads(flat, rag, gen, 1.0, torch.bfloat16)
+        if step % 2:
+            big = torch.empty(sum(p.numel() for p in rag.dsx_params) + 8, dtype=torch.bfloat16, device=gpu)
+            off = 1
+            for p in rag.dsx_params:
+                v = big[off:off + p.numel()].view(p.shape)
+                v.copy_(p.grad)
+                p.grad = v
+                off += p.numel() + 1
+        for o in (flat, rag):
+            o.step()
+        keys.add(rag.store._key)
+        _check(flat, rag, f"step {step}")
+    assert len(keys) == 4
+
+
+def test_engine_non_contiguous_gradients_matches_contiguous(gpu):
+    import torch
+    import distributedspeed_amd as ds
+    _say("engine contiguous_gradients false")
+    base = {"train_batch_size": 8, "optimizer": {"type": "AdamW", "params": {"lr": 1e-3}},
+            "fp16": {"enabled": True, "initial_scale_power": 12}, "max_grad_norm": 1.0}
+    opts = []
+    for contiguous in (True, False):
+        torch.manual_seed(0)
+        model = torch.nn.Sequential(torch.nn.Linear(64, 128), torch.nn.GELU(), torch.nn.Linear(128, 8))
+        cfg = dict(base, zero_optimization={"stage": 2, "contiguous_gradients": contiguous})
+        engine, opt, _, _ = ds.initialize(model, cfg)
+        gen = torch.Generator(device=gpu).manual_seed(1)
+        for _ in range(5):
+            x = torch.randn(8, 64, device=gpu, generator=gen)
+            loss = engine(x).float().pow(2).mean()
+            engine.backward(loss)
+            engine.step()
+        torch.cuda.synchronize()
+        opts.append(opt.base_optimizer)
+    from distributedspeed_amd.optimizers import MultiTensorAdamWOptimizer
+    assert isinstance(opts[1], MultiTensorAdamWOptimizer) and not isinstance(opts[0], MultiTensorAdamWOptimizer)
+    _check(opts[0], opts[1], "engine")
+    assert opts[1].read_state().t == 5

@@ -219,3 +219,39 @@ def test_pack_groups_checks_on_host():
     with pytest.raises(ValueError, match="groups"):
         ops.pack_groups([], [], [], 4)
     assert ops.GROUPS_BYTES == 1112
+
+
+# ---- ragged parameter store (CPU tensors) ------------------------------------------------
+
+def test_ragged_store_keeps_storage_and_masters():
+    from distributedspeed_amd.ragged import RaggedParams
+    ps = _params([(3, 5), (7,), (4, 4)])
+    orig = [p.detach().clone() for p in ps]
+    rp = RaggedParams([ps[:1], ps[1:]], torch.device("cpu"), torch.float16, {id(ps[1]): "b"})
+    assert rp.numel == 15 + 7 + 16 and rp.group_of == [0, 1, 1]
+    for p, o, m in zip(ps, orig, rp.master):
+        assert p.dtype == torch.float16 and m.dtype == torch.float32
+        assert torch.equal(m, o) and torch.equal(p.detach(), o.to(torch.float16))
+        assert p.data_ptr() != m.data_ptr()
+    assert [e["name"] for e in rp.layout()] == ["param0", "b", "param2"]
+    assert [e["offset"] for e in rp.layout()] == [0, 15, 22]
+    rp.ensure_grads()
+    assert all(p.grad is not None and p.grad.dtype == torch.float16 and float(p.grad.abs().sum()) == 0 for p in ps)
+    ps[0].grad = torch.ones(5, 3, dtype=torch.float16).t()  # a strided grad is made contiguous
+    rp.ensure_grads()
+    assert ps[0].grad.is_contiguous() and float(ps[0].grad.sum()) == 15
+    rp.zero_grad()
+    assert float(ps[0].grad.abs().sum()) == 0
+    rp.master[1].fill_(1.0 + 2 ** -12)  # rounds to 1.0 in fp16 (RNE, tie to even)
+    rp.refresh_params16()
+    assert torch.equal(ps[1].detach(), torch.ones(7, dtype=torch.float16))
+
+
+def test_ragged_store_fp32_master_is_the_param():
+    from distributedspeed_amd.ragged import RaggedParams
+    ps = _params([(5,), (2, 3)])
+    rp = RaggedParams([ps], torch.device("cpu"), None)
+    for p, m in zip(ps, rp.master):
+        assert p.data_ptr() == m.data_ptr() and p.dtype == torch.float32
+    with pytest.raises(ValueError):
+        RaggedParams([[torch.nn.Parameter(torch.zeros(2, dtype=torch.float16))]], torch.device("cpu"), None)
