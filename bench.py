@@ -40,9 +40,12 @@ def _args():
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                       "k2_adamw_flat_llama8b_shard_traffic.json"))
     ap.add_argument("--tuning", default="", help="k1_bpc,k2_bpc,k2_unroll,nt (library launch-shape override)")
-    ap.add_argument("--workload", default="llama8b-shard", choices=["llama8b-shard", "llama-ragged", "llama70b-offload"],
+    ap.add_argument("--workload", default="llama8b-shard",
+                    choices=["llama8b-shard", "llama-ragged", "llama70b-offload", "gpt2-small", "mlp"],
                     help="llama8b-shard: the headline flat step (K1/K0/K2); llama-ragged: configs[3]'s 289-tensor "
-                         "list through K3 (a secondary line, not the headline)")
+                         "list through K3; llama70b-offload: configs[4] with state in pinned host memory; "
+                         "gpt2-small / mlp: configs[1] / configs[0] through the drop-in optimizer classes, eager, "
+                         "graph-replayed and ragged (secondary lines, not the headline)")
     ap.add_argument("--pinned-budget-gib", type=float, default=32.0,
                     help="llama70b-offload: pinned host memory for the fp32 state (the shard shrinks to fit)")
     ap.add_argument("--profile-kernels", action="store_true",
@@ -109,6 +112,91 @@ def llama_ragged_shapes():
         shapes += [(4096, 4096)] * 4 + [(4096, 14336)] * 2 + [(14336, 4096)] + [(4096,)] * 2
     shapes.append((128256, 4096))
     return shapes
+
+
+def gpt2_small_shapes():
+    """configs[1]: wte, wpe, 12 x {ln_1 w,b; c_attn w,b; attn c_proj w,b;
+    ln_2 w,b; c_fc w,b; mlp c_proj w,b}, ln_f w,b -- 148 tensors,
+    124,439,808 elements."""
+    d, ff, vocab, ctx = 768, 3072, 50257, 1024
+    shapes = [(vocab, d), (ctx, d)]
+    for _ in range(12):
+        shapes += [(d,), (d,), (d, 3 * d), (3 * d,), (d, d), (d,), (d,), (d,), (d, ff), (ff,), (ff, d), (d,)]
+    return shapes + [(d,), (d,)]
+
+
+def mlp_shapes():
+    """784x1024, 1024, 1024x1024, 1024, 1024x10, 10 -- 1,863,690 elements."""
+    return [(1024, 784), (1024,), (1024, 1024), (1024,), (10, 1024), (10,)]
+
+
+def bench_dropin(a, dev) -> int:
+    """configs[0] (mlp) or configs[1] (gpt2-small) through the drop-in
+    optimizer classes, Python host code included: the flat form eager, the
+    flat form replayed as a HIP graph, and the ragged form (K3). These
+    partitions are small enough that launch and host overhead matter, which
+    is what the three modes show. fp16 params and grads; gpt2-small: grads
+    N(0, 1e-3^2) x 2^16, dynamic scaler (init 2^16, window 1000), clip 1.0;
+    mlp: grads N(0, 0.01^2) x 2^16, static scale 2^16, no clip."""
+    import math
+
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
+    gpt2 = a.workload == "gpt2-small"
+    shapes = gpt2_small_shapes() if gpt2 else mlp_shapes()
+    n = sum(math.prod(s) for s in shapes)
+    if gpt2:
+        sc = ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, window=1000, hysteresis=1, min_scale=1.0)
+        sigma, clip, kw = 1e-3, 1.0, dict(lr=6e-4, weight_decay=0.01)
+    else:
+        sc = ScalerConfig(mode="static", init_scale=2.0 ** 16)
+        sigma, clip, kw = 0.01, 0.0, dict(lr=1e-4, weight_decay=0.01)
+    modes = {}
+    for name, cls, extra in (("flat_eager", AdamWOptimizer, {}), ("flat_graph", AdamWOptimizer, {"graph": True}),
+                             ("ragged_eager", MultiTensorAdamWOptimizer, {})):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1)
+        ps = [torch.nn.Parameter(torch.empty(s, device=dev).normal_(0.0, 0.02, generator=gen)) for s in shapes]
+        opt = cls(ps, max_grad_norm=clip, param_dtype=torch.float16, loss_scaler=sc, device=dev, **kw, **extra)
+        for p in opt.dsx_params:
+            g = torch.empty(p.shape, device=dev).normal_(0.0, sigma, generator=gen).mul_(2.0 ** 16)
+            if p.grad is None:
+                p.grad = g.to(torch.float16)
+            else:
+                p.grad.copy_(g)
+        for _ in range(a.warmup):
+            opt.step()
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        s0.record()
+        for _ in range(a.steps):
+            opt.step()
+        t_issue = time.perf_counter() - t0
+        s1.record()
+        torch.cuda.synchronize()
+        ms = s0.elapsed_time(s1) / a.steps
+        st = opt.read_state()
+        if st.error or st.last_skip:
+            print(json.dumps({"error": f"{name}: state error={st.error} skip={st.last_skip}"}))
+            return 1
+        modes[name] = {"ms_per_step": round(ms, 4), "gparam_per_s": round(n / ms / 1e6, 3),
+                       "host_issue_us_per_step": round(t_issue / a.steps * 1e6, 1),
+                       "achieved_tbps": round(30 * n / ms / 1e9, 4)}
+        _progress(f"{name}: {modes[name]}")
+        del opt, ps
+        torch.cuda.empty_cache()
+    best = max(modes, key=lambda k: modes[k]["gparam_per_s"])
+    print(json.dumps({
+        "metric": f"drop-in optimizer step Gparam/s ({'configs[1]' if gpt2 else 'configs[0]'})",
+        "value": modes[best]["gparam_per_s"], "unit": "Gparam/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": modes[best]["ms_per_step"], "higher_is_better": True,
+        "dtype": "f32 state / fp16 grads+params", "data": "synthetic",
+        "config": {"workload": "gpt2-small fp16 (BASELINE configs[1])" if gpt2 else "mlp fp16 (BASELINE configs[0])",
+                   "tensors": len(shapes), "numel": n, "best_mode": best},
+        "modes": modes}), flush=True)
+    return 0
 
 
 def bench_ragged(a, dev) -> int:
@@ -359,6 +447,8 @@ def main() -> int:
         return bench_ragged(a, dev)
     if a.workload == "llama70b-offload":
         return bench_offload(a, dev)
+    if a.workload in ("gpt2-small", "mlp"):
+        return bench_dropin(a, dev)
     hyper = AdamWHyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     _progress(f"generating {n} elements")
     master, exp_avg, exp_avg_sq, p16, grad = make_inputs(n, 2, dev)

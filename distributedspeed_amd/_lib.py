@@ -75,6 +75,7 @@ for _s, _n in ((DsxState, 64), (DsxScalerConfig, 32), (DsxAdamwHyper, 56), (DsxS
 SIGNATURES = {
     "dsx_abi_version": (_c.c_int, []),
     "dsx_last_error": (_c.c_char_p, []),
+    "dsx_set_tuning_multi": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int]),
     "dsx_set_tuning": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int]),
     "dsx_suggest_partials": (_c.c_int32, [_c.c_int64]),
     "dsx_count_chunks": (_c.c_int64, [_P, _c.c_int32, _c.c_int64]),
@@ -85,6 +86,7 @@ SIGNATURES = {
     "dsx_finalize_groups": (_c.c_int, [_P, _c.c_int32, _P, DsxScalerConfig, _P, _P, _P, _c.c_int32, _c.c_int32,
                                        _P, _P]),
     "dsx_finalize_dev": (_c.c_int, [_P, _c.c_int32, _P, DsxScalerConfig, _P, _c.c_int32, _P, _P]),
+    "dsx_groups_upload": (_c.c_int, [_P, _P, _P]),
     "dsx_adamw_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, _P]),
     "dsx_zero_step_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, DsxScalerConfig,
                                       DsxAdamwHyper, _P, _c.c_int32, _P, _c.c_int32, _P, _P]),

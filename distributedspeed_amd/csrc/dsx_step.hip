@@ -76,6 +76,9 @@ struct Tuning {
   int k2_blocks_per_cu = 1;
   int k2_unroll = 4;      // slots per thread per trip: 2, 4 or 8
   int nontemporal = 1;    // nontemporal hint on the streaming loads/stores
+  int k3_blocks_per_cu = 0;  // 0: chosen per launch from the chunk count
+  int k3_unroll = 1;         // slots per thread per trip in K3: 1, 2 or 4 (when not chosen)
+  int k3_nontemporal = 1;
 };
 Tuning g_tune;
 
@@ -413,6 +416,16 @@ __global__ __launch_bounds__(kBlock) void k0_finalize_dev(const double* __restri
   finalize_body(sumsq, state, scfg, grp, bad, max_groups, out);
 }
 
+// Writes a group block passed by value (through the kernel-argument
+// segment, so no DMA copy and no host staging buffer) to device memory,
+// 8 bytes per lane.
+__global__ __launch_bounds__(64) void k_store_groups(DsxGroupsDev g, DsxGroupsDev* __restrict__ dst) {
+  static_assert(sizeof(DsxGroupsDev) % 8 == 0, "DsxGroupsDev is stored in 8-byte words");
+  const uint64_t* src = reinterpret_cast<const uint64_t*>(&g);
+  uint64_t* out = reinterpret_cast<uint64_t*>(dst);
+  for (int i = threadIdx.x; i < (int)(sizeof(DsxGroupsDev) / 8); i += 64) out[i] = src[i];
+}
+
 __global__ void k_state_init(DsxState* state, float scale, int32_t hysteresis) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
     DsxState s = {};
@@ -523,7 +536,7 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorR
   if (threadIdx.x == 0) partials[blockIdx.x] = s;
 }
 
-template <int GD, int PD>
+template <int GD, int PD, int U, bool NT>
 __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __restrict__ tensors,
                                                          const DsxChunk* __restrict__ chunks, int64_t nchunks,
                                                          const DsxStepScalars* __restrict__ scalars) {
@@ -554,15 +567,35 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __r
       u2* o2 = reinterpret_cast<u2*>(p16);
       const GS* g4 = reinterpret_cast<const GS*>(g);
       const int64_t nvec = len >> 2;
-      // plain loads/stores: on the 8.3e9-element ragged list nontemporal
-      // hints measured ~5% slower here
-      for (int64_t i = threadIdx.x; i < nvec; i += kBlock) {
-        float gf[4];
-        G::four(g4[i], gf);
-        f4 pp = p4[i], mm = m4[i], vv = v4[i];
-        adamw4(gf, pp, mm, vv, s);
-        p4[i] = pp; m4[i] = mm; v4[i] = vv;
-        if (cast) o2[i] = pack4<PD>(pp);
+      // U slots per thread: all loads of a trip are issued before any use,
+      // as in k2_adamw_flat.
+      for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += (int64_t)kBlock * U) {
+        GS Gs[U];
+        f4 P[U], M[U], V[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t i = i0 + (int64_t)u * kBlock;
+          if (i < nvec) {
+            Gs[u] = ld<NT>(g4 + i);
+            P[u] = ld<NT>(p4 + i);
+            M[u] = ld<NT>(m4 + i);
+            V[u] = ld<NT>(v4 + i);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t i = i0 + (int64_t)u * kBlock;
+          if (i < nvec) {
+            float gf[4];
+            G::four(Gs[u], gf);
+            f4 pp = P[u], mm = M[u], vv = V[u];
+            adamw4(gf, pp, mm, vv, s);
+            st<NT>(p4 + i, pp);
+            st<NT>(m4 + i, mm);
+            st<NT>(v4 + i, vv);
+            if (cast) st<NT>(o2 + i, pack4<PD>(pp));
+          }
+        }
       }
       done = nvec << 2;
     }
@@ -703,13 +736,30 @@ int do_adamw_flat(float* p, float* m, float* v, void* p16, int pdt, const void* 
   return launch_status("dsx_adamw_flat");
 }
 
-template <int GD>
-void launch_k3(int pd, dim3 grid, const DsxTensorRef* t, const DsxChunk* c, int64_t nc, const DsxStepScalars* sc,
-               hipStream_t s) {
-  if (pd == DSX_BF16)
-    hipLaunchKernelGGL((k2_adamw_multi<GD, DSX_BF16>), grid, dim3(kBlock), 0, s, t, c, nc, sc);
+template <int GD, int PD, int U>
+void launch_k3_u(dim3 grid, const DsxTensorRef* t, const DsxChunk* c, int64_t nc, const DsxStepScalars* sc,
+                 hipStream_t s) {
+  if (g_tune.k3_nontemporal)
+    hipLaunchKernelGGL((k2_adamw_multi<GD, PD, U, true>), grid, dim3(kBlock), 0, s, t, c, nc, sc);
   else
-    hipLaunchKernelGGL((k2_adamw_multi<GD, DSX_F16>), grid, dim3(kBlock), 0, s, t, c, nc, sc);
+    hipLaunchKernelGGL((k2_adamw_multi<GD, PD, U, false>), grid, dim3(kBlock), 0, s, t, c, nc, sc);
+}
+
+template <int GD, int PD>
+void launch_k3_p(int unroll, dim3 grid, const DsxTensorRef* t, const DsxChunk* c, int64_t nc,
+                 const DsxStepScalars* sc, hipStream_t s) {
+  switch (unroll) {
+    case 1: launch_k3_u<GD, PD, 1>(grid, t, c, nc, sc, s); break;
+    case 4: launch_k3_u<GD, PD, 4>(grid, t, c, nc, sc, s); break;
+    default: launch_k3_u<GD, PD, 2>(grid, t, c, nc, sc, s); break;
+  }
+}
+
+template <int GD>
+void launch_k3(int pd, int unroll, dim3 grid, const DsxTensorRef* t, const DsxChunk* c, int64_t nc,
+               const DsxStepScalars* sc, hipStream_t s) {
+  if (pd == DSX_BF16) launch_k3_p<GD, DSX_BF16>(unroll, grid, t, c, nc, sc, s);
+  else launch_k3_p<GD, DSX_F16>(unroll, grid, t, c, nc, sc, s);
 }
 
 }  // namespace
@@ -730,6 +780,15 @@ int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll, in
   g_tune.k2_blocks_per_cu = k2_blocks_per_cu;
   g_tune.k2_unroll = k2_unroll;
   g_tune.nontemporal = nontemporal ? 1 : 0;
+  return DSX_OK;
+}
+
+int dsx_set_tuning_multi(int k3_blocks_per_cu, int k3_unroll, int nontemporal) {
+  if (k3_blocks_per_cu < 0 || k3_blocks_per_cu > 64) return fail(DSX_EINVAL, "blocks per CU out of range");
+  if (k3_unroll != 1 && k3_unroll != 2 && k3_unroll != 4) return fail(DSX_EINVAL, "k3_unroll must be 1, 2 or 4");
+  g_tune.k3_blocks_per_cu = k3_blocks_per_cu;
+  g_tune.k3_unroll = k3_unroll;
+  g_tune.k3_nontemporal = nontemporal ? 1 : 0;
   return DSX_OK;
 }
 
@@ -848,6 +907,23 @@ int dsx_finalize_dev(const double* partials, int32_t nparts, DsxState* state, Ds
   return launch_status("dsx_finalize_dev");
 }
 
+int dsx_groups_upload(const DsxGroupsDev* groups, DsxGroupsDev* dst, void* stream) {
+  if (!groups || !dst) return fail(DSX_EINVAL, "null group block");
+  if (reinterpret_cast<uintptr_t>(dst) & 7u) return fail(DSX_EINVAL, "dst must be 8-byte aligned");
+  const DsxGroupsDev& g = *groups;
+  if (g.ngroups < 1 || g.ngroups > DSX_MAX_GROUPS)
+    return fail(DSX_EINVAL, "ngroups must be in [1, %d] (got %d)", DSX_MAX_GROUPS, g.ngroups);
+  if (g.bc_len < 0) return fail(DSX_EINVAL, "bad bias-correction table length");
+  for (int k = 0; k < g.ngroups; ++k) {
+    const int rc = check_hyper(g.hyper[k]);
+    if (rc) return rc;
+    if (g.bc_len > 0 && !g.bc_table[k]) return fail(DSX_EINVAL, "null bias-correction table for group %d", k);
+    if (g.t_offset[k] < 0) return fail(DSX_EINVAL, "negative t_offset for group %d", k);
+  }
+  hipLaunchKernelGGL(k_store_groups, dim3(1), dim3(64), 0, as_stream(stream), g, dst);
+  return launch_status("dsx_groups_upload");
+}
+
 int dsx_adamw_flat(float* master, float* exp_avg, float* exp_avg_sq, void* param16, int param_dtype,
                    const void* grad, int grad_dtype, int64_t n, const DsxStepScalars* scalars, void* stream) {
   int rc = check_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n);
@@ -910,14 +986,28 @@ int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t
   if (nchunks < 0 || (nchunks > 0 && (!tensors || !chunks))) return fail(DSX_EINVAL, "bad chunk table");
   if (!scalars) return fail(DSX_EINVAL, "null scalars");
   if (nchunks == 0) return DSX_OK;
-  int64_t blocks = (int64_t)cu_count() * 8;
+  // Chunks are handed out statically (block b takes b, b + grid, ...), so a
+  // list of few chunks per block loses its last, partly filled round. By
+  // default the grid keeps at least 16 rounds (down to one block per CU, which
+  // then takes two slots per trip) and at most 8 blocks per CU; measured on
+  // MI355X, 8 blocks of one slot suit lists of 1e5 chunks and one block of
+  // two slots lists of ~1e4.
+  const int64_t cus = cu_count();
+  int64_t bpc = g_tune.k3_blocks_per_cu;
+  int unroll = g_tune.k3_unroll;
+  if (bpc == 0) {
+    bpc = nchunks / (cus * 16);
+    bpc = bpc < 1 ? 1 : (bpc > 8 ? 8 : bpc);
+    unroll = bpc <= 2 ? 2 : 1;
+  }
+  int64_t blocks = cus * bpc;
   if (blocks > nchunks) blocks = nchunks;
   hipStream_t s = as_stream(stream);
   const dim3 grid((unsigned)blocks);
   switch (grad_dtype) {
-    case DSX_BF16: launch_k3<DSX_BF16>(param_dtype, grid, tensors, chunks, nchunks, scalars, s); break;
-    case DSX_F16: launch_k3<DSX_F16>(param_dtype, grid, tensors, chunks, nchunks, scalars, s); break;
-    default: launch_k3<DSX_F32>(param_dtype, grid, tensors, chunks, nchunks, scalars, s); break;
+    case DSX_BF16: launch_k3<DSX_BF16>(param_dtype, unroll, grid, tensors, chunks, nchunks, scalars, s); break;
+    case DSX_F16: launch_k3<DSX_F16>(param_dtype, unroll, grid, tensors, chunks, nchunks, scalars, s); break;
+    default: launch_k3<DSX_F32>(param_dtype, unroll, grid, tensors, chunks, nchunks, scalars, s); break;
   }
   return launch_status("dsx_adamw_multi");
 }

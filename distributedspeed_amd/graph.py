@@ -7,84 +7,78 @@ its address for the optimizer's life, so the recorded launches stay valid.
 What changes from step to step -- learning rate and the other per-group
 hyper-parameters a scheduler may set, the bias-correction tables as they
 grow -- lives in a DsxGroupsDev block in device memory, which K0 reads at
-replay time. Before each replay the host packs that block into a pinned
-staging slot and enqueues an async copy on the replay stream; the copy is
-not part of the graph, so nothing in the graph is a memset or a host copy.
+replay time. When those values changed since the last replay, the host
+enqueues dsx_groups_upload before the replay (a one-wave kernel that takes
+the block as its argument: no staging buffer, no DMA copy, no host wait);
+the upload is not part of the graph, and nothing in the graph is a memset
+or a host copy.
+
+A GraphedStep keeps no reference to its optimizer (the optimizer holds the
+GraphedStep), so the pair is freed by reference counting when the optimizer
+goes away, never later by the cyclic garbage collector -- which could
+otherwise destroy a graph in the middle of another graph's capture. The
+capture itself runs with the cyclic collector paused for the same reason.
 
 This path has no counterpart in the reference, which launches the step
 eagerly every iteration (Src/zero/optimizer.py:212-274).
 """
 from __future__ import annotations
 
-import numpy as np
+import gc
+
 import torch
 
 from . import ops
 
 
-class PinnedRing:
-    """A few pinned staging slots for small host->device uploads. A slot is
-    reused only after the copy that last read it has completed (its event),
-    so the host never overwrites bytes a pending copy still needs."""
-
-    def __init__(self, nbytes: int, slots: int = 4):
-        self.bufs = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(slots)]
-        self.events: list[torch.cuda.Event | None] = [None] * slots
-        self.i = 0
-
-    def upload(self, data: bytes, dst: torch.Tensor) -> None:
-        k = self.i
-        self.i = (k + 1) % len(self.bufs)
-        if self.events[k] is not None:
-            self.events[k].synchronize()
-        self.bufs[k].numpy()[:] = np.frombuffer(data, dtype=np.uint8)
-        dst.copy_(self.bufs[k], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(dst.device))
-        self.events[k] = ev
-
-
 class GraphedStep:
-    """Captures `opt`'s fused step (an AdamWOptimizer with HBM-resident
+    """Captures the fused step of `opt` (an AdamWOptimizer with HBM-resident
     state) and replays it. Construction synchronises the device once."""
 
     def __init__(self, opt):
         if opt.streamer is not None:
             raise NotImplementedError("graph capture covers HBM-resident state; the offloaded step streams "
                                       "host chunks under host control")
-        self.opt = opt
         dev = opt.device
+        self.device = dev
         self.ngroups = len(opt.param_groups)
         self.groups_dev = torch.zeros(ops.GROUPS_BYTES, dtype=torch.uint8, device=dev)
-        self.ring = PinnedRing(ops.GROUPS_BYTES)
-        self._warm(dev)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.device(dev), torch.cuda.graph(self.graph):
-            self._record()
+        self._uploaded = None  # the values groups_dev holds
         self.replays = 0
+        self.uploads = 0
+        plans = self._plans(opt)
+        self._warm(opt, dev)
+        self.graph = torch.cuda.CUDAGraph()
+        gc.collect()
+        was_enabled = gc.isenabled()
+        gc.disable()
+        try:
+            with torch.cuda.device(dev), torch.cuda.graph(self.graph):
+                s = ops.stream_of(dev)
+                for launch in plans:
+                    launch(s)
+        finally:
+            if was_enabled:
+                gc.enable()
 
-    def _launches(self):
-        opt = self.opt
-        yield lambda: ops.unscale_norm(opt.flat.grad, opt.dstate, opt.partials, opt.nparts)
-        yield lambda: ops.finalize_dev(opt.partials, opt.nparts, opt.dstate, opt.scaler.to_c(), self.groups_dev,
-                                       self.ngroups, opt.scalars)
+    def _plans(self, opt) -> list:
+        """Every launch of the step, checked and bound before the capture."""
+        plans = [ops.plan_unscale_norm(opt.flat.grad, opt.dstate, opt.partials, opt.nparts),
+                 ops.plan_finalize_dev(opt.partials, opt.nparts, opt.dstate, opt.scaler.to_c(), self.groups_dev,
+                                       self.ngroups, opt.scalars)]
         for gi in range(self.ngroups):
             master, m, v, p16, g = opt.flat.group_views(gi)
-            if master.numel() == 0:
-                continue
-            sc = opt.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
-            yield lambda master=master, m=m, v=v, p16=p16, g=g, sc=sc: ops.adamw_flat(master, m, v, p16, g, sc)
+            if master.numel():
+                sc = opt.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
+                plans.append(ops.plan_adamw_flat(master, m, v, p16, g, sc))
+        return plans
 
-    def _record(self) -> None:
-        for launch in self._launches():
-            launch()
-
-    def _warm(self, dev: torch.device) -> None:
+    @staticmethod
+    def _warm(opt, dev: torch.device) -> None:
         """Launch the same kernel instantiations once, eagerly, on small
         scratch buffers (K0 sees an empty group block and writes skip, so K2
         returns at once), so that loading the code object happens outside
         the capture."""
-        opt = self.opt
         gd = opt.flat.grad.dtype
         pd = opt.flat.param16.dtype if opt.flat.param16 is not None else None
         st = ops.new_state(dev)
@@ -99,10 +93,14 @@ class GraphedStep:
         ops.adamw_flat(f[0], f[1], f[2], p16, g, sc)
         torch.cuda.synchronize(dev)
 
-    def replay(self, hypers, tables, bc_len: int) -> None:
-        """Upload this step's group block, then replay, both on the current
-        stream (no host synchronisation beyond a staging slot's reuse)."""
-        blob = ops.pack_groups(hypers, tables, self.opt._t_offsets, bc_len)
-        self.ring.upload(blob, self.groups_dev)
+    def replay(self, hypers, tables, t_offsets, bc_len: int) -> None:
+        """Upload this step's group block if it differs from the one on the
+        device, then replay, both on the current stream (no host wait)."""
+        key = (tuple((h.lr, h.beta1, h.beta2, h.eps, h.weight_decay, h.max_grad_norm, h.clip_eps) for h in hypers),
+               tuple(t.data_ptr() for t in tables), tuple(t_offsets), int(bc_len))
+        if key != self._uploaded:
+            ops.groups_upload(ops.pack_groups(hypers, tables, t_offsets, bc_len), self.groups_dev)
+            self._uploaded = key
+            self.uploads += 1
         self.graph.replay()
         self.replays += 1

@@ -98,12 +98,36 @@ def scale_view(st: torch.Tensor) -> torch.Tensor:
     return st[0:4].view(torch.float32)
 
 
+class Launch:
+    """One entry point with its arguments checked and bound once; calling it
+    with a stream handle enqueues the launch. For buffers that never move
+    (a flat partition) this takes the per-step host cost down to the ctypes
+    call itself."""
+
+    __slots__ = ("name", "fn", "args")
+
+    def __init__(self, name: str, *args):
+        self.name = name
+        self.fn = getattr(_lib.load(), name)
+        self.args = args
+
+    def __call__(self, stream: ctypes.c_void_p) -> None:
+        rc = self.fn(*self.args, stream)
+        if rc:
+            raise _lib.DsxError(self.name, rc, _lib.last_error())
+
+
+def stream_of(device: torch.device) -> ctypes.c_void_p:
+    """torch's current HIP stream on `device` as the void* the ABI takes."""
+    return _stream(device)
+
+
 def suggest_partials(n: int) -> int:
     return int(_lib.load().dsx_suggest_partials(int(n)))
 
 
-def unscale_norm(grad: torch.Tensor, state: torch.Tensor, partials: torch.Tensor, nparts: int | None = None) -> None:
-    """K1: partials[:nparts] = per-block fp64 sums of (grad * inv_scale)^2."""
+def plan_unscale_norm(grad: torch.Tensor, state: torch.Tensor, partials: torch.Tensor,
+                      nparts: int | None = None) -> Launch:
     dev = _device(grad)
     _need(grad, "grad", None, None, dev)
     gdt = grad_code(grad.dtype)
@@ -112,8 +136,13 @@ def unscale_norm(grad: torch.Tensor, state: torch.Tensor, partials: torch.Tensor
     _need(partials, "partials", torch.float64, None, dev, 8)
     if nparts > partials.numel():
         raise ValueError("nparts exceeds the partials buffer")
-    _lib.call("dsx_unscale_norm", _ptr(grad), gdt, grad.numel(), _ptr(state), _ptr(partials), int(nparts),
-              _stream(dev))
+    return Launch("dsx_unscale_norm", _ptr(grad), gdt, ctypes.c_int64(grad.numel()), _ptr(state), _ptr(partials),
+                  int(nparts))
+
+
+def unscale_norm(grad: torch.Tensor, state: torch.Tensor, partials: torch.Tensor, nparts: int | None = None) -> None:
+    """K1: partials[:nparts] = per-block fp64 sums of (grad * inv_scale)^2."""
+    plan_unscale_norm(grad, state, partials, nparts)(_stream(grad.device))
 
 
 def finalize(partials: torch.Tensor, nparts: int, state: torch.Tensor, scaler: DsxScalerConfig,
@@ -133,6 +162,11 @@ def finalize(partials: torch.Tensor, nparts: int, state: torch.Tensor, scaler: D
 def adamw_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
                param16: torch.Tensor | None, grad: torch.Tensor, scalars: torch.Tensor) -> None:
     """K2: AdamW + 16-bit cast over a flat partition (in place)."""
+    plan_adamw_flat(master, exp_avg, exp_avg_sq, param16, grad, scalars)(_stream(master.device))
+
+
+def plan_adamw_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
+                    param16: torch.Tensor | None, grad: torch.Tensor, scalars: torch.Tensor) -> Launch:
     dev = _device(master)
     n = master.numel()
     for name, t in (("master", master), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
@@ -144,8 +178,8 @@ def adamw_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Te
         _need(param16, "param16", None, n, dev)
         pdt = dtype_code(param16.dtype)
     _need(scalars, "scalars", torch.uint8, SCALARS_BYTES, dev, 8)
-    _lib.call("dsx_adamw_flat", _ptr(master), _ptr(exp_avg), _ptr(exp_avg_sq), _ptr(param16), pdt, _ptr(grad), gdt,
-              n, _ptr(scalars), _stream(dev))
+    return Launch("dsx_adamw_flat", _ptr(master), _ptr(exp_avg), _ptr(exp_avg_sq), _ptr(param16), pdt, _ptr(grad),
+                  gdt, ctypes.c_int64(n), _ptr(scalars))
 
 
 def zero_step_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
@@ -193,31 +227,57 @@ def finalize_groups(partials: torch.Tensor, nparts: int, state: torch.Tensor, sc
         _need(t, f"bc_table[{i}]", torch.float64, None, dev, 8)
         if t.numel() < 2 * bc_len:
             raise ValueError("bc_table shorter than bc_len")
-    hy = (DsxAdamwHyper * k)(*hypers)
-    tabs = (ctypes.c_void_p * k)(*[t.data_ptr() for t in bc_tables])
-    offs = (ctypes.c_int32 * k)(*[int(x) for x in t_offsets])
-    _lib.call("dsx_finalize_groups", _ptr(partials), int(nparts), _ptr(state), scaler, hy, tabs, offs, k,
-              int(bc_len), _ptr(out), _stream(dev))
+    FinalizeGroups(partials, nparts, state, out, k)(scaler, hypers, bc_tables, t_offsets, bc_len, _stream(dev))
+
+
+class FinalizeGroups:
+    """K0 over `ngroups` parameter groups with its buffers checked once;
+    each call passes that step's scaler, hyper-parameters and tables."""
+
+    def __init__(self, partials: torch.Tensor, nparts: int, state: torch.Tensor, out: torch.Tensor, ngroups: int):
+        dev = _device(state)
+        if not 1 <= ngroups <= DSX_MAX_GROUPS:
+            raise ValueError(f"need 1..{DSX_MAX_GROUPS} groups")
+        _need(partials, "partials", torch.float64, None, dev, 8)
+        if nparts > partials.numel():
+            raise ValueError("nparts exceeds the partials buffer")
+        _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
+        _need(out, "scalars", torch.uint8, SCALARS_BYTES * ngroups, dev, 8)
+        self.k = ngroups
+        self.fn = _lib.load().dsx_finalize_groups
+        self.head = (_ptr(partials), int(nparts), _ptr(state))
+        self.out = _ptr(out)
+        self.hyper_t = DsxAdamwHyper * ngroups
+        self.tab_t = ctypes.c_void_p * ngroups
+        self.off_t = ctypes.c_int32 * ngroups
+
+    def __call__(self, scaler: DsxScalerConfig, hypers, bc_tables, t_offsets, bc_len: int,
+                 stream: ctypes.c_void_p) -> None:
+        k = self.k
+        if len(hypers) != k or len(bc_tables) != k or len(t_offsets) != k:
+            raise ValueError(f"expected {k} groups with one table and offset each")
+        for i, t in enumerate(bc_tables):
+            if t.dtype != torch.float64 or t.device.type != "cuda" or t.numel() < 2 * bc_len:
+                raise ValueError(f"bc_table[{i}] must be a float64 GPU tensor of at least {2 * bc_len} entries")
+        rc = self.fn(*self.head, scaler, self.hyper_t(*hypers), self.tab_t(*[t.data_ptr() for t in bc_tables]),
+                     self.off_t(*[int(x) for x in t_offsets]), k, int(bc_len), self.out, stream)
+        if rc:
+            raise _lib.DsxError("dsx_finalize_groups", rc, _lib.last_error())
 
 
 GROUPS_BYTES = ctypes.sizeof(_lib.DsxGroupsDev)
 
 
 def pack_groups(hypers: list[DsxAdamwHyper], bc_tables: list[torch.Tensor], t_offsets: list[int],
-                bc_len: int) -> bytes:
-    """A DsxGroupsDev image (for dsx_finalize_dev) with the host-side checks
-    dsx_finalize_groups makes, so a bad value raises here as it does eagerly."""
+                bc_len: int) -> _lib.DsxGroupsDev:
+    """A host DsxGroupsDev for dsx_groups_upload (which checks the
+    hyper-parameters as dsx_finalize_groups does)."""
     k = len(hypers)
     if not 1 <= k <= DSX_MAX_GROUPS or len(bc_tables) != k or len(t_offsets) != k:
         raise ValueError(f"need 1..{DSX_MAX_GROUPS} groups with one table and offset each")
-    from .flat_step import AdamWHyper
     g = _lib.DsxGroupsDev()
     for i in range(k):
         h = hypers[i]
-        try:
-            AdamWHyper(h.lr, h.beta1, h.beta2, h.eps, h.weight_decay, h.max_grad_norm, h.clip_eps).validate()
-        except ValueError as e:  # the error type and wording dsx_finalize_groups reports
-            raise _lib.DsxError("dsx_finalize_dev", _lib.DSX_EINVAL, str(e)) from None
         t = bc_tables[i]
         if t.dtype != torch.float64 or t.device.type != "cuda" or t.numel() < 2 * bc_len:
             raise ValueError(f"bc_table[{i}] must be a float64 GPU tensor of at least {2 * bc_len} entries")
@@ -228,7 +288,14 @@ def pack_groups(hypers: list[DsxAdamwHyper], bc_tables: list[torch.Tensor], t_of
         g.t_offset[i] = int(t_offsets[i])
     g.ngroups = k
     g.bc_len = int(bc_len)
-    return bytes(g)
+    return g
+
+
+def groups_upload(block: _lib.DsxGroupsDev, dst: torch.Tensor) -> None:
+    """dst (device, GROUPS_BYTES) <- block, in stream order."""
+    dev = _device(dst)
+    _need(dst, "groups", torch.uint8, GROUPS_BYTES, dev, 8)
+    _lib.call("dsx_groups_upload", ctypes.byref(block), _ptr(dst), _stream(dev))
 
 
 def finalize_dev(partials: torch.Tensor, nparts: int, state: torch.Tensor, scaler: DsxScalerConfig,
@@ -236,6 +303,11 @@ def finalize_dev(partials: torch.Tensor, nparts: int, state: torch.Tensor, scale
     """K0 reading its per-group inputs from `groups_dev` (a DsxGroupsDev in
     device memory), the form a captured graph replays; `out` holds max_groups
     DsxStepScalars, all written."""
+    plan_finalize_dev(partials, nparts, state, scaler, groups_dev, max_groups, out)(_stream(state.device))
+
+
+def plan_finalize_dev(partials: torch.Tensor, nparts: int, state: torch.Tensor, scaler: DsxScalerConfig,
+                      groups_dev: torch.Tensor, max_groups: int, out: torch.Tensor) -> Launch:
     dev = _device(state)
     if not 1 <= max_groups <= DSX_MAX_GROUPS:
         raise ValueError(f"max_groups must be in [1, {DSX_MAX_GROUPS}]")
@@ -245,8 +317,8 @@ def finalize_dev(partials: torch.Tensor, nparts: int, state: torch.Tensor, scale
     _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
     _need(groups_dev, "groups", torch.uint8, GROUPS_BYTES, dev, 8)
     _need(out, "scalars", torch.uint8, SCALARS_BYTES * max_groups, dev, 8)
-    _lib.call("dsx_finalize_dev", _ptr(partials), int(nparts), _ptr(state), scaler, _ptr(groups_dev),
-              int(max_groups), _ptr(out), _stream(dev))
+    return Launch("dsx_finalize_dev", _ptr(partials), int(nparts), _ptr(state), scaler, _ptr(groups_dev),
+                  int(max_groups), _ptr(out))
 
 
 # ---- ragged lists (K3) --------------------------------------------------------------

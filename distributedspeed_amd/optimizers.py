@@ -248,11 +248,22 @@ class AdamWOptimizer(_FusedAdamWBase):
         self.use_graph = bool(graph)
         self._graph = None
         self._bind_state()
+        # The flat buffers never move, so every launch of the step is checked
+        # and bound once here; a step then costs one ctypes call per launch.
+        self._k1 = ops.plan_unscale_norm(self.flat.grad, self.dstate, self.partials, self.nparts)
+        self._k0 = ops.FinalizeGroups(self.partials, self.nparts, self.dstate, self.scalars, len(self.param_groups))
+        self._k2 = []
+        if self.streamer is None:
+            for gi in range(len(self.param_groups)):
+                master, m, v, p16, g = self.flat.group_views(gi)
+                if master.numel():
+                    sc = self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
+                    self._k2.append(ops.plan_adamw_flat(master, m, v, p16, g, sc))
 
     def launch_norm(self) -> None:
         """K1 alone over the current grads (partials <- squared norms)."""
         self.flat.check_grads_bound()
-        ops.unscale_norm(self.flat.grad, self.dstate, self.partials, self.nparts)
+        self._k1(ops.stream_of(self.device))
 
     def step_fused(self) -> None:
         """K1 -> K0 -> K2 on the current stream; no host synchronisation."""
@@ -265,11 +276,11 @@ class AdamWOptimizer(_FusedAdamWBase):
             if self._graph is None:
                 from .graph import GraphedStep
                 self._graph = GraphedStep(self)
-            self._graph.replay(hs, tables, bc_len)
+            self._graph.replay(hs, tables, self._t_offsets, bc_len)
             return
-        ops.unscale_norm(self.flat.grad, self.dstate, self.partials, self.nparts)
-        ops.finalize_groups(self.partials, self.nparts, self.dstate, self.scaler.to_c(), hs, tables,
-                            self._t_offsets, bc_len, self.scalars)
+        s = ops.stream_of(self.device)
+        self._k1(s)
+        self._k0(self.scaler.to_c(), hs, tables, self._t_offsets, bc_len, s)
         if self.streamer is not None:
             # State in pinned host memory: stream it through HBM chunk by chunk.
             # A skipped step streams too (K2 leaves the chunks unchanged), which
@@ -279,12 +290,8 @@ class AdamWOptimizer(_FusedAdamWBase):
             self.streamer.run((self.flat.master, self.flat.exp_avg, self.flat.exp_avg_sq), self.flat.param16,
                               self.flat.grad, pieces)
             return
-        for gi in range(len(self.param_groups)):
-            master, m, v, p16, g = self.flat.group_views(gi)
-            if master.numel() == 0:
-                continue
-            sc = self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
-            ops.adamw_flat(master, m, v, p16, g, sc)
+        for k2 in self._k2:
+            k2(s)
 
 
 
@@ -297,7 +304,7 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
     def __init__(self, params: Iterable, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
                  weight_decay: float = 1e-2, *, max_grad_norm: float = 0.0, param_dtype: torch.dtype | None = None,
                  loss_scaler: ScalerConfig | None = None, device: torch.device | None = None,
-                 param_names: dict | None = None, chunk_elems: int = 65536, offload: bool = False,
+                 param_names: dict | None = None, chunk_elems: int | None = None, offload: bool = False,
                  graph: bool = False):
         if offload or graph:
             raise ValueError("offload and graph capture need the flat form (contiguous_gradients = true)")

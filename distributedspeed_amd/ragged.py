@@ -21,16 +21,26 @@ import torch
 from . import ops
 
 
+def auto_chunk_elems(numel: int) -> int:
+    """Chunk size for a list of `numel` elements: 65536 for large lists; for
+    smaller ones a power of two down to 4096, so that the list still splits
+    into about 4096 chunks (the kernels hand chunks to blocks statically, and
+    a GPU of 256 CUs needs several rounds of them to balance)."""
+    c = 65536
+    while c > 4096 and numel // c < 4096:
+        c //= 2
+    return c
+
+
 class RaggedParams:
     def __init__(self, groups: list[list[torch.nn.Parameter]], device: torch.device,
-                 param_dtype: torch.dtype | None, names: dict | None = None, chunk_elems: int = 65536):
+                 param_dtype: torch.dtype | None, names: dict | None = None, chunk_elems: int | None = None):
         if param_dtype not in (None, torch.float16, torch.bfloat16):
             raise ValueError(f"param_dtype must be float16, bfloat16 or None, got {param_dtype}")
         names = names or {}
         self.device = torch.device(device)
         self.param_dtype = param_dtype
         self.grad_dtype = param_dtype or torch.float32
-        self.chunk_elems = int(chunk_elems)
         self.params: list[torch.nn.Parameter] = []
         self.group_of: list[int] = []
         self.names: list[str] = []
@@ -62,6 +72,7 @@ class RaggedParams:
                     if p.grad is not None:
                         p.grad = p.grad.to(self.device, self.grad_dtype).contiguous()
         self.numel = sum(m.numel() for m in self.master)
+        self.chunk_elems = int(chunk_elems) if chunk_elems else auto_chunk_elems(self.numel)
         self.ngroups = len(groups)
         self._table = None
         self._key = None
@@ -80,7 +91,7 @@ class RaggedParams:
         """The device chunk table for the current storage (rebuilt only when
         a param's or a grad's address changed)."""
         self.ensure_grads()
-        key = tuple((p.data.data_ptr(), p.grad.data_ptr()) for p in self.params)
+        key = tuple((p.data_ptr(), p.grad.data_ptr()) for p in self.params)
         if key != self._key:
             for p, m in zip(self.params, self.master):
                 if p.data.shape != m.shape or (self.param_dtype is None and p.data.data_ptr() != m.data_ptr()):

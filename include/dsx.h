@@ -163,6 +163,12 @@ const char* dsx_last_error(void);
 int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll,
                    int nontemporal);
 
+/* The same for K3 (dsx_adamw_multi): blocks per CU (the grid is also capped
+ * at the chunk count; 0, the default, picks blocks per CU and slots per
+ * thread from the chunk count), slots per thread per trip (1, 2 or 4) and
+ * the nontemporal hint. No counterpart in the reference. */
+int dsx_set_tuning_multi(int k3_blocks_per_cu, int k3_unroll, int nontemporal);
+
 /* Partials a K1 launch over n elements should use on the current device
  * (a multiple of the CU count, <= DSX_MAX_PARTIALS). */
 int32_t dsx_suggest_partials(int64_t n);
@@ -247,6 +253,14 @@ typedef struct DsxGroupsDev {
 int dsx_finalize_dev(const double* partials, int32_t nparts, DsxState* state,
                      DsxScalerConfig scaler, const DsxGroupsDev* groups,
                      int32_t max_groups, DsxStepScalars* out, void* stream);
+
+/* Copies the HOST block `groups` into the device block `dst` in stream
+ * order (a one-wave kernel that takes the block as its argument: no host
+ * staging buffer, no DMA copy, nothing to wait for on the host). Checks the
+ * block as dsx_finalize_groups checks its arrays. Used before each replay of
+ * a graph that holds dsx_finalize_dev. No counterpart in the reference. */
+int dsx_groups_upload(const DsxGroupsDev* groups, DsxGroupsDev* dst,
+                      void* stream);
 
 /* ---- K2: AdamW + cast over a flat partition -------------------------- */
 

@@ -102,9 +102,27 @@ def test_argument_checks_reject_before_launch(lib):
     # partial count out of range
     assert lib.dsx_unscale_norm(al, 2, 16, al, al, 0, None) == EINVAL
     assert lib.dsx_unscale_norm(al, 2, 16, al, al, _lib.DSX_MAX_PARTIALS + 1, None) == EINVAL
+    # the graph path's group block: same checks and wording as dsx_finalize_groups
+    g = _lib.DsxGroupsDev()
+    g.ngroups = 1
+    g.bc_len = 4
+    g.bc_table[0] = al
+    g.hyper[0] = _lib.DsxAdamwHyper(-1.0, 0.9, 0.999, 1e-8, 0.0, 0.0, 1e-6)
+    assert lib.dsx_groups_upload(ctypes.byref(g), al, None) == EINVAL
+    assert b"Invalid learning rate" in lib.dsx_last_error()
+    g.hyper[0].lr = 1e-3
+    g.ngroups = 0
+    assert lib.dsx_groups_upload(ctypes.byref(g), al, None) == EINVAL
+    assert b"ngroups" in lib.dsx_last_error()
+    g.ngroups = 1
+    g.bc_table[0] = None
+    assert lib.dsx_groups_upload(ctypes.byref(g), al, None) == EINVAL
+    assert lib.dsx_groups_upload(ctypes.byref(g), al + 4, None) == EINVAL
     # tuning validation
     assert lib.dsx_set_tuning(8, 8, 3, 1) == EINVAL
     assert lib.dsx_set_tuning(0, 8, 4, 1) == EINVAL
+    assert lib.dsx_set_tuning_multi(8, 3, 0) == EINVAL
+    assert lib.dsx_set_tuning_multi(-1, 1, 0) == EINVAL
 
 
 def test_python_layer_mirrors_torch_errors():

@@ -80,6 +80,7 @@ def test_graph_replays_match_eager_step_by_step(gpu, dtype_name):
         torch.cuda.synchronize()
         _same(eager, graphed, f"step {step}")
     assert graphed._graph is not None and graphed._graph.replays == 14
+    assert graphed._graph.uploads == 14  # lr changed every step
     st = graphed.read_state()
     if dtype == torch.float16:
         assert st.overflow_count == 3 and st.t == 11 and st.iter == 14
@@ -101,6 +102,7 @@ def test_graph_survives_bias_table_growth_and_checkpoint_load(gpu):
             torch.cuda.synchronize()
             _same(eager, graphed, f"step {step}")
     assert min(t.length for t in graphed._bc.values()) >= 1030
+    assert graphed._graph.uploads == 2  # constant lr: the first step and the table regrowth
     # load an earlier checkpoint into the graphed optimizer: same addresses, so
     # the captured graph keeps working from the loaded state
     sd = eager.state_dict()
@@ -188,3 +190,25 @@ def test_engine_hip_graph_config_matches_eager(gpu):
         runs.append(opt.base_optimizer)
     assert runs[1]._graph is not None and runs[0]._graph is None
     _same(runs[0], runs[1], "engine")
+
+
+def test_graphed_optimizer_is_freed_by_refcount(gpu):
+    """The optimizer -> GraphedStep link is one-way, so dropping a graphed
+    optimizer frees it (and its graph) at once, not at some later cyclic
+    collection that might land inside another graph's capture."""
+    import gc
+    import weakref
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    _, graphed = _pair(gpu, torch.bfloat16, ScalerConfig(mode="none"), shapes=((16,), (8,), (8,)))
+    graphed.step()
+    torch.cuda.synchronize()
+    refs = [weakref.ref(graphed), weakref.ref(graphed._graph)]
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        del graphed
+        assert all(r() is None for r in refs)
+    finally:
+        if was:
+            gc.enable()

@@ -208,12 +208,10 @@ def test_oracle_not_imported_by_product():
 
 
 def test_pack_groups_checks_on_host():
-    """The graph path's per-step group block is checked on the host with the
-    eager path's error type and wording."""
-    from distributedspeed_amd import _lib, ops
+    """The graph path's per-step group block: table checks in Python (the
+    hyper-parameters are checked by dsx_groups_upload, tested with the ABI)."""
+    from distributedspeed_amd import ops
     t = torch.zeros(8, dtype=torch.float64)
-    with pytest.raises(_lib.DsxError, match="Invalid learning rate"):
-        ops.pack_groups([AdamWHyper(lr=-1).to_c()], [t], [0], 4)
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.pack_groups([AdamWHyper().to_c()], [t], [0], 4)
     with pytest.raises(ValueError, match="groups"):
@@ -255,3 +253,12 @@ def test_ragged_store_fp32_master_is_the_param():
         assert p.data_ptr() == m.data_ptr() and p.dtype == torch.float32
     with pytest.raises(ValueError):
         RaggedParams([[torch.nn.Parameter(torch.zeros(2, dtype=torch.float16))]], torch.device("cpu"), None)
+
+
+def test_ragged_chunk_size_fills_the_gpu():
+    from distributedspeed_amd.ragged import auto_chunk_elems
+    assert auto_chunk_elems(8_310_226_944) == 65536 and auto_chunk_elems(124_439_808) == 16384
+    assert auto_chunk_elems(1_863_690) == 4096 and auto_chunk_elems(10) == 4096
+    for n in (1 << 20, 1 << 27, 3 << 28):
+        c = auto_chunk_elems(n)
+        assert c % 8 == 0 and (c == 4096 or n // c >= 4096)
