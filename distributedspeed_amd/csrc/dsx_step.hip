@@ -74,7 +74,7 @@ bool is_grad_dtype(int dt) { return dt == DSX_F16 || dt == DSX_BF16 || dt == DSX
 struct Tuning {
   int k1_blocks_per_cu = 2;
   int k2_blocks_per_cu = 1;
-  int k2_unroll = 4;      // slots per thread per trip: 2, 4 or 8
+  int k2_unroll = 2;      // slots per thread per trip: 2, 4 or 8
   int nontemporal = 1;    // nontemporal hint on the streaming loads/stores
   int k3_blocks_per_cu = 0;  // 0: chosen per launch from the chunk count
   int k3_unroll = 1;         // slots per thread per trip in K3: 1, 2 or 4 (when not chosen)
