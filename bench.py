@@ -35,8 +35,10 @@ def _args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--numel", type=int, default=HEADLINE_NUMEL)
-    ap.add_argument("--cpu-sample", type=int, default=16 * 1024 * 1024,
+    ap.add_argument("--cpu-sample", type=int, default=128 * 1024 * 1024,
                     help="elements in the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="CPU time budget of the port's timed steps (torch's gets half)")
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                       "k2_adamw_flat_llama8b_shard_traffic.json"))
     ap.add_argument("--tuning", default="", help="k1_bpc,k2_bpc,k2_unroll,nt (library launch-shape override)")
@@ -358,10 +360,11 @@ def bench_offload(a, dev) -> int:
     return 0
 
 
-def cpu_baseline(n_sample: int, hyper) -> dict | None:
+def cpu_baseline(n_sample: int, hyper, seconds: float = 8.0) -> dict | None:
     """The C oracle (a CPU port of the step) on a bounded sample, on this
-    host's cores; plus torch.optim.AdamW on CPU (the reference's cpu_offload
-    route) on the same sample, for context."""
+    host's cores, stepping until `seconds` of timed work (at least 3 steps);
+    plus torch.optim.AdamW on CPU (the reference's cpu_offload route) on the
+    same sample for half that budget, for context."""
     if n_sample <= 0:
         return None
     import numpy as np
@@ -380,7 +383,9 @@ def cpu_baseline(n_sample: int, hyper) -> dict | None:
     h = O.Hyper(lr=hyper.lr, beta1=hyper.beta1, beta2=hyper.beta2, eps=hyper.eps,
                 weight_decay=hyper.weight_decay, max_grad_norm=hyper.max_grad_norm)
     times = []
-    for t in range(1, 4):
+    t = 0
+    while t < 4 or sum(times[1:]) < seconds:
+        t += 1
         t0 = time.perf_counter()
         ss = O.sumsq(g16, O.BF16, 1.0)
         coef = O.clip_coef(ss ** 0.5, h.max_grad_norm, h.clip_eps)
@@ -396,7 +401,7 @@ def cpu_baseline(n_sample: int, hyper) -> dict | None:
                             weight_decay=hyper.weight_decay, foreach=False)
     g16t = torch.from_numpy(g16.view(np.int16)).view(torch.bfloat16)
     ttimes = []
-    for _ in range(3):
+    while len(ttimes) < 4 or sum(ttimes[1:]) < seconds / 2:
         t0 = time.perf_counter()
         g = g16t.float()
         norm = g.norm(dtype=torch.float32).item()
@@ -413,9 +418,10 @@ def cpu_baseline(n_sample: int, hyper) -> dict | None:
         "cores": int(O.lib().dsxo_num_threads()),
         "kind": "port",
         "sample": f"{n_sample} elements of the same workload (bf16 grads N(0,5e-4^2), fp32 state), "
-                  f"one full step (norm + clip + AdamW + cast), median of 2 after 1 warm-up",
+                  f"one full step (norm + clip + AdamW + cast); median of {len(times) - 1} steps "
+                  f"({sum(times[1:]):.1f} s) after 1 warm-up",
         "torch_adamw_cpu": {"value": round(n_sample / torch_s / 1e9, 4), "unit": "Gparam/s",
-                            "threads": torch.get_num_threads(),
+                            "threads": torch.get_num_threads(), "steps": len(ttimes) - 1,
                             "what": "torch.optim.AdamW(foreach=False) on CPU fp32 + fp32 norm/clip + bf16 cast"},
     }
 
@@ -514,7 +520,7 @@ def main() -> int:
             traffic = None
 
     _progress("cpu baseline")
-    cpu = cpu_baseline(min(a.cpu_sample, n), hyper)
+    cpu = cpu_baseline(min(a.cpu_sample, n), hyper, a.cpu_seconds)
 
     out = {
         "metric": "AdamW step Gparam/s + achieved HBM TB/s (% of 8 TB/s), 1.0B-elt bf16 shard",
