@@ -48,7 +48,7 @@ class DsxAdamwHyper(_c.Structure):
 
 class DsxStepScalars(_c.Structure):
     _fields_ = [("skip", _c.c_int32), ("t", _c.c_int32)] + \
-               [(k, _c.c_float) for k in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2",
+               [(k, _c.c_float) for k in ("inv_scale", "clip_coef", "decay", "w1", "w1c", "b2", "val2",
                                           "eps", "bc2s", "nss")] + \
                [("sumsq", _c.c_double), ("norm", _c.c_double)]
 

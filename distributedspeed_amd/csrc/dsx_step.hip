@@ -16,7 +16,8 @@
 //
 // Compile with -ffp-contract=off: the element math must round exactly where
 // torch rounds, and the only fused multiply-adds are the explicit fmaf calls
-// that mirror torch's lerp and addcmul kernels.
+// that mirror the fused operations of torch's GPU kernels (lerp, addcmul,
+// addcdiv).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -177,35 +178,40 @@ struct Grad<DSX_F32> {
 
 // Step scalars held in registers.
 struct Sc {
-  float inv, coef, decay, w1, w1m1, b2, val2, eps, bc2s, nss;
+  float inv, coef, decay, w1, w1c, b2, val2, eps, bc2s, nss;
   bool small;
 };
 
 __device__ __forceinline__ Sc load_sc(const DsxStepScalars& s) {
   Sc r;
   r.inv = s.inv_scale; r.coef = s.clip_coef; r.decay = s.decay;
-  r.w1 = s.w1; r.w1m1 = s.w1m1; r.b2 = s.b2; r.val2 = s.val2;
+  r.w1 = s.w1; r.w1c = s.w1c; r.b2 = s.b2; r.val2 = s.val2;
   r.eps = s.eps; r.bc2s = s.bc2s; r.nss = s.nss;
   r.small = fabsf(s.w1) < 0.5f;
   return r;
 }
 
-// One element of the step. Order and rounding follow torch's CPU kernels:
-// unscale and clip are fp32 multiplies; param.mul_(1 - lr*wd); lerp_ with a
-// scalar weight is fma(w, end - self, self) (or fma(w - 1, end - self, end)
-// for |w| >= 0.5); exp_avg_sq.mul_(b2).addcmul_(g, g, 1 - b2) is
-// fma((1 - b2) * g, g, v * b2); denom = sqrt(v) / bc2s + eps with IEEE sqrt
-// and division; addcdiv_ is p + (value * m) / denom.
+// One element of the step. Order and rounding are those of torch.optim.AdamW
+// on a GPU -- its default multi-tensor path, torch/optim/adam.py:692-800,
+// which the reference's stages reach through optimizer.step() -- measured
+// bit for bit against torch on MI355X: unscale and clip are fp32 multiplies;
+// _foreach_mul_(params, 1 - lr*wd); _foreach_lerp_ with a scalar weight is
+// fma(w, end - self, self), or for |w| >= 0.5 end - (end - self) * (1 - w)
+// as fma(-(end - self), 1 - w, end) (which keeps the sign of a zero as torch);
+// _foreach_mul_(v, b2) then _foreach_addcmul_(v, g, g, 1 - b2) is
+// fma(1 - b2, g * g, v); denom = sqrt(v) / bc2s + eps with IEEE sqrt and
+// true division (_foreach_div_ by a list of scalars); _foreach_addcdiv_ is
+// fma(value, m / denom, p).
 __device__ __forceinline__ void adamw_elt(float graw, float& p, float& m, float& v, const Sc& s) {
   float g = graw * s.inv;
   g = g * s.coef;
   p = p * s.decay;
   const float d = g - m;
-  m = s.small ? __builtin_fmaf(s.w1, d, m) : __builtin_fmaf(s.w1m1, d, g);
+  m = s.small ? __builtin_fmaf(s.w1, d, m) : __builtin_fmaf(-d, s.w1c, g);
   v = v * s.b2;
-  v = __builtin_fmaf(s.val2 * g, g, v);
+  v = __builtin_fmaf(s.val2, g * g, v);
   const float den = __builtin_sqrtf(v) / s.bc2s + s.eps;
-  p = p + (s.nss * m) / den;
+  p = __builtin_fmaf(s.nss, m / den, p);
 }
 
 // Four elements held in vector registers.
@@ -349,7 +355,7 @@ __device__ void finalize_body(double sumsq, DsxState* __restrict__ state, const 
       const double bc2s = grp.bc_table[k][2 * (int64_t)(tk - 1) + 1];
       if (hp.weight_decay != 0.0) o.decay = (float)(1.0 - hp.lr * hp.weight_decay);
       o.w1 = (float)(1.0 - hp.beta1);
-      o.w1m1 = o.w1 - 1.0f;
+      o.w1c = 1.0f - o.w1;
       o.b2 = (float)hp.beta2;
       o.val2 = (float)(1.0 - hp.beta2);
       o.eps = (float)hp.eps;

@@ -30,13 +30,14 @@
  *     rejected argument; otherwise the hipError_t of a failed launch.
  *     dsx_last_error() returns a thread-local message for the last failure.
  *
- * Arithmetic (fp32, in this order, no FMA contraction except where named):
+ * Arithmetic (fp32, in this order, no FMA contraction except where named;
+ * the roundings of torch.optim.AdamW's default multi-tensor path on a GPU):
  *   g  = f32(g16) * inv_scale;  g = g * clip_coef
  *   p  = p * decay                               decay = f32(1 - lr*wd)
- *   m  = fma(w1, g - m, m)           if |w1| < .5, else fma(w1 - 1, g - m, g)
- *   v  = v * b2;  v = fma(val2 * g, g, v)        val2 = f32(1 - beta2)
+ *   m  = fma(w1, g - m, m)        if |w1| < .5, else fma(-(g - m), 1 - w1, g)
+ *   v  = v * b2;  v = fma(val2, g * g, v)        val2 = f32(1 - beta2)
  *   d  = sqrt(v) / bc2s + eps                    IEEE sqrt and division
- *   p  = p + (nss * m) / d                       nss = f32(-lr / bc1[t])
+ *   p  = fma(nss, m / d, p)                      nss = f32(-lr / bc1[t])
  *   p16 = round_to_nearest_even(p)
  */
 #ifndef DSX_H_
@@ -120,7 +121,7 @@ typedef struct DsxStepScalars {
   float   clip_coef;      /* 1.0f when not clipping                          */
   float   decay;          /* f32(1 - lr*wd), 1.0f when wd == 0               */
   float   w1;             /* f32(1 - beta1), lerp weight                     */
-  float   w1m1;           /* w1 - 1.0f                                       */
+  float   w1c;            /* 1.0f - w1                                       */
   float   b2;             /* f32(beta2)                                      */
   float   val2;           /* f32(1 - beta2)                                  */
   float   eps;            /* f32(eps)                                        */

@@ -11,22 +11,28 @@
  *       torch/amp/grad_scaler.py:235-286)
  *   - clipping g *= max_norm / (norm + 1e-6) iff norm > max_norm:
  *       Src/zero/utils.py:187-216
- *   - AdamW (decoupled weight decay) with torch's per-op rounding, called by
- *       the reference at Src/zero/stage1.py:522-525, Src/zero/stage2.py:609-612;
- *       algorithm torch/optim/adam.py:347-552 (_single_tensor_adam):
- *         p *= f32(1 - lr*wd)                         adam.py:415-418
- *         m  = lerp(m, g, f32(1 - beta1))             adam.py:456
- *              (ATen's vectorised lerp: one fused multiply-add,
- *               torch/include/ATen/native/Lerp.h:21-35 for the branch)
- *         v  = fma(f32(1 - beta2) * g, g, v * beta2)  adam.py:476 (addcmul_)
- *         d  = sqrt(v) / f32(bc2_sqrt) + f32(eps)     adam.py:543-545
- *         p  = p + (f32(-lr/bc1) * m) / d             adam.py:547 (addcdiv_)
+ *   - AdamW (decoupled weight decay) with the per-op rounding of
+ *       torch.optim.AdamW on a GPU, called by the reference at
+ *       Src/zero/stage1.py:522-525, Src/zero/stage2.py:609-612; on GPU
+ *       tensors torch defaults to the multi-tensor path (adam.py:938),
+ *       torch/optim/adam.py:554-800 (_multi_tensor_adam):
+ *         p *= f32(1 - lr*wd)                         adam.py:692
+ *         m  = lerp(m, g, f32(1 - beta1))             adam.py:705-707
+ *              (one fused multiply-add: fma(w, g - m, m), or for
+ *               |w| >= 0.5 g - (g - m) * (1 - w) as fma(-(g - m), 1 - w, g),
+ *               torch/include/ATen/native/Lerp.h:21-35)
+ *         v  = fma(f32(1 - beta2), g * g, v * beta2)  adam.py:709, 722-724
+ *         d  = sqrt(v) / f32(bc2_sqrt) + f32(eps)     adam.py:781, 791-794
+ *         p  = fma(f32(-lr/bc1), m / d, p)            adam.py:779, 795-800
  *   - the 16-bit cast of the updated fp32 master (round to nearest even).
  *
  * Built with -ffp-contract=off so that every operation rounds on its own;
- * fmaf() is called exactly where torch's CPU kernels fuse. sqrtf() and '/'
- * are IEEE correctly rounded here. torch's own CPU sqrt (MKL VML) is not, so
- * the master weight can differ from torch CPU by 1 ulp; m and v cannot.
+ * fmaf() is called exactly where torch's GPU kernels fuse (measured bit for
+ * bit against torch on MI355X; tests/golden/adamw_torch_gpu.npz). sqrtf()
+ * and '/' are IEEE correctly rounded, as torch's GPU sqrt and division are.
+ * torch's CPU kernels round differently (addcmul as fma((1-b2)*g, g, v*b2),
+ * addcdiv as p + (s*m)/d, MKL's sqrt), so against torch on a CPU the oracle
+ * agrees within a few ulp rather than bit for bit.
  *
  * The fp16/bf16 conversions are written from the IEEE 754 binary16 and
  * bfloat16 definitions, without hardware conversion instructions.
@@ -40,7 +46,7 @@
 #define DSXO_BF16 2
 
 typedef struct DsxoScalars {
-  float inv_scale, clip_coef, decay, w1, w1m1, b2, val2, eps, bc2s, nss;
+  float inv_scale, clip_coef, decay, w1, w1c, b2, val2, eps, bc2s, nss;
 } DsxoScalars;
 
 static inline uint32_t f2u(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
@@ -144,11 +150,11 @@ static inline void step_elt(float graw, float* p, float* m, float* v, const Dsxo
   g = g * s->clip_coef;
   float pp = *p * s->decay;
   const float d = g - *m;
-  const float mm = (fabsf(s->w1) < 0.5f) ? fmaf(s->w1, d, *m) : fmaf(s->w1m1, d, g);
+  const float mm = (fabsf(s->w1) < 0.5f) ? fmaf(s->w1, d, *m) : fmaf(-d, s->w1c, g);
   float vv = *v * s->b2;
-  vv = fmaf(s->val2 * g, g, vv);
+  vv = fmaf(s->val2, g * g, vv);
   const float den = sqrtf(vv) / s->bc2s + s->eps;
-  pp = pp + (s->nss * mm) / den;
+  pp = fmaf(s->nss, mm / den, pp);
   *p = pp;
   *m = mm;
   *v = vv;

@@ -43,7 +43,7 @@ _lib = None
 
 class _Scalars(ctypes.Structure):
     _fields_ = [(name, ctypes.c_float) for name in
-                ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss")]
+                ("inv_scale", "clip_coef", "decay", "w1", "w1c", "b2", "val2", "eps", "bc2s", "nss")]
 
 
 def build() -> str:
@@ -163,7 +163,7 @@ def step_scalars(h: Hyper, t: int, inv_scale: float, coef: float) -> _Scalars:
     s.clip_coef = coef
     s.decay = f(1 - h.lr * h.weight_decay) if h.weight_decay != 0 else 1.0
     s.w1 = f(1 - h.beta1)
-    s.w1m1 = float(np.float32(s.w1) - np.float32(1.0))
+    s.w1c = float(np.float32(1.0) - np.float32(s.w1))
     s.b2 = f(h.beta2)
     s.val2 = f(1 - h.beta2)
     s.eps = f(h.eps)

@@ -50,26 +50,30 @@ def bf16_exact(x: np.ndarray) -> np.ndarray:
     return torch.from_numpy(x).to(torch.bfloat16).float().numpy()
 
 
-def adamw_fixture(n: int = 1024, steps: int = 5) -> dict:
+def adamw_fixture(n: int = 1024, steps: int = 5, device: str = "cpu", foreach=False) -> dict:
+    """torch.optim.AdamW on `device` (foreach=None: torch's default dispatch)."""
     out = {"capability": np.array(torch.backends.cpu.get_cpu_capability()),
            "torch_version": np.array(torch.__version__)}
+    if device != "cpu":
+        out["device"] = np.array(torch.cuda.get_device_name(0))
+        out["foreach"] = np.array(str(foreach))
     for k, h in enumerate(HYPERS):
         rng = np.random.default_rng(500 + k)
         p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
         p0[:4] = [0.0, -0.0, 1e-30, -3.0]
         grads = np.stack([bf16_exact((rng.standard_normal(n) * 1e-3).astype(np.float32)) for _ in range(steps)])
         grads[:, 4:8] = bf16_exact(np.array([0.0, -0.0, 1e-20, 65504.0], np.float32))
-        param = torch.nn.Parameter(torch.from_numpy(p0.copy()))
+        param = torch.nn.Parameter(torch.from_numpy(p0.copy()).to(device))
         opt = torch.optim.AdamW([param], lr=h["lr"], betas=(h["beta1"], h["beta2"]), eps=h["eps"],
-                                weight_decay=h["weight_decay"], foreach=False)
+                                weight_decay=h["weight_decay"], foreach=foreach)
         ps, ms, vs = [], [], []
         for t in range(steps):
-            param.grad = torch.from_numpy(grads[t].copy())
+            param.grad = torch.from_numpy(grads[t].copy()).to(device)
             opt.step()
             st = opt.state[param]
-            ps.append(param.detach().numpy().copy())
-            ms.append(st["exp_avg"].numpy().copy())
-            vs.append(st["exp_avg_sq"].numpy().copy())
+            ps.append(param.detach().cpu().numpy().copy())
+            ms.append(st["exp_avg"].cpu().numpy().copy())
+            vs.append(st["exp_avg_sq"].cpu().numpy().copy())
         out[f"h{k}_hyper"] = np.array([h["lr"], h["beta1"], h["beta2"], h["eps"], h["weight_decay"]])
         out[f"h{k}_p0"] = p0
         out[f"h{k}_grads"] = grads

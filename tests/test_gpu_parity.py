@@ -29,7 +29,7 @@ def _run_k2(gpu, p, m, v, g16, gdt, pdt, sc_host, with_p16=True):
     c = _lib.DsxStepScalars()
     c.skip = 0
     c.t = 1
-    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss"):
+    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1c", "b2", "val2", "eps", "bc2s", "nss"):
         setattr(c, k, getattr(sc_host, k))
     scal = ops.scalars_from_host(c, gpu)
     ops.adamw_flat(tp, tm, tv, tp16, tg, scal)
@@ -279,7 +279,7 @@ def test_multi_tensor_equals_flat(gpu, oracle):
     c = oracle  # noqa: F841
     from distributedspeed_amd import _lib
     hs = _lib.DsxStepScalars()
-    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss"):
+    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1c", "b2", "val2", "eps", "bc2s", "nss"):
         setattr(hs, k, getattr(sc, k))
     scal = ops.scalars_from_host(hs, gpu)
     ops.adamw_multi(table, scal)
@@ -375,7 +375,7 @@ def test_k2_fp32_grads_bit_exact(gpu, oracle):
     sc = O.step_scalars(O.Hyper(lr=1e-3, weight_decay=0.02), 4, 1.0, 0.25)
     from distributedspeed_amd import _lib, ops
     c = _lib.DsxStepScalars()
-    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss"):
+    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1c", "b2", "val2", "eps", "bc2s", "nss"):
         setattr(c, k, getattr(sc, k))
     tp, tm, tv, tg = (f32_to_torch(a, gpu) for a in (p, m, v, g))
     ops.adamw_flat(tp, tm, tv, None, tg, ops.scalars_from_host(c, gpu))
@@ -418,7 +418,7 @@ def test_finalize_groups_matches_oracle(gpu, oracle):
             ref = O.step_scalars(h, t - offs[k], O.inv_scale_of(8.0), O.clip_coef(4.0, 1.0))
             assert got.skip == 0 and got.t == t - offs[k]
             assert got.norm == 4.0
-            for name in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss"):
+            for name in ("inv_scale", "clip_coef", "decay", "w1", "w1c", "b2", "val2", "eps", "bc2s", "nss"):
                 assert np.float32(getattr(got, name)) == np.float32(getattr(ref, name)), (t, k, name)
     # an offset beyond the current step is an error: the step is skipped and flagged
     ops.finalize_groups(parts, 3, st, cfg, hc, [x.table for x in tabs], [0, 0, 7], tabs[0].length, out)
@@ -446,7 +446,7 @@ def test_multi_tensor_groups(gpu, oracle):
     for k, h in enumerate(hyps):
         sc = O.step_scalars(h, t, 1.0, 1.0)
         c = _lib.DsxStepScalars()
-        for f in ("inv_scale", "clip_coef", "decay", "w1", "w1m1", "b2", "val2", "eps", "bc2s", "nss"):
+        for f in ("inv_scale", "clip_coef", "decay", "w1", "w1c", "b2", "val2", "eps", "bc2s", "nss"):
             setattr(c, f, getattr(sc, f))
         scal[k * ops.SCALARS_BYTES:(k + 1) * ops.SCALARS_BYTES] = ops.scalars_from_host(c, gpu)
     ops.adamw_multi(table, scal)

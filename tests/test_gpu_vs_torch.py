@@ -1,0 +1,156 @@
+"""GPU parity against the reference's own update rule on the same device: the
+fused step (K1/K0/K2 through AdamWOptimizer) against the step the reference
+takes at world size 1 -- unscale by 1/scale (GradScaler.unscale_), skip on a
+non-finite grad, per-tensor fp32 norm combined in Python double
+(Src/zero/utils.py:126-154), g *= max/(norm + 1e-6) when norm > max
+(Src/zero/utils.py:187-216), then torch.optim.AdamW.step on fp32 GPU tensors
+(Src/zero/stage2.py:609-612) -- with torch's default dispatch (on GPU
+tensors the multi-tensor path) and with the single-tensor path.
+
+Bar: skip decisions and the loss-scale sequence
+bit-exact; fp32 master / exp_avg / exp_avg_sq within 2 ulp; 16-bit params
+within 1 ulp; grad norm within 1e-6 relative. Against torch's default path
+the kernels follow its roundings, so the state is required bit-identical;
+the single-tensor path (foreach=False, not the default on a GPU) divides
+by the bias correction through a reciprocal (x * fl(1/b), up to 1.5 ulp
+from x / b), which moves the update by up to ~3 ulp: it is held to 2 ulp on
+exp_avg / exp_avg_sq and 4 ulp on the master, one step at a time from
+torch's state. Where a result comes out of
+cancellation (p*decay + update, m + w*(g - m)) the ulp is taken of the
+largest operand of that last operation, as for the CPU pins of the oracle.
+The reference's norm is an fp32 reduction, ours an fp64 sum of exact
+squares; they are compared to 1e-6, and the clip coefficient on the
+reference side is then taken (by the reference's formula) from our norm, so
+that a last-bit difference between the two norms does not leak into the
+AdamW comparison as a 1-ulp difference of every clipped grad."""
+from __future__ import annotations
+
+import math
+import sys
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[gpu-test] {msg}", file=sys.stderr, flush=True)
+
+
+def _ulp(x):
+    """ulp of fp32 values (of their magnitude), as float64, computed exactly
+    on the host (np.frexp / np.ldexp; torch's ldexp goes through pow)."""
+    import numpy as np
+    a = np.abs(x.detach().float().cpu().numpy())
+    _, e = np.frexp(a)  # a = m * 2^e, m in [0.5, 1)
+    return np.ldexp(np.float64(1.0), np.maximum(e - 24, -149))
+
+
+def _within(ours, ref, scale_of, k, what):
+    """|ours - ref| <= k * ulp(scale_of) elementwise; returns the max ratio."""
+    import numpy as np
+    d = np.abs(ours.detach().cpu().numpy().astype(np.float64) - ref.detach().cpu().numpy().astype(np.float64))
+    u = _ulp(scale_of)
+    bad = ~(d <= k * u)  # k * u is exact (u is a power of two); NaN counts as bad
+    r = d / u
+    assert not bool(bad.any()), (f"{what}: {int(bad.sum())} elements beyond {k} ulp "
+                                 f"(max {float(np.max(r[np.isfinite(r)])):.3f})")
+    return float(np.max(r))
+
+
+def _ulp16_diff(a, b, dt):
+    """max ulp distance between two 16-bit tensors of the same sign pattern."""
+    import torch
+    ia = a.view(torch.int16).int()
+    ib = b.view(torch.int16).int()
+    # map sign-magnitude to a monotone integer line
+    ma = torch.where(ia < 0, -(ia & 0x7FFF), ia)
+    mb = torch.where(ib < 0, -(ib & 0x7FFF), ib)
+    return int((ma - mb).abs().max())
+
+
+@pytest.mark.parametrize("dtype_name,foreach", [("bfloat16", None), ("float16", None), ("bfloat16", False),
+                                                ("float16", False)])
+def test_fused_step_matches_torch_adamw_on_gpu(gpu, dtype_name, foreach):
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    dt = getattr(torch, dtype_name)
+    _say(f"fused step vs torch AdamW (foreach={foreach}) {dtype_name}")
+    n = 1 << 22
+    lr, betas, eps, wd, max_norm = 3e-4, (0.9, 0.95), 1e-8, 0.1, 1.0
+    gen = torch.Generator(device=gpu).manual_seed(21)
+    p0 = torch.randn(n, device=gpu, generator=gen) * 0.02
+    fp16 = dt == torch.float16
+    sc = (ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, window=3, hysteresis=1, min_scale=1.0) if fp16
+          else ScalerConfig(mode="none"))
+    mine = AdamWOptimizer([torch.nn.Parameter(p0.clone())], lr=lr, betas=betas, eps=eps, weight_decay=wd,
+                          max_grad_norm=max_norm, param_dtype=dt, loss_scaler=sc, device=gpu)
+    ref_p = torch.nn.Parameter(p0.clone())
+    ref = torch.optim.AdamW([ref_p], lr=lr, betas=betas, eps=eps, weight_decay=wd, foreach=foreach)
+    scale, good = (2.0 ** 16 if fp16 else 1.0), 0
+    worst = {"master": 0.0, "exp_avg": 0.0, "exp_avg_sq": 0.0}
+    for step in range(8):
+        sigma = 2e-4 if step % 2 else 3e-2  # alternate unclipped / clipped steps
+        g32 = torch.randn(n, device=gpu, generator=gen) * sigma * scale
+        g16 = g32.to(dt)
+        inject = fp16 and step == 3
+        if inject:
+            g16[12345] = float("inf")
+        mine.flat.grad.copy_(g16)
+        # -- ours --
+        mine.step()
+        s = mine.read_state()
+        # -- the reference's step at world size 1 --
+        p_before = ref_p.detach().clone()
+        st = ref.state.get(ref_p, {})
+        m_before = st["exp_avg"].clone() if st else torch.zeros_like(p0)
+        g = g16.float() * float(torch.tensor(1.0 / scale, dtype=torch.float32))
+        skipped = not bool(torch.isfinite(g).all())
+        if not skipped:
+            norm = math.sqrt(float(g.norm(2).item()) ** 2)
+            assert abs(s.last_norm - norm) <= 1e-6 * norm, f"step {step}: norm {s.last_norm} vs {norm}"
+            if s.last_norm > max_norm:
+                g.mul_(max_norm / (s.last_norm + 1e-6))
+            ref_p.grad = g
+            ref.step()
+        if fp16:  # GradScaler.update with growth_interval = window, hysteresis 1
+            if skipped:
+                scale, good = max(scale * 0.5, 1.0), 0
+            else:
+                good += 1
+                if good == 3:
+                    scale, good = scale * 2.0, 0
+        assert bool(s.last_skip) == skipped, f"step {step}: skip"
+        assert s.scale == scale, f"step {step}: scale {s.scale} vs {scale}"
+        if skipped:
+            continue
+        rs = ref.state[ref_p]
+        if foreach is None:  # torch's default: bit for bit
+            for name, a, b in (("master", mine.flat.master, ref_p.detach()), ("exp_avg", mine.flat.exp_avg, rs["exp_avg"]),
+                               ("exp_avg_sq", mine.flat.exp_avg_sq, rs["exp_avg_sq"])):
+                assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"step {step}: {name} not bit-identical"
+            assert torch.equal(mine.flat.param16.view(torch.int16), ref_p.detach().to(dt).view(torch.int16))
+            continue
+        # exp_avg: m + w*(g - m); exp_avg_sq: no cancellation
+        gc = ref_p.grad
+        worst["exp_avg"] = max(worst["exp_avg"], _within(
+            mine.flat.exp_avg, rs["exp_avg"], torch.maximum(torch.maximum(m_before.abs(), gc.abs()),
+                                                            rs["exp_avg"].abs()), 2, f"step {step} exp_avg"))
+        worst["exp_avg_sq"] = max(worst["exp_avg_sq"], _within(
+            mine.flat.exp_avg_sq, rs["exp_avg_sq"], rs["exp_avg_sq"], 2, f"step {step} exp_avg_sq"))
+        # master: p*decay + update
+        upd = (ref_p.detach() - p_before * (1 - lr * wd)).abs()
+        big = torch.maximum(torch.maximum((p_before * (1 - lr * wd)).abs(), upd), ref_p.detach().abs())
+        worst["master"] = max(worst["master"], _within(mine.flat.master, ref_p.detach(), big, 4,
+                                                       f"step {step} master"))
+        # 16-bit params: the cast of the master; compare with the cast of torch's fp32 param
+        assert _ulp16_diff(mine.flat.param16, ref_p.detach().to(dt), dt) <= 1, f"step {step}: param16"
+        # next step from torch's state: two trajectories that run apart would
+        # count a within-bar difference again wherever |p| is far below the update
+        with torch.no_grad():
+            mine.flat.master.copy_(ref_p.detach())
+            mine.flat.exp_avg.copy_(rs["exp_avg"])
+            mine.flat.exp_avg_sq.copy_(rs["exp_avg_sq"])
+            mine.flat.param16.copy_(mine.flat.master)
+    _say(f"worst ulp: {worst}")

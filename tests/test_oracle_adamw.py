@@ -1,18 +1,24 @@
 """Pins the oracle's AdamW element math (oracle/dsx_oracle.c) to the library
 routine the reference calls -- torch.optim.AdamW at Src/zero/stage1.py:522-525
-and Src/zero/stage2.py:609-612 -- run on the CPU here.
+and Src/zero/stage2.py:609-612.
 
 What is fixed, and how:
-  * exp_avg and exp_avg_sq: bit-identical to torch on hosts where torch's CPU
-    kernels are vectorised (AVX2/AVX512: lerp_ and addcmul_ are single fused
-    multiply-adds there); the one host-dependent op, sqrt, does not feed them.
-  * master: torch's CPU sqrt (MKL VML) is not correctly rounded and the
-    oracle's is, so the master may differ around the last place of the final
-    add p_new = p_decayed + u: within 3 ulp of max(|p_decayed|, |u|, |p_new|)
-    (one sqrt ulp moves u by up to ~1.5 ulp, plus the two roundings).
+  * bit for bit: torch.optim.AdamW with torch's default dispatch on a GPU
+    (the multi-tensor path, torch/optim/adam.py:554-800), recorded on an
+    MI355X in tests/golden/adamw_torch_gpu.npz -- master, exp_avg and
+    exp_avg_sq of every step, four hyper-parameter sets (both lerp branches,
+    weight_decay 0, beta 0), grads with 0, -0, 1e-20 and 65504 among them.
+  * against torch on this CPU (its kernels round differently: addcmul as
+    fma((1-b2)*g, g, v*b2), addcdiv as p + (s*m)/d, MKL's sqrt): exp_avg
+    equal in value on AVX2/AVX512 hosts (lerp is the same fused op there;
+    only the sign of a zero differs -- torch's CPU lerp gives -0 where its
+    GPU lerp gives +0 for g = -0, m = +0, weight 1), exp_avg_sq within
+    1 ulp, master within 4 ulp of the largest operand of the final add
+    p_new = p_decayed + u.
   * the first step's closed form p1 = p0(1 - lr wd) - lr g / (|g| + eps).
   * planted mistakes (a dropped term, a wrong index, a swapped operand) in the
-    oracle's scalars must break the torch comparison.
+    oracle's scalars must break the bit-exact GPU comparison and the 2-ulp
+    bar, while the unmodified oracle meets both.
 """
 from __future__ import annotations
 
@@ -79,8 +85,41 @@ def _grads(rng, n, steps, sigma):
     return gs
 
 
+def _golden_gpu():
+    import os
+    return np.load(os.path.join(os.path.dirname(__file__), "golden", "adamw_torch_gpu.npz"))
+
+
+def _replay_golden(O, z, k, scalar_hook=None):
+    """Runs the oracle over hyper set k of a golden file, one step at a time
+    from the recorded state; yields (t, ours, recorded, p_decayed)."""
+    lr, b1, b2, eps, wd = (float(x) for x in z[f"h{k}_hyper"])
+    h = O.Hyper(lr=lr, beta1=b1, beta2=b2, eps=eps, weight_decay=wd)
+    p = z[f"h{k}_p0"].copy()
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    for t in range(z[f"h{k}_grads"].shape[0]):
+        dec = p * np.float32(1 - lr * wd)
+        sc = O.step_scalars(h, t + 1, 1.0, 1.0)
+        if scalar_hook:
+            scalar_hook(sc, t + 1, h)
+        O.adamw(p, m, v, None, O.BF16, O.cast16(z[f"h{k}_grads"][t], O.BF16), O.BF16, sc)
+        rec = (z[f"h{k}_p"][t], z[f"h{k}_m"][t], z[f"h{k}_v"][t])
+        yield t, (p.copy(), m.copy(), v.copy()), rec, dec
+        p, m, v = (x.copy() for x in rec)
+
+
+@pytest.mark.parametrize("k", range(4))
+def test_oracle_bit_exact_against_torch_gpu_golden(oracle, k):
+    z = _golden_gpu()
+    assert str(z["foreach"]) == "None"  # torch's default dispatch
+    for t, ours, rec, _ in _replay_golden(oracle, z, k):
+        for name, a, b in zip(("master", "exp_avg", "exp_avg_sq"), ours, rec):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (k, t, name)
+
+
 @pytest.mark.parametrize("hi", range(len(HYPERS)))
-def test_oracle_matches_torch_adamw_single_tensor(oracle, hi):
+def test_oracle_near_torch_cpu_adamw(oracle, hi):
     h = HYPERS[hi]
     rng = np.random.default_rng(100 + hi)
     n = 50_003
@@ -94,30 +133,36 @@ def test_oracle_matches_torch_adamw_single_tensor(oracle, hi):
         sc = O.step_scalars(O.Hyper(**h), t, 1.0, 1.0)
         O.adamw(p, m, v, None, O.BF16, O.cast16(g, O.BF16), O.BF16, sc)
         if VECTORISED:
-            assert np.array_equal(m.view(np.uint32), tm.view(np.uint32)), f"t={t} exp_avg"
-            assert np.array_equal(v.view(np.uint32), tv.view(np.uint32)), f"t={t} exp_avg_sq"
+            assert (O.ulp_diff_f32(m, tm) == 0).all(), f"t={t} exp_avg"
+            assert (O.ulp_diff_f32(v, tv) <= 1).all(), f"t={t} exp_avg_sq"
         else:
             assert (O.ulp_diff_f32(m, tm) <= 2).all() and (O.ulp_diff_f32(v, tv) <= 2).all()
-        ok = cancellation_ulp_ok(p, tp, tp_dec, k=3)
-        assert ok.all(), f"t={t}: {np.count_nonzero(~ok)} master elements beyond 3 ulp"
+        ok = cancellation_ulp_ok(p, tp, tp_dec, k=4)
+        assert ok.all(), f"t={t}: {np.count_nonzero(~ok)} master elements beyond 4 ulp"
         frac_exact = np.mean(p == tp)
-        assert frac_exact > 0.9, f"t={t}: only {frac_exact:.4f} of master bit-identical"
+        assert frac_exact > 0.5, f"t={t}: only {frac_exact:.4f} of master bit-identical"
         p, m, v = tp.copy(), tm.copy(), tv.copy()
 
 
 def test_oracle_matches_torch_fused_and_foreach_within_tolerance(oracle):
+    """torch's CPU fused and foreach AdamW, one step at a time from torch's
+    own state (trajectories that run apart accumulate their differences where
+    |p| is far below the update)."""
+    O = oracle
     h = HYPERS[1]
     rng = np.random.default_rng(7)
     n = 20_011
     p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
     grads = _grads(rng, n, 3, 5e-4)
-    mine = _oracle_steps(oracle, p0, grads, h)
     for kw in (dict(fused=True), dict(foreach=True)):
         ref = _torch_steps(p0, grads, h, **kw)
-        for t, ((op, om, ov), (tp, tm, tv, tp_dec)) in enumerate(zip(mine, ref), start=1):
-            assert (oracle.ulp_diff_f32(om, tm) <= 2).all(), (kw, t)
-            assert (oracle.ulp_diff_f32(ov, tv) <= 2).all(), (kw, t)
-            assert cancellation_ulp_ok(op, tp, tp_dec, k=8).all(), (kw, t)
+        p, m, v = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+        for t, (g, (tp, tm, tv, tp_dec)) in enumerate(zip(grads, ref), start=1):
+            O.adamw(p, m, v, None, O.BF16, O.cast16(g, O.BF16), O.BF16, O.step_scalars(O.Hyper(**h), t, 1.0, 1.0))
+            assert (O.ulp_diff_f32(m, tm) <= 2).all(), (kw, t)
+            assert (O.ulp_diff_f32(v, tv) <= 2).all(), (kw, t)
+            assert cancellation_ulp_ok(p, tp, tp_dec, k=8).all(), (kw, t)
+            p, m, v = tp.copy(), tm.copy(), tv.copy()
 
 
 def test_first_step_closed_form(oracle):
@@ -143,40 +188,43 @@ def test_first_step_closed_form(oracle):
 @pytest.mark.parametrize("mistake", ["bc2_wrong_t", "no_weight_decay", "beta_not_complement", "eps_dropped",
                                      "step_size_sign"])
 def test_planted_mistakes_are_caught(oracle, mistake):
-    """A plausible error in the oracle's scalars must fail the torch pin."""
+    """A plausible error in the oracle's scalars must break the bit-exact
+    comparison with torch's GPU AdamW and the 2-ulp bar; the unmodified
+    oracle (checked first, same data) meets both."""
     O = oracle
-    h = HYPERS[0] if mistake != "eps_dropped" else dict(HYPERS[3], eps=1e-3)
-    rng = np.random.default_rng(11)
-    n = 4096
-    p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
-    grads = _grads(rng, n, 3, 1e-3)
+    z = _golden_gpu()
+    k = 3 if mistake == "eps_dropped" else 0  # set 3 has eps = 1e-3, where dropping it shows
 
-    def hook(sc, t):
+    def hook(sc, t, h):
         f32 = lambda x: float(np.float32(x))  # noqa: E731
         if mistake == "bc2_wrong_t":
-            sc.bc2s = f32((1 - h["beta2"] ** float(t + 1)) ** 0.5)
+            sc.bc2s = f32((1 - h.beta2 ** float(t + 1)) ** 0.5)
         elif mistake == "no_weight_decay":
             sc.decay = 1.0
         elif mistake == "beta_not_complement":
-            sc.w1 = f32(h["beta1"])
-            sc.w1m1 = f32(np.float32(sc.w1) - np.float32(1))
+            sc.w1 = f32(h.beta1)
+            sc.w1c = f32(np.float32(1) - np.float32(sc.w1))
         elif mistake == "eps_dropped":
             sc.eps = 0.0
         elif mistake == "step_size_sign":
             sc.nss = -sc.nss
 
-    mine = _oracle_steps(O, p0, grads, h, scalar_hook=hook)
-    ref = _torch_steps(p0, grads, h)
-    bad = False
-    for (op, om, ov), (tp, tm, tv, tp_dec) in zip(mine, ref):
-        bad |= not cancellation_ulp_ok(op, tp, tp_dec).all()
-        bad |= not (O.ulp_diff_f32(om, tm) <= 2).all()
-    assert bad, f"planted mistake {mistake} was not detected"
+    for hook_on in (False, True):
+        exact, within = True, True
+        for t, (op, om, ov), (tp, tm, tv), dec in _replay_golden(O, z, k, hook if hook_on else None):
+            exact &= all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in ((op, tp), (om, tm), (ov, tv)))
+            within &= bool(cancellation_ulp_ok(op, tp, dec, k=2).all()) and bool((O.ulp_diff_f32(om, tm) <= 2).all())
+        if hook_on:
+            assert not exact and not within, f"planted mistake {mistake} was not detected"
+        else:
+            assert exact and within, "the unmodified oracle must match"
 
 
 def test_oracle_against_golden_torch_vectors(oracle):
     """tests/golden/adamw_torch_cpu.npz: torch.optim.AdamW CPU outputs for four
-    hyper-parameter sets, five steps each, from zero state."""
+    hyper-parameter sets, five steps each, from zero state (within the CPU
+    tolerances above: torch's CPU kernels round differently from its GPU
+    kernels, which the oracle follows)."""
     import os
     O = oracle
     z = np.load(os.path.join(os.path.dirname(__file__), "golden", "adamw_torch_cpu.npz"))
@@ -193,12 +241,12 @@ def test_oracle_against_golden_torch_vectors(oracle):
             O.adamw(p, m, v, None, O.BF16, g16, O.BF16, O.step_scalars(h, t + 1, 1.0, 1.0))
             tp, tm, tv = z[f"h{k}_p"][t], z[f"h{k}_m"][t], z[f"h{k}_v"][t]
             if bitwise_mv:
-                assert np.array_equal(m.view(np.uint32), tm.view(np.uint32)), (k, t)
-                assert np.array_equal(v.view(np.uint32), tv.view(np.uint32)), (k, t)
+                assert (O.ulp_diff_f32(m, tm) == 0).all(), (k, t)
+                assert (O.ulp_diff_f32(v, tv) <= 1).all(), (k, t)
             else:
                 assert (O.ulp_diff_f32(m, tm) <= 2).all() and (O.ulp_diff_f32(v, tv) <= 2).all()
             dec = p_prev * np.float32(h.weight_decay and (1 - lr * wd) or 1.0)
-            assert cancellation_ulp_ok(p, tp, dec, k=3).all(), (k, t)
+            assert cancellation_ulp_ok(p, tp, dec, k=4).all(), (k, t)
             # continue from torch's master so every step is a single-step comparison
             p = tp.copy()
             m, v = tm.copy(), tv.copy()
