@@ -12,8 +12,9 @@ fused step:
                        the 16-bit parameter dtype under fp16/bf16)
   backward(loss)       ZeROOptimizer.backward: / accumulation, * loss scale
   step()               ZeROOptimizer.step (accumulation gate, fused step),
-                       then the LR scheduler and zero_grad, as DeepSpeed's
-                       engine does after a boundary step
+                       then the LR scheduler (not on a step skipped for
+                       overflow) and zero_grad, as DeepSpeed's engine does
+                       after a boundary step
   save_checkpoint / load_checkpoint   flat state keyed by parameter name
 """
 from __future__ import annotations
@@ -76,6 +77,13 @@ class DistributedSpeedEngine(torch.nn.Module):
                 "gradient_accumulation_steps": config.gradient_accumulation_steps}
         self.optimizer = ZeROOptimizer(optimizer, zcfg, list(optimizer.dsx_params))
         self.lr_scheduler = lr_scheduler
+        # DeepSpeed's engine leaves the LR scheduler alone on a step skipped for
+        # overflow. Under dynamic loss scaling the engine therefore needs the
+        # skip flag on the host; it is mirrored right after K0, so reading it
+        # waits for the norm pass only, not for the AdamW pass.
+        self._skip_aware = lr_scheduler is not None and optimizer.scaler.mode == "dynamic"
+        if self._skip_aware:
+            optimizer.track_skips(True)
         self.global_steps = 0
         self.micro_steps = 0
 
@@ -100,7 +108,8 @@ class DistributedSpeedEngine(torch.nn.Module):
         if boundary:
             self.global_steps += 1
             if self.lr_scheduler is not None:
-                self.lr_scheduler.step()
+                if not (self._skip_aware and self.optimizer.base_optimizer.last_step_skipped()):
+                    self.lr_scheduler.step()
             self.optimizer.base_optimizer.zero_grad()
 
     def zero_grad(self) -> None:

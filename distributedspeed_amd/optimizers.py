@@ -87,6 +87,34 @@ class _FusedAdamWBase(torch.optim.Optimizer):
         self._bc: dict[tuple[float, float], BiasCorrectionTable] = {}
         self._t_offsets = [0] * len(self.param_groups)
         self.steps_issued = 0
+        self._skip_host = None  # pinned mirror of DsxState.last_skip (see track_skips)
+        self._skip_event = None
+
+    # ---- skip flag on the host, without waiting for K2 ---------------------------------
+
+    def track_skips(self, on: bool = True) -> None:
+        """After every K0, copy DsxState.last_skip into pinned host memory
+        and record an event, so that last_step_skipped() waits for K1 and K0
+        only (not for K2). Costs one small device-to-host copy per step in
+        stream order; off by default."""
+        if on and self._skip_host is None:
+            self._skip_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+            self._skip_event = torch.cuda.Event()
+        elif not on:
+            self._skip_host = self._skip_event = None
+
+    def _after_finalize(self) -> None:
+        if self._skip_host is not None:
+            self._skip_host.copy_(self.dstate[36:40].view(torch.int32), non_blocking=True)  # DsxState.last_skip
+            self._skip_event.record(torch.cuda.current_stream(self.device))
+
+    def last_step_skipped(self) -> bool:
+        """Whether the last step was skipped (overflow). With track_skips on
+        this waits only for that step's K0; otherwise it synchronises."""
+        if self._skip_host is not None and self._skip_event is not None and self.steps_issued:
+            self._skip_event.synchronize()
+            return bool(int(self._skip_host[0]))
+        return bool(self.read_state().last_skip)
 
     # ---- torch.optim.Optimizer protocol ---------------------------------------------
 
@@ -277,10 +305,12 @@ class AdamWOptimizer(_FusedAdamWBase):
                 from .graph import GraphedStep
                 self._graph = GraphedStep(self)
             self._graph.replay(hs, tables, self._t_offsets, bc_len)
+            self._after_finalize()  # after the replay: waits for the graph's K2 too
             return
         s = ops.stream_of(self.device)
         self._k1(s)
         self._k0(self.scaler.to_c(), hs, tables, self._t_offsets, bc_len, s)
+        self._after_finalize()
         if self.streamer is not None:
             # State in pinned host memory: stream it through HBM chunk by chunk.
             # A skipped step streams too (K2 leaves the chunks unchanged), which
@@ -331,12 +361,14 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
         ops.unscale_norm_multi(table, self.dstate, self.partials, self.nparts)
         ops.finalize_groups(self.partials, self.nparts, self.dstate, self.scaler.to_c(), hs, tables,
                             self._t_offsets, bc_len, self.scalars)
+        self._after_finalize()
         ops.adamw_multi(table, self.scalars)
 
 
 def adopt_torch_optimizer(opt: torch.optim.Optimizer, contiguous: bool = True, **kwargs) -> _FusedAdamWBase:
     """torch.optim.AdamW (or Adam without weight decay, where Adam and AdamW
-    coincide) -> AdamWOptimizer over the same param groups and
+    coincide) -> AdamWOptimizer over the same param groups (the same dict
+    objects: a scheduler attached to `opt` keeps working) and
     hyper-parameters. Anything else is refused rather than silently changed
     into a different update rule."""
     if not isinstance(opt, torch.optim.Optimizer):
@@ -351,8 +383,10 @@ def adopt_torch_optimizer(opt: torch.optim.Optimizer, contiguous: bool = True, *
         raise NotImplementedError(f"{type(opt).__name__} is not supported by the fused step; use AdamW")
     if any(g.get("amsgrad") or g.get("maximize") for g in opt.param_groups):
         raise NotImplementedError("amsgrad / maximize are not supported by the fused step")
-    groups = [{k: v for k, v in g.items() if k in ("params", "lr", "betas", "eps", "weight_decay")}
-              for g in opt.param_groups]
+    # The group dicts themselves are handed over (torch's add_param_group keeps
+    # the dict it is given), so an LR scheduler built on `opt` -- which writes
+    # into these dicts -- drives the fused step too.
+    groups = list(opt.param_groups)
     d = opt.defaults
     cls = AdamWOptimizer if contiguous else MultiTensorAdamWOptimizer
     return cls(groups, lr=float(d["lr"]), betas=d["betas"], eps=d["eps"], weight_decay=d["weight_decay"], **kwargs)

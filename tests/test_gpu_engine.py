@@ -309,3 +309,37 @@ def test_engine_cpu_offload_config(gpu):
     assert opt.base_optimizer.read_state().t == 2
     with pytest.raises(ValueError):
         ds.initialize(_mlp(9), {"zero_optimization": {"cpu_offload": True}})  # fp32 params cannot offload
+
+
+def test_scheduler_on_adopted_optimizer_and_overflow_skip(gpu):
+    """A scheduler built on the user's torch.optim.AdamW drives the fused
+    step after initialize() adopts it, and (as in DeepSpeed's engine) is not
+    stepped on a step skipped for overflow; the skip flag is read on the host
+    from the pinned mirror written after K0."""
+    import torch
+    import distributedspeed_amd as ds
+    _say("scheduler + overflow skip")
+    torch.manual_seed(0)
+    model = torch.nn.Sequential(torch.nn.Linear(32, 64), torch.nn.ReLU(), torch.nn.Linear(64, 4)).to(gpu)
+    topt = torch.optim.AdamW(model.parameters(), lr=1e-3, weight_decay=0.0)
+    sched = torch.optim.lr_scheduler.LambdaLR(topt, lambda e: 0.5 ** e)
+    cfg = {"fp16": {"enabled": True, "initial_scale_power": 8, "hysteresis": 1}}
+    engine, opt, _, sch = ds.initialize(model, cfg, optimizer=topt, lr_scheduler=sched)
+    base = opt.base_optimizer
+    assert sch is sched and base.param_groups[0] is topt.param_groups[0]
+    gen = torch.Generator(device=gpu).manual_seed(4)
+    skips = []
+    for step in range(6):
+        x = torch.randn(8, 32, device=gpu, generator=gen)
+        loss = engine(x).float().pow(2).mean()
+        if step == 2:
+            loss = loss * float("inf")  # every grad becomes non-finite: the step is skipped
+        engine.backward(loss)
+        engine.step()
+        skips.append(base.last_step_skipped())
+        assert skips[-1] == bool(base.read_state().last_skip)
+    assert skips == [False, False, True, False, False, False]
+    assert sched.last_epoch == 5  # six boundaries, one skipped
+    assert base.param_groups[0]["lr"] == 1e-3 * 0.5 ** 5
+    st = base.read_state()
+    assert st.t == 5 and st.overflow_count == 1 and st.scale == 2.0 ** 7
