@@ -154,3 +154,45 @@ def test_fused_step_matches_torch_adamw_on_gpu(gpu, dtype_name, foreach):
             mine.flat.exp_avg_sq.copy_(rs["exp_avg_sq"])
             mine.flat.param16.copy_(mine.flat.master)
     _say(f"worst ulp: {worst}")
+
+
+def test_headline_shard_full_size_bit_identical_to_torch(gpu):
+    """configs[2] at its full size -- 1,003,782,656 elements, bf16 grads
+    N(0, 5e-4^2), lr 3e-4, betas (0.9, 0.95), eps 1e-8, wd 0.1, clip 1.0
+    (active: the norm is about 15.8) -- two steps of the fused step against
+    torch.optim.AdamW (default dispatch) on the same GPU: master, exp_avg,
+    exp_avg_sq and bf16 params bit-identical."""
+    import torch
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    _say("configs[2] full size vs torch AdamW")
+    n = 1_003_782_656
+    lr, betas, eps, wd, max_norm = 3e-4, (0.9, 0.95), 1e-8, 0.1, 1.0
+    gen = torch.Generator(device=gpu).manual_seed(2)
+    p0 = torch.empty(n, device=gpu).normal_(0.0, 0.02, generator=gen)
+    mine = AdamWOptimizer([torch.nn.Parameter(p0)], lr=lr, betas=betas, eps=eps, weight_decay=wd,
+                          max_grad_norm=max_norm, param_dtype=torch.bfloat16, device=gpu)
+    ref_p = torch.nn.Parameter(mine.flat.master.clone())  # same fp32 start (p0's storage was re-homed)
+    del p0
+    ref = torch.optim.AdamW([ref_p], lr=lr, betas=betas, eps=eps, weight_decay=wd)
+    for step in range(2):
+        g16 = mine.flat.grad
+        chunk = 1 << 27
+        for s in range(0, n, chunk):
+            e = min(n, s + chunk)
+            g16[s:e].copy_(torch.empty(e - s, device=gpu).normal_(0.0, 5e-4, generator=gen))
+        mine.step()
+        st = mine.read_state()
+        g = g16.float()
+        norm = float(g.norm(2).item())
+        assert abs(st.last_norm - norm) <= 1e-6 * norm and st.last_norm > max_norm, (st.last_norm, norm)
+        g.mul_(max_norm / (st.last_norm + 1e-6))
+        ref_p.grad = g
+        ref.step()
+        del g
+        ref_p.grad = None
+        rs = ref.state[ref_p]
+        for name, a, b in (("master", mine.flat.master, ref_p.detach()), ("exp_avg", mine.flat.exp_avg, rs["exp_avg"]),
+                           ("exp_avg_sq", mine.flat.exp_avg_sq, rs["exp_avg_sq"])):
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"step {step}: {name}"
+        assert torch.equal(mine.flat.param16.view(torch.int16), ref_p.detach().to(torch.bfloat16).view(torch.int16))
+        torch.cuda.synchronize()
