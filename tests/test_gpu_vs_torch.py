@@ -196,3 +196,75 @@ def test_headline_shard_full_size_bit_identical_to_torch(gpu):
             assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"step {step}: {name}"
         assert torch.equal(mine.flat.param16.view(torch.int16), ref_p.detach().to(torch.bfloat16).view(torch.int16))
         torch.cuda.synchronize()
+
+
+def _random_case(rng):
+    import torch
+    dt = [torch.float16, torch.bfloat16, None][int(rng.integers(3))]
+    ngroups = int(rng.integers(1, 4))
+    groups = []
+    for _ in range(ngroups):
+        sizes = [int(x) for x in rng.integers(1, 40_000, size=int(rng.integers(1, 4)))]
+        b1 = float(rng.choice([0.9, 0.5, 0.0, 0.3, 0.99, 0.8]))
+        b2 = float(rng.choice([0.999, 0.95, 0.0, 0.5, 0.9999]))
+        groups.append(dict(sizes=sizes, lr=float(10 ** rng.uniform(-5, -1.5)), betas=(b1, b2),
+                           eps=float(rng.choice([1e-8, 1e-6, 1e-3, 0.0])),
+                           weight_decay=float(rng.choice([0.0, 0.01, 0.1, 0.5]))))
+    max_norm = float(rng.choice([0.0, 1.0, 1e3]))
+    sigma = float(10 ** rng.uniform(-5, -1))
+    return dt, groups, max_norm, sigma
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_configurations_bit_identical_to_torch(gpu, case):
+    """Seeded random configurations -- sizes (odd, tiny), grad dtype fp16 /
+    bf16 / fp32, 1-3 parameter groups with their own lr / betas (both lerp
+    branches, beta1 = 0.5 exactly, beta = 0) / eps (0 included) / weight
+    decay, clipping off / active / inactive -- three steps against
+    torch.optim.AdamW (default dispatch) on the same GPU, bit for bit."""
+    import numpy as np
+    import torch
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    rng = np.random.default_rng(9000 + case)
+    dt, groups, max_norm, sigma = _random_case(rng)
+    _say(f"random case {case}: dtype={dt} groups={len(groups)} max_norm={max_norm} sigma={sigma:.2e}")
+    gen = torch.Generator(device=gpu).manual_seed(case)
+    inits = [[torch.randn(n, device=gpu, generator=gen) * 0.05 for n in g["sizes"]] for g in groups]
+    mine_groups, ref_groups, ref_params = [], [], []
+    for g, ini in zip(groups, inits):
+        hp = dict(lr=g["lr"], betas=g["betas"], eps=g["eps"], weight_decay=g["weight_decay"])
+        mine_groups.append(dict(hp, params=[torch.nn.Parameter(t.clone()) for t in ini]))
+        rp = [torch.nn.Parameter(t.clone()) for t in ini]
+        ref_params += rp
+        ref_groups.append(dict(hp, params=rp))
+    mine = AdamWOptimizer(mine_groups, max_grad_norm=max_norm, param_dtype=dt, device=gpu)
+    ref = torch.optim.AdamW(ref_groups)
+    # start from the master the flat partition holds (fp32 values of the inits)
+    for i, p in enumerate(ref_params):
+        with torch.no_grad():
+            p.copy_(mine.flat.views_of(i)["master"])
+    gdt = dt or torch.float32
+    for step in range(3):
+        gs = [(torch.randn(p.shape, device=gpu, generator=gen) * sigma).to(gdt) for p in ref_params]
+        for p, g in zip(mine.dsx_params, gs):
+            p.grad.copy_(g)
+        mine.step()
+        st = mine.read_state()
+        gf = [g.float() for g in gs]
+        norm = float(torch.linalg.vector_norm(torch.cat(gf)).item())
+        assert abs(st.last_norm - norm) <= 1e-6 * max(norm, 1e-30), (st.last_norm, norm)
+        if max_norm > 0 and st.last_norm > max_norm:
+            coef = max_norm / (st.last_norm + 1e-6)
+            for g in gf:
+                g.mul_(coef)
+        for p, g in zip(ref_params, gf):
+            p.grad = g
+        ref.step()
+        for i, p in enumerate(ref_params):
+            v = mine.flat.views_of(i)
+            s = ref.state[p]
+            for name, a, b in (("master", v["master"], p.detach()), ("exp_avg", v["exp_avg"], s["exp_avg"]),
+                               ("exp_avg_sq", v["exp_avg_sq"], s["exp_avg_sq"])):
+                assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"step {step} param {i}: {name}"
+            if dt is not None:
+                assert torch.equal(mine.dsx_params[i].detach().view(torch.int16), p.detach().to(dt).view(torch.int16))
