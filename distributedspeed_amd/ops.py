@@ -117,8 +117,14 @@ class Launch:
             raise _lib.DsxError(self.name, rc, _lib.last_error())
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> ctypes.c_void_p:
-    """torch's current HIP stream on `device` as the void* the ABI takes."""
+    """torch's current HIP stream on `device` as the void* the ABI takes
+    (the raw handle query, without building a Stream object)."""
+    if _RAW_STREAM is not None and device.index is not None:
+        return ctypes.c_void_p(_RAW_STREAM(device.index))
     return _stream(device)
 
 
@@ -239,13 +245,14 @@ class FinalizeGroups:
         if not 1 <= ngroups <= DSX_MAX_GROUPS:
             raise ValueError(f"need 1..{DSX_MAX_GROUPS} groups")
         _need(partials, "partials", torch.float64, None, dev, 8)
-        if nparts > partials.numel():
-            raise ValueError("nparts exceeds the partials buffer")
+        if not 1 <= nparts <= partials.numel():
+            raise ValueError("nparts must be in [1, partials.numel()]")
         _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
         _need(out, "scalars", torch.uint8, SCALARS_BYTES * ngroups, dev, 8)
         self.k = ngroups
-        self.fn = _lib.load().dsx_finalize_groups
+        self.name = "dsx_finalize_groups"
         self.head = (_ptr(partials), int(nparts), _ptr(state))
+        self.fn = getattr(_lib.load(), self.name)
         self.out = _ptr(out)
         self.hyper_t = DsxAdamwHyper * ngroups
         self.tab_t = ctypes.c_void_p * ngroups
@@ -256,13 +263,19 @@ class FinalizeGroups:
         k = self.k
         if len(hypers) != k or len(bc_tables) != k or len(t_offsets) != k:
             raise ValueError(f"expected {k} groups with one table and offset each")
-        for i, t in enumerate(bc_tables):
-            if t.dtype != torch.float64 or t.device.type != "cuda" or t.numel() < 2 * bc_len:
-                raise ValueError(f"bc_table[{i}] must be a float64 GPU tensor of at least {2 * bc_len} entries")
-        rc = self.fn(*self.head, scaler, self.hyper_t(*hypers), self.tab_t(*[t.data_ptr() for t in bc_tables]),
-                     self.off_t(*[int(x) for x in t_offsets]), k, int(bc_len), self.out, stream)
+        key = (tuple(map(id, bc_tables)), tuple(t_offsets), bc_len)
+        if key != getattr(self, "_key", None):  # tables / offsets checked and packed once per change
+            for i, t in enumerate(bc_tables):
+                if t.dtype != torch.float64 or t.device.type != "cuda" or t.numel() < 2 * bc_len:
+                    raise ValueError(f"bc_table[{i}] must be a float64 GPU tensor of at least {2 * bc_len} entries")
+            self._tabs = self.tab_t(*[t.data_ptr() for t in bc_tables])
+            self._offs = self.off_t(*[int(x) for x in t_offsets])
+            self._held = list(bc_tables)  # keep the tables (and their ids) alive while cached
+            self._key = key
+        rc = self.fn(*self.head, scaler, self.hyper_t(*hypers), self._tabs, self._offs, k, int(bc_len), self.out,
+                     stream)
         if rc:
-            raise _lib.DsxError("dsx_finalize_groups", rc, _lib.last_error())
+            raise _lib.DsxError(self.name, rc, _lib.last_error())
 
 
 GROUPS_BYTES = ctypes.sizeof(_lib.DsxGroupsDev)

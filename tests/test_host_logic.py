@@ -262,3 +262,33 @@ def test_ragged_chunk_size_fills_the_gpu():
     for n in (1 << 20, 1 << 27, 3 << 28):
         c = auto_chunk_elems(n)
         assert c % 8 == 0 and (c == 4096 or n // c >= 4096)
+
+
+def test_optimizer_step_hooks_still_run():
+    """AdamWOptimizer.step skips torch's per-call wrapper when nothing needs
+    it, and runs the step pre / post hooks (and the closure) when they are
+    registered; checked without a GPU by replacing the fused step."""
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    assert getattr(AdamWOptimizer.step, "hooked", False)  # torch does not wrap it again
+    calls = []
+
+    class Probe(AdamWOptimizer):
+        def __init__(self):  # no device state: only the protocol is exercised
+            torch.optim.Optimizer.__init__(self, [torch.nn.Parameter(torch.zeros(2))], dict(lr=1.0))
+
+        def step_fused(self):
+            calls.append("fused")
+
+    o = Probe()
+    assert o.step() is None and calls == ["fused"]
+    h1 = o.register_step_pre_hook(lambda opt, a, k: calls.append("pre"))
+    from torch.optim.optimizer import register_optimizer_step_post_hook
+    h2 = register_optimizer_step_post_hook(lambda opt, a, k: calls.append("post"))
+    try:
+        assert o.step(lambda: 3.0) == 3.0
+        assert calls == ["fused", "pre", "fused", "post"]
+    finally:
+        h1.remove()
+        h2.remove()
+    o.step()
+    assert calls[-1] == "fused" and calls.count("pre") == 1
