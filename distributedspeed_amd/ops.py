@@ -387,21 +387,30 @@ class ChunkTable:
         self.chunks = torch.frombuffer(bytearray(bytes(chunks)), dtype=torch.uint8).to(dev)
 
 
-def unscale_norm_multi(table: ChunkTable, state: torch.Tensor, partials: torch.Tensor, nparts: int) -> None:
+def plan_unscale_norm_multi(table: ChunkTable, state: torch.Tensor, partials: torch.Tensor, nparts: int) -> Launch:
     dev = table.device
     _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
     _need(partials, "partials", torch.float64, None, dev, 8)
     if nparts > partials.numel():
         raise ValueError("nparts exceeds the partials buffer")
-    _lib.call("dsx_unscale_norm_multi", _ptr(table.tensors), _ptr(table.chunks), table.nchunks, table.gdt,
-              _ptr(state), _ptr(partials), int(nparts), _stream(dev))
+    return Launch("dsx_unscale_norm_multi", _ptr(table.tensors), _ptr(table.chunks), ctypes.c_int64(table.nchunks),
+                  table.gdt, _ptr(state), _ptr(partials), int(nparts))
 
 
-def adamw_multi(table: ChunkTable, scalars: torch.Tensor) -> None:
-    """K3: AdamW + cast over the list; scalars holds table.ngroups entries."""
+def unscale_norm_multi(table: ChunkTable, state: torch.Tensor, partials: torch.Tensor, nparts: int) -> None:
+    """K1 over a ragged list: partials[:nparts] as unscale_norm."""
+    plan_unscale_norm_multi(table, state, partials, nparts)(_stream(table.device))
+
+
+def plan_adamw_multi(table: ChunkTable, scalars: torch.Tensor) -> Launch:
     dev = table.device
     _need(scalars, "scalars", torch.uint8, None, dev, 8)
     if scalars.numel() < SCALARS_BYTES * table.ngroups:
         raise ValueError(f"scalars must hold {table.ngroups} DsxStepScalars")
-    _lib.call("dsx_adamw_multi", _ptr(table.tensors), _ptr(table.chunks), table.nchunks, table.pdt, table.gdt,
-              _ptr(scalars), _stream(dev))
+    return Launch("dsx_adamw_multi", _ptr(table.tensors), _ptr(table.chunks), ctypes.c_int64(table.nchunks),
+                  table.pdt, table.gdt, _ptr(scalars))
+
+
+def adamw_multi(table: ChunkTable, scalars: torch.Tensor) -> None:
+    """K3: AdamW + cast over the list; scalars holds table.ngroups entries."""
+    plan_adamw_multi(table, scalars)(_stream(table.device))

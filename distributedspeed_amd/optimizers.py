@@ -380,21 +380,32 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
         self._graph = None
         self._init_device(self.store.numel)
         self._bind_state()
+        self._k0 = ops.FinalizeGroups(self.partials, self.nparts, self.dstate, self.scalars, len(self.param_groups))
+        self._plans_for = None  # the chunk table the bound K1 / K3 launches point at
+
+    def _plans(self):
+        table = self.store.table()
+        if table is not self._plans_for:  # rebuilt after storage moved: bind again
+            self._k1 = ops.plan_unscale_norm_multi(table, self.dstate, self.partials, self.nparts)
+            self._k3 = ops.plan_adamw_multi(table, self.scalars)
+            self._plans_for = table
+        return self._k1, self._k3
 
     def launch_norm(self) -> None:
-        ops.unscale_norm_multi(self.store.table(), self.dstate, self.partials, self.nparts)
+        k1, _ = self._plans()
+        k1(ops.stream_of(self.device))
 
     def step_fused(self) -> None:
         """K1 (list) -> K0 -> K3 on the current stream; no host synchronisation
         (a chunk-table rebuild, after storage moved, uploads the new table)."""
-        table = self.store.table()
+        k1, k3 = self._plans()
         self.steps_issued += 1
         hs, tables, bc_len = self._hypers()
-        ops.unscale_norm_multi(table, self.dstate, self.partials, self.nparts)
-        ops.finalize_groups(self.partials, self.nparts, self.dstate, self.scaler.to_c(), hs, tables,
-                            self._t_offsets, bc_len, self.scalars)
+        s = ops.stream_of(self.device)
+        k1(s)
+        self._k0(self.scaler.to_c(), hs, tables, self._t_offsets, bc_len, s)
         self._after_finalize()
-        ops.adamw_multi(table, self.scalars)
+        k3(s)
 
 
 def adopt_torch_optimizer(opt: torch.optim.Optimizer, contiguous: bool = True, **kwargs) -> _FusedAdamWBase:
