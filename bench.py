@@ -43,11 +43,12 @@ def _args():
                                                       "k2_adamw_flat_llama8b_shard_traffic.json"))
     ap.add_argument("--tuning", default="", help="k1_bpc,k2_bpc,k2_unroll,nt (library launch-shape override)")
     ap.add_argument("--workload", default="llama8b-shard",
-                    choices=["llama8b-shard", "llama-ragged", "llama70b-offload", "gpt2-small", "mlp"],
+                    choices=["llama8b-shard", "llama-ragged", "llama70b-offload", "gpt2-small", "mlp", "mlp-train"],
                     help="llama8b-shard: the headline flat step (K1/K0/K2); llama-ragged: configs[3]'s 289-tensor "
                          "list through K3; llama70b-offload: configs[4] with state in pinned host memory; "
                          "gpt2-small / mlp: configs[1] / configs[0] through the drop-in optimizer classes, eager, "
-                         "graph-replayed and ragged (secondary lines, not the headline)")
+                         "graph-replayed and ragged; mlp-train: a whole training iteration of configs[0]'s "
+                         "model, eager and captured in one graph (secondary lines, not the headline)")
     ap.add_argument("--pinned-budget-gib", type=float, default=32.0,
                     help="llama70b-offload: pinned host memory for the fp32 state (the shard shrinks to fit)")
     ap.add_argument("--profile-kernels", action="store_true",
@@ -198,6 +199,82 @@ def bench_dropin(a, dev) -> int:
         "config": {"workload": "gpt2-small fp16 (BASELINE configs[1])" if gpt2 else "mlp fp16 (BASELINE configs[0])",
                    "tensors": len(shapes), "numel": n, "best_mode": best},
         "modes": modes}), flush=True)
+    return 0
+
+
+def bench_mlp_train(a, dev) -> int:
+    """configs[0]'s MLP (784-1024-1024-10, fp16 params, static scale 2^16,
+    AdamW lr 1e-4 wd 0.01) trained on synthetic batches of 32: one whole
+    iteration -- zero_grad, forward, cross-entropy * loss scale, backward,
+    fused step -- run eagerly, and captured once into a HIP graph
+    (AdamWOptimizer(capturable=True)) and replayed with prepare_step()."""
+    import torch
+    import torch.nn.functional as F
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+
+    def make():
+        torch.manual_seed(0)
+        model = torch.nn.Sequential(torch.nn.Linear(784, 1024), torch.nn.ReLU(), torch.nn.Linear(1024, 1024),
+                                    torch.nn.ReLU(), torch.nn.Linear(1024, 10)).to(dev)
+        opt = AdamWOptimizer(model.parameters(), lr=1e-4, weight_decay=0.01, param_dtype=torch.float16,
+                             loss_scaler=ScalerConfig(mode="static", init_scale=2.0 ** 16), device=dev, capturable=True)
+        return model, opt
+
+    def iteration(model, opt, x, y):
+        opt.zero_grad()
+        loss = F.cross_entropy(model(x).float(), y)
+        (loss * opt.loss_scale_tensor()).backward()
+        opt.step()
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    x = torch.randn(32, 784, device=dev, generator=gen).half()
+    y = torch.randint(0, 10, (32,), device=dev, generator=gen)
+    res = {}
+    model, opt = make()
+    for _ in range(a.warmup):
+        iteration(model, opt, x, y)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(a.steps):
+        iteration(model, opt, x, y)
+    e1.record()
+    torch.cuda.synchronize()
+    res["eager_us_per_iter"] = round(e0.elapsed_time(e1) / a.steps * 1e3, 2)
+    model, opt = make()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for _ in range(max(3, a.warmup)):
+            iteration(model, opt, x, y)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        iteration(model, opt, x, y)
+    for _ in range(a.warmup):
+        opt.prepare_step()
+        graph.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(a.steps):
+        opt.prepare_step()
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    res["graph_us_per_iter"] = round(e0.elapsed_time(e1) / a.steps * 1e3, 2)
+    st = opt.read_state()
+    if st.error or st.last_skip:
+        print(json.dumps({"error": f"state error={st.error} skip={st.last_skip}"}))
+        return 1
+    print(json.dumps({
+        "metric": "training iteration (fwd + bwd + fused step) us, configs[0] MLP, batch 32",
+        "value": res["graph_us_per_iter"], "unit": "us/iter", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "higher_is_better": False, "dtype": "fp16 params/grads, f32 state", "data": "synthetic",
+        "config": {"workload": "mlp training iteration (BASELINE configs[0] model)", "batch": 32},
+        "modes": res, "speedup_graph_over_eager": round(res["eager_us_per_iter"] / res["graph_us_per_iter"], 3)}),
+        flush=True)
     return 0
 
 
@@ -455,6 +532,8 @@ def main() -> int:
         return bench_offload(a, dev)
     if a.workload in ("gpt2-small", "mlp"):
         return bench_dropin(a, dev)
+    if a.workload == "mlp-train":
+        return bench_mlp_train(a, dev)
     hyper = AdamWHyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     _progress(f"generating {n} elements")
     master, exp_avg, exp_avg_sq, p16, grad = make_inputs(n, 2, dev)

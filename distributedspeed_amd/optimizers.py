@@ -294,12 +294,14 @@ class AdamWOptimizer(_FusedAdamWBase):
                  weight_decay: float = 1e-2, *, max_grad_norm: float = 0.0, param_dtype: torch.dtype | None = None,
                  loss_scaler: ScalerConfig | None = None, device: torch.device | None = None,
                  param_names: dict | None = None, offload: bool = False, offload_chunk_elems: int = 64 << 20,
-                 graph: bool = False):
+                 graph: bool = False, capturable: bool = False):
         plist = self._init_common(params, lr, betas, eps, weight_decay, max_grad_norm, loss_scaler, device)
         if param_dtype is None and plist[0].dtype in (torch.float16, torch.bfloat16):
             param_dtype = plist[0].dtype
-        if graph and offload:
-            raise ValueError("graph=True needs HBM-resident state (offload=False)")
+        if (graph or capturable) and offload:
+            raise ValueError("graph=True / capturable=True need HBM-resident state (offload=False)")
+        if graph and capturable:
+            raise ValueError("graph=True captures the step itself; capturable=True is for callers that capture it")
         self.flat = FlatPartition([g["params"] for g in self.param_groups], self.device, param_dtype, param_names,
                                   offload=offload)
         self.store = self.flat
@@ -319,6 +321,49 @@ class AdamWOptimizer(_FusedAdamWBase):
                 if master.numel():
                     sc = self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
                     self._k2.append(ops.plan_adamw_flat(master, m, v, p16, g, sc))
+        self.capturable = bool(capturable)
+        if self.capturable:
+            # K0 reads the per-group values from device memory, so the launches
+            # can be recorded into a caller's graph and replayed.
+            self.groups_dev = torch.zeros(ops.GROUPS_BYTES, dtype=torch.uint8, device=self.device)
+            self._k0dev = ops.plan_finalize_dev(self.partials, self.nparts, self.dstate, self.scaler.to_c(),
+                                                self.groups_dev, len(self.param_groups), self.scalars)
+            self._uploaded = None
+            self._prepared = False
+
+    # ---- capturable form ----------------------------------------------------------------
+
+    def prepare_step(self) -> None:
+        """capturable=True: the host half of a step, outside any capture --
+        count the step, grow the bias-correction tables if needed, and upload
+        the per-group block (lr, betas, eps, weight decay, tables) when it
+        changed (a kernel launch in stream order; no host wait). Eager step()
+        calls it; a caller replaying a captured step calls it before each
+        replay."""
+        if not self.capturable:
+            raise RuntimeError("prepare_step() belongs to capturable=True")
+        self.steps_issued += 1
+        hs, tables, bc_len = self._hypers()
+        key = (tuple((h.lr, h.beta1, h.beta2, h.eps, h.weight_decay, h.max_grad_norm, h.clip_eps) for h in hs),
+               tuple(t.data_ptr() for t in tables), tuple(self._t_offsets), int(bc_len))
+        if key != self._uploaded:
+            ops.groups_upload(ops.pack_groups(hs, tables, self._t_offsets, bc_len), self.groups_dev)
+            self._uploaded = key
+        self._prepared = True
+
+    def _step_capturable(self) -> None:
+        capturing = torch.cuda.is_current_stream_capturing()
+        if not capturing and not self._prepared:
+            self.prepare_step()
+        self._prepared = False
+        self.flat.check_grads_bound()
+        s = ops.stream_of(self.device)
+        self._k1(s)
+        self._k0dev(s)
+        if not capturing:
+            self._after_finalize()
+        for k2 in self._k2:
+            k2(s)
 
     def launch_norm(self) -> None:
         """K1 alone over the current grads (partials <- squared norms)."""
@@ -327,6 +372,9 @@ class AdamWOptimizer(_FusedAdamWBase):
 
     def step_fused(self) -> None:
         """K1 -> K0 -> K2 on the current stream; no host synchronisation."""
+        if self.capturable:
+            self._step_capturable()
+            return
         self.flat.check_grads_bound()
         self.steps_issued += 1
         hs, tables, bc_len = self._hypers()

@@ -212,3 +212,72 @@ def test_graphed_optimizer_is_freed_by_refcount(gpu):
     finally:
         if was:
             gc.enable()
+
+
+def test_capturable_whole_iteration_in_one_graph(gpu):
+    """AdamWOptimizer(capturable=True): a small fp16 model's whole iteration
+    -- zero_grad, forward, loss * loss scale, backward, fused step -- is
+    captured into one HIP graph by the caller and replayed, with
+    prepare_step() before each replay; every replay is checked bit for bit
+    against the same iteration run eagerly on a twin model (an lr change and
+    an overflow-skipped step included), with unrelated eager work and a
+    host synchronisation between replays."""
+    import torch
+    import torch.nn.functional as F
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    _say("capturable: whole iteration in one graph")
+
+    def make():
+        torch.manual_seed(0)
+        model = torch.nn.Sequential(torch.nn.Linear(64, 128), torch.nn.GELU(), torch.nn.Linear(128, 16)).to(gpu)
+        opt = AdamWOptimizer(model.parameters(), lr=1e-3, max_grad_norm=1.0, param_dtype=torch.float16,
+                             loss_scaler=ScalerConfig(mode="dynamic", init_scale=2.0 ** 12, window=4, hysteresis=1),
+                             device=gpu, capturable=True)
+        return model, opt
+
+    def iteration(model, opt, x, y):
+        opt.zero_grad()
+        loss = F.mse_loss(model(x).float(), y)
+        (loss * opt.loss_scale_tensor()).backward()
+        opt.step()
+
+    gen = torch.Generator(device=gpu).manual_seed(5)
+    data = [(torch.randn(32, 64, device=gpu, generator=gen).half(), torch.randn(32, 16, device=gpu, generator=gen))
+            for _ in range(14)]
+    data[8][1][0, 0] = float("inf")  # an overflow: the step is skipped, the scale halves
+    m1, o1 = make()
+    m2, o2 = make()
+    sx, sy = data[0][0].clone(), data[0][1].clone()
+    side = torch.cuda.Stream(gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):  # warm-up (eager) on a side stream, as torch's graph capture asks
+        for x, y in data[:3]:
+            sx.copy_(x)
+            sy.copy_(y)
+            iteration(m2, o2, sx, sy)
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    for x, y in data[:3]:
+        iteration(m1, o1, x, y)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        iteration(m2, o2, sx, sy)
+    noise = torch.randn(1 << 16, device=gpu)
+    for i, (x, y) in enumerate(data[3:], start=3):
+        if i == 6:
+            for o in (o1, o2):
+                o.param_groups[0]["lr"] = 4e-4
+        iteration(m1, o1, x, y)
+        sx.copy_(x)
+        sy.copy_(y)
+        o2.prepare_step()
+        graph.replay()
+        noise.mul_(0.5).add_(1.0)  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        for name in ("master", "exp_avg", "exp_avg_sq", "param16"):
+            a, b = getattr(o1.flat, name), getattr(o2.flat, name)
+            assert torch.equal(a.view(torch.int16 if a.dtype == torch.float16 else torch.int32),
+                               b.view(torch.int16 if b.dtype == torch.float16 else torch.int32)), f"iter {i}: {name}"
+        assert torch.equal(o1.dstate, o2.dstate), f"iter {i}: state"
+    s = o2.read_state()
+    assert s.iter == 14 and s.overflow_count == 1 and s.t == 13
