@@ -41,6 +41,8 @@ def _args():
                     help="CPU time budget of the port's timed steps (torch's gets half)")
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                       "k2_adamw_flat_llama8b_shard_traffic.json"))
+    ap.add_argument("--torch-gpu", type=int, default=1,
+                    help="also time the reference's update as torch ops on this GPU (context line; 0 disables)")
     ap.add_argument("--tuning", default="", help="k1_bpc,k2_bpc,k2_unroll,nt (library launch-shape override)")
     ap.add_argument("--workload", default="llama8b-shard",
                     choices=["llama8b-shard", "llama-ragged", "llama70b-offload", "gpt2-small", "mlp", "mlp-train"],
@@ -437,6 +439,51 @@ def bench_offload(a, dev) -> int:
     return 0
 
 
+def torch_gpu_reference(master, grad16, hyper, ours_ms: float, steps: int = 5) -> dict:
+    """The reference's update at world size 1 as torch runs it on this GPU,
+    over the same shard: fp32 grads from the 16-bit ones, the norm with a
+    host read (Src/zero/utils.py:150), g *= max/(norm + 1e-6) when above the
+    threshold (utils.py:211-214), torch.optim.AdamW.step
+    (Src/zero/stage2.py:609-612; default dispatch = multi-tensor, and fused),
+    then the bf16 cast of the updated fp32 params. Timed with events around
+    `steps` steps after two warm-up steps; context only (not the headline)."""
+    import torch
+    _progress("torch reference path on the GPU")
+    p = torch.nn.Parameter(master.detach().clone())
+    p16 = torch.empty_like(p, dtype=torch.bfloat16)
+    res = {"what": "fp32 grad copy + norm (.item()) + clip + torch.optim.AdamW.step + bf16 cast, same shard"}
+    for name, kw in (("foreach", {}), ("fused", {"fused": True})):
+        opt = torch.optim.AdamW([p], lr=hyper.lr, betas=(hyper.beta1, hyper.beta2), eps=hyper.eps,
+                                weight_decay=hyper.weight_decay, **kw)
+
+        def step():
+            g = grad16.float()
+            norm = float(torch.linalg.vector_norm(g).item())
+            if norm > hyper.max_grad_norm:
+                g.mul_(hyper.max_grad_norm / (norm + 1e-6))
+            p.grad = g
+            opt.step()
+            p.grad = None
+            p16.copy_(p)
+
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        res[f"{name}_ms_per_step"] = round(ms, 3)
+        res[f"speedup_of_fused_step_over_{name}"] = round(ms / ours_ms, 2)
+        del opt
+    del p, p16
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(n_sample: int, hyper, seconds: float = 8.0) -> dict | None:
     """The C oracle (a CPU port of the step) on a bounded sample, on this
     host's cores, stepping until `seconds` of timed work (at least 3 steps);
@@ -489,6 +536,21 @@ def cpu_baseline(n_sample: int, hyper, seconds: float = 8.0) -> dict | None:
         param.detach().to(torch.bfloat16)
         ttimes.append(time.perf_counter() - t0)
     torch_s = sorted(ttimes[1:])[len(ttimes[1:]) // 2]
+    # torch's fused CPU AdamW on the same sample: the fastest CPU route torch has
+    fopt = torch.optim.AdamW([param], lr=hyper.lr, betas=(hyper.beta1, hyper.beta2), eps=hyper.eps,
+                             weight_decay=hyper.weight_decay, fused=True)
+    ftimes = []
+    while len(ftimes) < 4 or sum(ftimes[1:]) < seconds / 4:
+        t0 = time.perf_counter()
+        g = g16t.float()
+        norm = g.norm(dtype=torch.float32).item()
+        if norm > hyper.max_grad_norm:
+            g.mul_(hyper.max_grad_norm / (norm + 1e-6))
+        param.grad = g
+        fopt.step()
+        param.detach().to(torch.bfloat16)
+        ftimes.append(time.perf_counter() - t0)
+    fused_s = sorted(ftimes[1:])[len(ftimes[1:]) // 2]
     return {
         "value": round(n_sample / port_s / 1e9, 4),
         "unit": "Gparam/s",
@@ -500,6 +562,9 @@ def cpu_baseline(n_sample: int, hyper, seconds: float = 8.0) -> dict | None:
         "torch_adamw_cpu": {"value": round(n_sample / torch_s / 1e9, 4), "unit": "Gparam/s",
                             "threads": torch.get_num_threads(), "steps": len(ttimes) - 1,
                             "what": "torch.optim.AdamW(foreach=False) on CPU fp32 + fp32 norm/clip + bf16 cast"},
+        "torch_adamw_cpu_fused": {"value": round(n_sample / fused_s / 1e9, 4), "unit": "Gparam/s",
+                                  "threads": torch.get_num_threads(), "steps": len(ftimes) - 1,
+                                  "what": "torch.optim.AdamW(fused=True) on CPU, same sample and steps"},
     }
 
 
@@ -599,6 +664,7 @@ def main() -> int:
             traffic = None
 
     _progress("cpu baseline")
+    torch_gpu = torch_gpu_reference(master, grad, hyper, ms_step) if a.torch_gpu else None
     cpu = cpu_baseline(min(a.cpu_sample, n), hyper, a.cpu_seconds)
 
     out = {
@@ -627,6 +693,7 @@ def main() -> int:
                      "frac": round(k2_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k2_adamw_flat", "algorithmic_bytes_per_launch": K2_BYTES * n},
         "cpu_baseline": cpu,
+        "torch_gpu_reference_path": torch_gpu,
         "wall_s_timed": round(wall, 3),
         "torch": torch.__version__, "hip": torch.version.hip,
         "device": torch.cuda.get_device_name(dev),
