@@ -268,3 +268,48 @@ def test_random_configurations_bit_identical_to_torch(gpu, case):
                 assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"step {step} param {i}: {name}"
             if dt is not None:
                 assert torch.equal(mine.dsx_params[i].detach().view(torch.int16), p.detach().to(dt).view(torch.int16))
+
+
+def test_sixteen_groups_with_empty_and_single_element_groups(gpu):
+    """DSX_MAX_GROUPS parameter groups, one of them empty and one holding a
+    single element, each with its own lr / betas / eps / weight decay: three
+    steps bit for bit against torch.optim.AdamW (default dispatch)."""
+    import torch
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    _say("16 groups")
+    gen = torch.Generator(device=gpu).manual_seed(16)
+    sizes = [[37, 5], [], [1], [4096], [3, 3, 3], [1000], [8], [9], [17, 1], [2048], [513], [7], [64, 64], [1], [100],
+             [31]]
+    mine_groups, ref_groups, ref_params = [], [], []
+    for k, sz in enumerate(sizes):
+        hp = dict(lr=1e-4 * (k + 1), betas=(0.9 - 0.02 * k, 0.999 - 0.01 * k), eps=10.0 ** (-8 + k % 4),
+                  weight_decay=0.01 * (k % 3))
+        ini = [torch.randn(n, device=gpu, generator=gen) * 0.05 for n in sz]
+        mine_groups.append(dict(hp, params=[torch.nn.Parameter(t.clone()) for t in ini]))
+        rp = [torch.nn.Parameter(t.clone()) for t in ini]
+        ref_params += rp
+        ref_groups.append(dict(hp, params=rp))
+    mine = AdamWOptimizer(mine_groups, max_grad_norm=1.0, param_dtype=torch.bfloat16, device=gpu)
+    ref = torch.optim.AdamW(ref_groups)
+    for i, p in enumerate(ref_params):
+        with torch.no_grad():
+            p.copy_(mine.flat.views_of(i)["master"])
+    for step in range(3):
+        gs = [(torch.randn(p.shape, device=gpu, generator=gen) * 0.05).to(torch.bfloat16) for p in ref_params]
+        for p, g in zip(mine.dsx_params, gs):
+            p.grad.copy_(g)
+        mine.step()
+        st = mine.read_state()
+        gf = [g.float() for g in gs]
+        if st.last_norm > 1.0:
+            for g in gf:
+                g.mul_(1.0 / (st.last_norm + 1e-6))
+        for p, g in zip(ref_params, gf):
+            p.grad = g
+        ref.step()
+        for i, p in enumerate(ref_params):
+            v = mine.flat.views_of(i)
+            s = ref.state[p]
+            for name, a, b in (("master", v["master"], p.detach()), ("exp_avg", v["exp_avg"], s["exp_avg"]),
+                               ("exp_avg_sq", v["exp_avg_sq"], s["exp_avg_sq"])):
+                assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"step {step} param {i}: {name}"

@@ -292,3 +292,10 @@ def test_optimizer_step_hooks_still_run():
         h2.remove()
     o.step()
     assert calls[-1] == "fused" and calls.count("pre") == 1
+
+
+def test_more_than_sixteen_groups_is_refused():
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    groups = [{"params": [torch.nn.Parameter(torch.zeros(2))]} for _ in range(17)]
+    with pytest.raises(ValueError, match="at most 16 parameter groups"):
+        AdamWOptimizer(groups)
