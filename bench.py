@@ -197,8 +197,9 @@ def bench_dropin(a, dev) -> int:
         "metric": f"drop-in optimizer step Gparam/s ({'configs[1]' if gpt2 else 'configs[0]'})",
         "value": modes[best]["gparam_per_s"], "unit": "Gparam/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": modes[best]["ms_per_step"], "higher_is_better": True,
-        "dtype": "f32 state / fp16 grads+params", "data": "synthetic",
+        "dtype": "f32", "data": "synthetic",
         "config": {"workload": "gpt2-small fp16 (BASELINE configs[1])" if gpt2 else "mlp fp16 (BASELINE configs[0])",
+                   "storage": "f32 state / fp16 grads+params",
                    "tensors": len(shapes), "numel": n, "best_mode": best},
         "modes": modes}), flush=True)
     return 0
@@ -273,8 +274,9 @@ def bench_mlp_train(a, dev) -> int:
     print(json.dumps({
         "metric": "training iteration (fwd + bwd + fused step) us, configs[0] MLP, batch 32",
         "value": res["graph_us_per_iter"], "unit": "us/iter", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "higher_is_better": False, "dtype": "fp16 params/grads, f32 state", "data": "synthetic",
-        "config": {"workload": "mlp training iteration (BASELINE configs[0] model)", "batch": 32},
+        "higher_is_better": False, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "mlp training iteration (BASELINE configs[0] model)", "batch": 32,
+                   "storage": "fp16 params/grads, f32 state"},
         "modes": res, "speedup_graph_over_eager": round(res["eager_us_per_iter"] / res["graph_us_per_iter"], 3)}),
         flush=True)
     return 0
@@ -345,8 +347,8 @@ def bench_ragged(a, dev) -> int:
     print(json.dumps({
         "metric": "ragged multi-tensor ZeRO step Gparam/s (configs[3], K3)", "value": round(n / ms / 1e6, 3),
         "unit": "Gparam/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4),
-        "higher_is_better": True, "dtype": "f32 state / fp16 grads+params", "data": "synthetic",
-        "config": {"workload": "llama ragged list (BASELINE configs[3])", "tensors": len(sizes), "numel": n,
+        "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "llama ragged list (BASELINE configs[3])", "storage": "f32 state / fp16 grads+params", "tensors": len(sizes), "numel": n,
                    "chunks": table.nchunks},
         "achieved_tbps_end_to_end": round(30 * n / ms / 1e9, 4),
         "kernels_ms": {"k1_unscale_norm_multi": round(k1, 4), "k2_adamw_multi": round(k3, 4)},
@@ -423,9 +425,10 @@ def bench_offload(a, dev) -> int:
     print(json.dumps({
         "metric": "offloaded ZeRO step (configs[4]): Gparam/s and host-link GB/s each way",
         "value": round(n / sec / 1e9, 4), "unit": "Gparam/s", "n_gpus": 1, "steps": steps, "warmup": 1,
-        "ms_per_step": round(sec * 1e3, 1), "higher_is_better": True, "dtype": "f32 state (host) / bf16 grads+params",
+        "ms_per_step": round(sec * 1e3, 1), "higher_is_better": True, "dtype": "f32",
         "data": "synthetic", "config": {"workload": "llama3-70b zero3 one-rank shard, state offloaded "
-                                                    "(BASELINE configs[4])", "numel": n, "chunk_elems": chunk},
+                                                    "(BASELINE configs[4])",
+                                        "storage": "f32 state (pinned host) / bf16 grads+params", "numel": n, "chunk_elems": chunk},
         "link_gbs_each_way": round(each_way, 2), "link_ceiling_gbs": {k: round(x, 2) for k, x in link.items()},
         "frac_of_measured_bidirectional_link": round(each_way / link["both_each_way"], 4),
         "frac_of_one_direction_link": round(each_way / min(link["h2d"], link["d2h"]), 4),
@@ -675,10 +678,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 state / bf16 grads+params",
+        "dtype": "f32",
         "data": "synthetic (seeded torch generator on the GPU)",
         "config": {"workload": "llama3-8b zero2 one-rank shard (BASELINE configs[2])", "numel": n,
-                   "grad_dtype": "bf16", "param_dtype": "bf16", "lr": hyper.lr, "betas": [hyper.beta1, hyper.beta2],
+                   "grad_dtype": "bf16", "param_dtype": "bf16", "state_dtype": "f32", "lr": hyper.lr, "betas": [hyper.beta1, hyper.beta2],
                    "eps": hyper.eps, "weight_decay": hyper.weight_decay, "max_grad_norm": hyper.max_grad_norm,
                    "parallelism": "dp1 (one rank's ZeRO shard)"},
         "achieved_tbps_end_to_end": round(e2e_gbs / 1000, 4),
