@@ -144,3 +144,11 @@ class FlatPartition:
     def layout(self) -> list[dict]:
         return [{"name": s.name, "offset": s.offset, "numel": s.numel, "shape": list(s.shape), "group": s.group}
                 for s in self.slots]
+
+    def storage_bytes(self) -> dict:
+        """Bytes held by the partition's buffers (padding included). With fp32
+        training the params are views into the master: no separate bytes."""
+        state = sum(t.numel() * t.element_size() for t in (self.master, self.exp_avg, self.exp_avg_sq))
+        return {"params": self.param16.numel() * self.param16.element_size() if self.param16 is not None else 0,
+                "grads": self.grad.numel() * self.grad.element_size(),
+                "optimizer_states": state, "optimizer_states_on_host": self.offload}

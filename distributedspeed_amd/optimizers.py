@@ -91,6 +91,16 @@ class _FusedAdamWBase(torch.optim.Optimizer):
         self.steps_issued = 0
         self._skip_host = None  # pinned mirror of DsxState.last_skip (see track_skips)
         self._skip_event = None
+        self._adopted_from = None  # the torch optimizer whose param groups were adopted, if any
+
+    def _note_stepped(self) -> None:
+        """What torch's LR schedulers look for to know that the optimizer
+        stepped before them (the flag their step() wrapper sets): the step
+        usually runs through step_fused(), which that wrapper does not see,
+        and a scheduler may be attached to an adopted torch optimizer."""
+        self._opt_called = True
+        if self._adopted_from is not None:
+            self._adopted_from._opt_called = True
 
     # ---- skip flag on the host, without waiting for K2 ---------------------------------
 
@@ -372,6 +382,7 @@ class AdamWOptimizer(_FusedAdamWBase):
 
     def step_fused(self) -> None:
         """K1 -> K0 -> K2 on the current stream; no host synchronisation."""
+        self._note_stepped()
         if self.capturable:
             self._step_capturable()
             return
@@ -446,6 +457,7 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
     def step_fused(self) -> None:
         """K1 (list) -> K0 -> K3 on the current stream; no host synchronisation
         (a chunk-table rebuild, after storage moved, uploads the new table)."""
+        self._note_stepped()
         k1, k3 = self._plans()
         self.steps_issued += 1
         hs, tables, bc_len = self._hypers()
@@ -480,4 +492,6 @@ def adopt_torch_optimizer(opt: torch.optim.Optimizer, contiguous: bool = True, *
     groups = list(opt.param_groups)
     d = opt.defaults
     cls = AdamWOptimizer if contiguous else MultiTensorAdamWOptimizer
-    return cls(groups, lr=float(d["lr"]), betas=d["betas"], eps=d["eps"], weight_decay=d["weight_decay"], **kwargs)
+    new = cls(groups, lr=float(d["lr"]), betas=d["betas"], eps=d["eps"], weight_decay=d["weight_decay"], **kwargs)
+    new._adopted_from = opt
+    return new

@@ -122,6 +122,14 @@ class RaggedParams:
             for p, m in zip(self.params, self.master):
                 p.data.copy_(m)
 
+    def storage_bytes(self) -> dict:
+        """Bytes held per the layout: 16-bit params (with fp32 training the
+        param is the master), grads of the grad dtype, fp32 master/m/v."""
+        elt16 = 2 if self.param_dtype is not None else 0
+        return {"params": elt16 * self.numel,
+                "grads": self.numel * torch.empty(0, dtype=self.grad_dtype).element_size(),
+                "optimizer_states": 12 * self.numel, "optimizer_states_on_host": False}
+
     def layout(self) -> list[dict]:
         out, off = [], 0
         for p, name, gi in zip(self.params, self.names, self.group_of):

@@ -7,6 +7,7 @@ from __future__ import annotations
 import math
 import os
 import sys
+import warnings
 
 import numpy as np
 import pytest
@@ -118,7 +119,7 @@ def _run_training(gpu, oracle, ds_config, steps, seed=0, groups=None, scheduler=
             assert bool(st.last_skip) == skipped, f"step {step}: skip {st.last_skip} vs {skipped}"
             assert st.scale == spec.scale, f"step {step}: scale {st.scale} vs {spec.scale}"
             orc.compare(base, f"step {step}")
-            log.append((skipped, st.scale, float(loss)))
+            log.append((skipped, st.scale, float(loss.detach())))
     return engine, log
 
 
@@ -329,17 +330,77 @@ def test_scheduler_on_adopted_optimizer_and_overflow_skip(gpu):
     assert sch is sched and base.param_groups[0] is topt.param_groups[0]
     gen = torch.Generator(device=gpu).manual_seed(4)
     skips = []
-    for step in range(6):
-        x = torch.randn(8, 32, device=gpu, generator=gen)
-        loss = engine(x).float().pow(2).mean()
-        if step == 2:
-            loss = loss * float("inf")  # every grad becomes non-finite: the step is skipped
-        engine.backward(loss)
-        engine.step()
-        skips.append(base.last_step_skipped())
-        assert skips[-1] == bool(base.read_state().last_skip)
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        for step in range(6):
+            x = torch.randn(8, 32, device=gpu, generator=gen)
+            loss = engine(x).float().pow(2).mean()
+            if step == 2:
+                loss = loss * float("inf")  # every grad becomes non-finite: the step is skipped
+            engine.backward(loss)
+            engine.step()
+            skips.append(base.last_step_skipped())
+            assert skips[-1] == bool(base.read_state().last_skip)
+    # the scheduler sees that the optimizer stepped before it (no order warning)
+    assert not [w for w in caught if "lr_scheduler.step()" in str(w.message)]
     assert skips == [False, False, True, False, False, False]
     assert sched.last_epoch == 5  # six boundaries, one skipped
     assert base.param_groups[0]["lr"] == 1e-3 * 0.5 ** 5
     st = base.read_state()
     assert st.t == 5 and st.overflow_count == 1 and st.scale == 2.0 ** 7
+
+
+def test_zero_optimizer_counters_and_accessors(gpu):
+    """The reference's ZeROOptimizer counters and accessors
+    (Src/zero/optimizer.py:212-274, 407-559): current_step counts clean
+    optimizer steps only (an overflow-skipped step and accumulation-only calls
+    do not), overflow_count the skipped ones; both survive state_dict /
+    load_state_dict and reset_stats clears overflow_count; the memory figures
+    are this layout's bytes (2-byte params and grads, 12 bytes of fp32 state per
+    padded element)."""
+    import torch
+    import distributedspeed_amd as ds
+    _say("ZeROOptimizer counters and accessors")
+    torch.manual_seed(1)
+    model = torch.nn.Sequential(torch.nn.Linear(32, 64), torch.nn.ReLU(), torch.nn.Linear(64, 4))
+    cfg = {"fp16": {"enabled": True, "initial_scale_power": 8, "hysteresis": 1},
+           "gradient_accumulation_steps": 2, "zero_optimization": {"stage": 1}}
+    engine, opt, _, _ = ds.initialize(model, cfg)
+    gen = torch.Generator(device=gpu).manual_seed(2)
+    for it in range(5):
+        for micro in range(2):
+            with opt.no_sync():
+                loss = engine(torch.randn(8, 32, device=gpu, generator=gen)).float().pow(2).mean()
+                if it == 1 and micro == 1:
+                    loss = loss * float("inf")
+                engine.backward(loss)
+            engine.step()
+    assert opt.current_step == 4 and opt.overflow_count == 1
+    thr = opt.get_throughput_stats()
+    assert set(thr) == {"steps_per_second", "avg_step_time", "overflow_rate"}
+    assert thr["overflow_rate"] == 0.25
+    assert opt.get_communication_stats()["total_comm_bytes"] == 0
+
+    numel = opt.base_optimizer.numel
+    assert numel % 8 == 0 and numel >= sum(p.numel() for p in model.parameters())
+    est = opt.estimate_memory_usage()
+    assert est["parameters_gb"] == est["gradients_gb"] == 2 * numel / 1e9
+    assert est["optimizer_states_gb"] == 12 * numel / 1e9
+    assert est["memory_per_gpu_gb"] == est["total_gb"] == pytest.approx(16 * numel / 1e9, rel=1e-12)
+    info = opt.get_memory_info()
+    assert info["allocated_gb"] > 0 and info["optimizer_states_on_host"] is False
+    gp = opt.gather_params()
+    assert list(gp) == [f"param_{i}" for i in range(4)] and gp["param_0"] is opt.model_parameters[0]
+    assert opt.partition_params(gp) is None
+
+    sd = opt.state_dict()
+    assert sd["current_step"] == 4 and sd["overflow_count"] == 1
+    opt.reset_stats()
+    assert opt.overflow_count == 0 and opt.current_step == 4
+    opt.load_state_dict(sd)
+    assert opt.current_step == 4 and opt.overflow_count == 1
+    sd["current_step"], sd["overflow_count"] = 10, 3
+    opt.load_state_dict(sd)
+    assert opt.current_step == 10 and opt.overflow_count == 3
+    opt.current_step = 7
+    assert opt.current_step == 7 and opt.base_optimizer.read_state().t == 4

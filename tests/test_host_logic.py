@@ -148,6 +148,26 @@ def test_flat_rejects_duplicates_and_bad_dtype():
         FlatPartition([[torch.nn.Parameter(torch.zeros(3))]], torch.device("cpu"), None, offload=True)
 
 
+def test_storage_bytes_of_both_forms():
+    """What get_memory_info / estimate_memory_usage report: 16-bit params and
+    grads plus 12 bytes of fp32 state per element (padding included in the
+    flat form); with fp32 training the params are the master (no extra bytes)."""
+    from distributedspeed_amd.ragged import RaggedParams
+    fp = FlatPartition([_params([(3, 5), (7,)])], torch.device("cpu"), torch.bfloat16)
+    assert fp.numel == 24
+    assert fp.storage_bytes() == {"params": 48, "grads": 48, "optimizer_states": 288,
+                                  "optimizer_states_on_host": False}
+    f32 = FlatPartition([_params([(9,)])], torch.device("cpu"), None)
+    assert f32.numel == 16
+    assert f32.storage_bytes() == {"params": 0, "grads": 64, "optimizer_states": 192,
+                                   "optimizer_states_on_host": False}
+    rp = RaggedParams([_params([(3, 5), (7,)])], torch.device("cpu"), torch.float16)
+    assert rp.storage_bytes() == {"params": 44, "grads": 44, "optimizer_states": 264,
+                                  "optimizer_states_on_host": False}
+    r32 = RaggedParams([_params([(9,)])], torch.device("cpu"), None)
+    assert r32.storage_bytes()["params"] == 0 and r32.storage_bytes()["grads"] == 36
+
+
 def test_layout_manifest_names():
     lin = torch.nn.Linear(2, 2)
     names = {id(p): n for n, p in lin.named_parameters()}
