@@ -488,8 +488,9 @@ def torch_gpu_reference(master, grad16, hyper, ours_ms: float, steps: int = 5) -
 
 
 def cpu_baseline(n_sample: int, hyper, seconds: float = 8.0) -> dict | None:
-    """The C oracle (a CPU port of the step) on a bounded sample, on this
-    host's cores, stepping until `seconds` of timed work (at least 3 steps);
+    """The C oracle (a CPU port of the step: the norm as 1024 compensated
+    block sums, the AdamW loop, both on OpenMP threads) on a bounded sample,
+    on this host's cores, stepping until `seconds` of timed work (at least 3 steps);
     plus torch.optim.AdamW on CPU (the reference's cpu_offload route) on the
     same sample for half that budget, for context."""
     if n_sample <= 0:
@@ -514,7 +515,7 @@ def cpu_baseline(n_sample: int, hyper, seconds: float = 8.0) -> dict | None:
     while t < 4 or sum(times[1:]) < seconds:
         t += 1
         t0 = time.perf_counter()
-        ss = O.sumsq(g16, O.BF16, 1.0)
+        ss = O.sumsq_parallel(g16, O.BF16, 1.0, 1024)
         coef = O.clip_coef(ss ** 0.5, h.max_grad_norm, h.clip_eps)
         O.adamw(p, m, v, p16, O.BF16, g16, O.BF16, O.step_scalars(h, t, 1.0, coef))
         times.append(time.perf_counter() - t0)
@@ -560,7 +561,8 @@ def cpu_baseline(n_sample: int, hyper, seconds: float = 8.0) -> dict | None:
         "cores": int(O.lib().dsxo_num_threads()),
         "kind": "port",
         "sample": f"{n_sample} elements of the same workload (bf16 grads N(0,5e-4^2), fp32 state), "
-                  f"one full step (norm + clip + AdamW + cast); median of {len(times) - 1} steps "
+                  f"one full step (norm in 1024 compensated blocks + clip + AdamW + cast, all on OpenMP "
+                  f"threads); median of {len(times) - 1} steps "
                   f"({sum(times[1:]):.1f} s) after 1 warm-up",
         "torch_adamw_cpu": {"value": round(n_sample / torch_s / 1e9, 4), "unit": "Gparam/s",
                             "threads": torch.get_num_threads(), "steps": len(ttimes) - 1,

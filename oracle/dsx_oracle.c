@@ -145,12 +145,37 @@ double dsxo_sumsq_blocked(const void* g, int dt, int64_t n, float inv_scale, int
   return total;
 }
 
-static inline void step_elt(float graw, float* p, float* m, float* v, const DsxoScalars* s) {
+/* dsxo_sumsq_blocked with the blocks summed in parallel (OpenMP) and then
+ * added in block order: the same value, bit for bit, on any thread count.
+ * Used where the oracle is timed (the CPU baseline). */
+double dsxo_sumsq_parallel(const void* g, int dt, int64_t n, float inv_scale, int64_t nblocks) {
+  enum { kMaxBlocks = 4096 };
+  double part[kMaxBlocks];
+  if (nblocks < 1) nblocks = 1;
+  if (nblocks > kMaxBlocks) nblocks = kMaxBlocks;
+  const int64_t per = (n + nblocks - 1) / nblocks;
+  const size_t esz = dt == DSXO_F32 ? 4 : 2;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t b = 0; b < nblocks; ++b) {
+    const int64_t lo = b * per, hi = lo + per < n ? lo + per : n;
+    part[b] = lo < n ? dsxo_sumsq((const char*)g + (size_t)lo * esz, dt, hi - lo, inv_scale) : 0.0;
+  }
+  double total = 0.0;
+  for (int64_t b = 0; b < nblocks; ++b) {
+    if (b * per >= n) break;
+    total += part[b];
+  }
+  return total;
+}
+
+/* One element of the step. `small` selects lerp's form (|w1| < 0.5); it is
+ * a constant at each call site, so the branch leaves the loops below. */
+static inline void step_elt(float graw, float* p, float* m, float* v, const DsxoScalars* s, int small) {
   float g = graw * s->inv_scale;
   g = g * s->clip_coef;
   float pp = *p * s->decay;
   const float d = g - *m;
-  const float mm = (fabsf(s->w1) < 0.5f) ? fmaf(s->w1, d, *m) : fmaf(-d, s->w1c, g);
+  const float mm = small ? fmaf(s->w1, d, *m) : fmaf(-d, s->w1c, g);
   float vv = *v * s->b2;
   vv = fmaf(s->val2, g * g, vv);
   const float den = sqrtf(vv) / s->bc2s + s->eps;
@@ -160,15 +185,46 @@ static inline void step_elt(float graw, float* p, float* m, float* v, const Dsxo
   *v = vv;
 }
 
+enum { kChunk = 512 };
+
+/* Elements [0, len) of one chunk: grads widened into a local array, the
+ * element math in a loop without branches (vectorised by the compiler; the
+ * arithmetic and its rounding are those of step_elt), then the cast. */
+static void adamw_chunk(float* restrict p, float* restrict m, float* restrict v, uint16_t* restrict p16, int pdt,
+                        const void* g, int gdt, int64_t len, const DsxoScalars* s, int small) {
+  float gw[kChunk];
+  if (gdt == DSXO_BF16) {
+    const uint16_t* h = (const uint16_t*)g;
+    for (int64_t i = 0; i < len; ++i) gw[i] = u2f((uint32_t)h[i] << 16);
+  } else {
+    for (int64_t i = 0; i < len; ++i) gw[i] = load_grad(g, i, gdt);
+  }
+  if (small) {
+    for (int64_t i = 0; i < len; ++i) step_elt(gw[i], p + i, m + i, v + i, s, 1);
+  } else {
+    for (int64_t i = 0; i < len; ++i) step_elt(gw[i], p + i, m + i, v + i, s, 0);
+  }
+  if (!p16) return;
+  if (pdt == DSXO_BF16) {
+    for (int64_t i = 0; i < len; ++i) p16[i] = dsxo_f32_to_bf16(p[i]);
+  } else {
+    for (int64_t i = 0; i < len; ++i) p16[i] = dsxo_f32_to_f16(p[i]);
+  }
+}
+
 /* One AdamW step over n elements, in place; p16 (may be NULL) receives the
  * cast master. Grads are 16-bit storage (gdt F16/BF16) or fp32 (gdt F32).
- * Elements are independent, so the loop may run in parallel. */
+ * Elements are independent, so chunks run in parallel. */
 void dsxo_adamw(float* p, float* m, float* v, uint16_t* p16, int pdt, const void* g, int gdt, int64_t n,
                 const DsxoScalars* s) {
+  const int small = fabsf(s->w1) < 0.5f;
+  const size_t gsz = gdt == DSXO_F32 ? 4 : 2;
+  const int64_t nchunks = (n + kChunk - 1) / kChunk;
 #pragma omp parallel for schedule(static)
-  for (int64_t i = 0; i < n; ++i) {
-    step_elt(load_grad(g, i, gdt), p + i, m + i, v + i, s);
-    if (p16) p16[i] = pdt == DSXO_BF16 ? dsxo_f32_to_bf16(p[i]) : dsxo_f32_to_f16(p[i]);
+  for (int64_t c = 0; c < nchunks; ++c) {
+    const int64_t lo = c * kChunk, len = n - lo < kChunk ? n - lo : kChunk;
+    adamw_chunk(p + lo, m + lo, v + lo, p16 ? p16 + lo : NULL, pdt, (const char*)g + (size_t)lo * gsz, gdt, len, s,
+                small);
   }
 }
 

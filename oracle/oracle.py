@@ -63,6 +63,8 @@ def lib() -> ctypes.CDLL:
         L.dsxo_sumsq.argtypes = [P, ctypes.c_int, ctypes.c_int64, ctypes.c_float]
         L.dsxo_sumsq_blocked.restype = ctypes.c_double
         L.dsxo_sumsq_blocked.argtypes = [P, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_int64]
+        L.dsxo_sumsq_parallel.restype = ctypes.c_double
+        L.dsxo_sumsq_parallel.argtypes = [P, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_int64]
         L.dsxo_adamw.restype = None
         L.dsxo_adamw.argtypes = [P, P, P, P, ctypes.c_int, P, ctypes.c_int, ctypes.c_int64,
                                  ctypes.POINTER(_Scalars)]
@@ -124,6 +126,13 @@ def sumsq(g16: np.ndarray, dt: int, inv_scale: float, blocks: int = 0) -> float:
     if blocks:
         return lib().dsxo_sumsq_blocked(_ptr(g16), dt, g16.size, inv_scale, blocks)
     return lib().dsxo_sumsq(_ptr(g16), dt, g16.size, inv_scale)
+
+
+def sumsq_parallel(g16: np.ndarray, dt: int, inv_scale: float, blocks: int = 1024) -> float:
+    """sumsq(..., blocks=blocks) with the blocks summed on all OpenMP threads
+    (bit-identical to it); for timing the oracle as a CPU baseline."""
+    _check(g16, _gdtype(dt))
+    return lib().dsxo_sumsq_parallel(_ptr(g16), dt, g16.size, inv_scale, blocks)
 
 
 # ---- hyper-parameters and per-step scalars ---------------------------------------

@@ -250,3 +250,33 @@ def test_oracle_against_golden_torch_vectors(oracle):
             # continue from torch's master so every step is a single-step comparison
             p = tp.copy()
             m, v = tm.copy(), tv.copy()
+
+
+@pytest.mark.parametrize("n", [0, 1, 511, 512, 513, 5000])
+@pytest.mark.parametrize("hi", range(len(HYPERS)))
+def test_step_same_for_every_grad_storage_and_cast_matches(oracle, n, hi):
+    """The step runs in chunks with the grad dtype and lerp form decided per
+    call: grads that are exactly representable in fp16, bf16 and fp32 (k/64
+    for small integers k) must give bit-identical master/m/v through all three
+    storages, and the 16-bit params it writes must be the casts of the master
+    (the casts are pinned on their own against numpy / torch)."""
+    O = oracle
+    rng = np.random.default_rng(100 + n)
+    g32 = (rng.integers(-64, 65, n) / 64.0).astype(np.float32)
+    p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    m0 = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    v0 = np.abs(rng.standard_normal(n) * 1e-6).astype(np.float32)
+    sc = O.step_scalars(O.Hyper(**HYPERS[hi]), 3, 1.0, 0.75)
+    outs = []
+    for gdt, gin, pdt in ((O.F32, g32, O.BF16), (O.BF16, O.cast16(g32, O.BF16), O.F16),
+                          (O.F16, O.cast16(g32, O.F16), O.BF16)):
+        if gdt != O.F32:
+            assert np.array_equal(O.widen16(gin, gdt), g32)
+        p, m, v = p0.copy(), m0.copy(), v0.copy()
+        p16 = np.empty(n, np.uint16)
+        O.adamw(p, m, v, p16, pdt, gin, gdt, sc)
+        assert np.array_equal(p16, O.cast16(p, pdt))
+        outs.append((p, m, v))
+    for p, m, v in outs[1:]:
+        for a, b in zip((p, m, v), outs[0]):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

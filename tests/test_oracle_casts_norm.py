@@ -93,6 +93,22 @@ def test_sumsq_against_fp64_brute_force(oracle, dt):
     assert math.sqrt(got) == pytest.approx(float(tn), rel=1e-13)
 
 
+@pytest.mark.parametrize("n,blocks", [(1_000_003, 1021), (5, 16), (0, 8), (4097, 4096), (70_001, 9000)])
+def test_parallel_blocked_sumsq_is_the_blocked_sum(oracle, n, blocks):
+    """The OpenMP form used for the CPU-baseline timing adds the same block
+    sums in the same order as the serial blocked form (blocks past the end,
+    and more blocks than its cap of 4096, included), so it returns the same
+    bits; and a non-finite grad still makes it non-finite."""
+    rng = np.random.default_rng(n)
+    g16 = oracle.cast16((rng.standard_normal(n) * 5e-4).astype(np.float32), oracle.BF16)
+    serial = oracle.sumsq(g16, oracle.BF16, 1.0, blocks=min(blocks, 4096))
+    par = oracle.sumsq_parallel(g16, oracle.BF16, 1.0, blocks)
+    assert np.float64(par).view(np.uint64) == np.float64(serial).view(np.uint64)
+    if n:
+        g16[n // 3] = 0x7F80  # +inf
+        assert not math.isfinite(oracle.sumsq_parallel(g16, oracle.BF16, 1.0, blocks))
+
+
 @pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
 @pytest.mark.parametrize("pos", [0, 5, 1023, 1024])
 def test_nonfinite_detection_matches_torch_unscale(oracle, bad, pos):
