@@ -164,6 +164,12 @@ const char* dsx_last_error(void);
 int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll,
                    int nontemporal);
 
+/* K2's grid size: k2_blocks_per_cu blocks on k2_cu_eighths eighths of the
+ * CUs (1..8; default 7: on MI355X a block on 7 of every 8 CUs moves K2's
+ * 50:50 read/write stream faster than one on every CU). No counterpart in
+ * the reference. */
+int dsx_set_tuning_k2_grid(int k2_cu_eighths);
+
 /* The same for K3 (dsx_adamw_multi): blocks per CU (the grid is also capped
  * at the chunk count; 0, the default, picks blocks per CU and slots per
  * thread from the chunk count), slots per thread per trip (1, 2 or 4) and
