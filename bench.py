@@ -44,7 +44,7 @@ def _args():
     ap.add_argument("--torch-gpu", type=int, default=1,
                     help="also time the reference's update as torch ops on this GPU (context line; 0 disables)")
     ap.add_argument("--tuning", default="",
-                    help="k1_bpc,k2_bpc,k2_unroll,nt[,k2_cu_eighths] (library launch-shape override)")
+                    help="k1_bpc,k2_bpc,k2_unroll,nt[,k2_cu_eighths,k2_drain] (library launch-shape override)")
     ap.add_argument("--workload", default="llama8b-shard",
                     choices=["llama8b-shard", "llama-ragged", "llama70b-offload", "gpt2-small", "mlp", "mlp-train"],
                     help="llama8b-shard: the headline flat step (K1/K0/K2); llama-ragged: configs[3]'s 289-tensor "
@@ -595,7 +595,7 @@ def main() -> int:
         vals = [int(x) for x in a.tuning.split(",")]
         _lib.call("dsx_set_tuning", *vals[:4])
         if len(vals) > 4:
-            _lib.call("dsx_set_tuning_k2_grid", vals[4])
+            _lib.call("dsx_set_tuning_k2", vals[4], vals[5] if len(vals) > 5 else 1)
     n = int(a.numel)
     if a.profile_kernels:
         return profile_kernels(n, dev)

@@ -77,7 +77,7 @@ SIGNATURES = {
     "dsx_last_error": (_c.c_char_p, []),
     "dsx_set_tuning_multi": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int]),
     "dsx_set_tuning": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int]),
-    "dsx_set_tuning_k2_grid": (_c.c_int, [_c.c_int]),
+    "dsx_set_tuning_k2": (_c.c_int, [_c.c_int, _c.c_int]),
     "dsx_suggest_partials": (_c.c_int32, [_c.c_int64]),
     "dsx_count_chunks": (_c.c_int64, [_P, _c.c_int32, _c.c_int64]),
     "dsx_build_chunks": (_c.c_int64, [_P, _c.c_int32, _c.c_int64, _P, _c.c_int64]),

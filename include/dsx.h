@@ -160,15 +160,16 @@ const char* dsx_last_error(void);
 
 /* Launch-shape override for the current process (library tuning; no
  * counterpart in the reference): K1 and K2 blocks per CU, K2 slots per
- * thread per trip (2, 4 or 8) and the nontemporal hint (0/1). */
+ * thread per trip (2, 4 or 8; default 4) and the nontemporal hint (0/1). */
 int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll,
                    int nontemporal);
 
-/* K2's grid size: k2_blocks_per_cu blocks on k2_cu_eighths eighths of the
- * CUs (1..8; default 7: on MI355X a block on 7 of every 8 CUs moves K2's
- * 50:50 read/write stream faster than one on every CU). No counterpart in
- * the reference. */
-int dsx_set_tuning_k2_grid(int k2_cu_eighths);
+/* K2's grid and pacing: k2_blocks_per_cu blocks on k2_cu_eighths eighths of
+ * the CUs (1..8; default 7), and whether each wave waits for its stores to
+ * complete before the next trip's loads (drain, default 1). On MI355X both
+ * move K2's 50:50 read/write stream faster: fewer requests in flight keep
+ * DRAM's read/write mix efficient. No counterpart in the reference. */
+int dsx_set_tuning_k2(int k2_cu_eighths, int drain);
 
 /* The same for K3 (dsx_adamw_multi): blocks per CU (the grid is also capped
  * at the chunk count; 0, the default, picks blocks per CU and slots per
