@@ -595,7 +595,7 @@ def main() -> int:
         vals = [int(x) for x in a.tuning.split(",")]
         _lib.call("dsx_set_tuning", *vals[:4])
         if len(vals) > 4:
-            _lib.call("dsx_set_tuning_k2", vals[4], vals[5] if len(vals) > 5 else 1)
+            _lib.call("dsx_set_tuning_k2", vals[4], vals[5] if len(vals) > 5 else -1)
     n = int(a.numel)
     if a.profile_kernels:
         return profile_kernels(n, dev)

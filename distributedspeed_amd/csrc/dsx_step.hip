@@ -68,20 +68,26 @@ bool is_grad_dtype(int dt) { return dt == DSX_F16 || dt == DSX_BF16 || dt == DSX
 
 // ---- launch shape ----------------------------------------------------------
 
-// Defaults from launch-shape sweeps on MI355X over a 1.0e9-element
-// partition. K2's 50:50 read/write stream runs best when the chip issues
-// fewer requests than it could: one 256-thread block on 7 of every 8 CUs
-// (224 blocks on 256 CUs), 4 slots per thread per trip, and each wave waiting
-// for its own stores to complete before it loads the next trip ("drain";
-// 5.50 TB/s against 5.43 without the wait and 5.32 with a block on every CU).
-// K1 (read-only) runs best with two blocks per CU. Nontemporal hints help
-// both by a few percent.
+// Defaults from launch-shape sweeps of the library's kernels on MI355X over
+// partitions of 1.9e6 to 1.0e9 elements. K2 (one 256-thread block per CU
+// unless said otherwise) has two regimes. Up to ~2.5e8 elements, 2 slots per
+// thread per trip with a block on every CU is best. From ~5e8 elements up,
+// K2's 50:50 read/write stream runs best when the chip issues fewer requests
+// than it could: 4 slots per thread, each wave waiting for its own stores to
+// complete before it loads the next trip ("drain"), and blocks on only 7 of
+// every 8 CUs (1.0e9 elements: 5.12 ms against 5.19 on every CU and 5.24 in
+// the small-partition shape; 5e8: 2.51 against 2.55 ms). K1 (read-only) runs
+// best with two blocks per CU. Nontemporal hints help both by a few percent.
+constexpr int64_t kK2LargeN = int64_t(3) << 27;  // K2's large-partition shape from here on
+
 struct Tuning {
   int k1_blocks_per_cu = 2;
   int k2_blocks_per_cu = 1;
-  int k2_cu_eighths = 7;  // K2's grid: k2_blocks_per_cu blocks on this many eighths of the CUs
-  int k2_unroll = 4;      // slots per thread per trip: 2, 4 or 8
-  int k2_drain = 1;       // wait for a trip's stores before the next trip's loads
+  // K2's shape; 0 (-1 for the drain) picks by n: below kK2LargeN 8 eighths,
+  // 2 slots, no drain; from kK2LargeN on 7 eighths, 4 slots, drain.
+  int k2_cu_eighths = 0;  // blocks on this many eighths of the CUs
+  int k2_unroll = 0;      // slots per thread per trip: 2, 4 or 8
+  int k2_drain = -1;      // wait for a trip's stores before the next trip's loads
   int nontemporal = 1;    // nontemporal hint on the streaming loads/stores
   int k3_blocks_per_cu = 0;  // 0: chosen per launch from the chunk count
   int k3_unroll = 1;         // slots per thread per trip in K3: 1, 2 or 4 (when not chosen)
@@ -640,19 +646,22 @@ void launch_k2_u(float* p, float* m, float* v, void* p16, const void* g, int64_t
                  hipStream_t s) {
   const int64_t slots = n >> 2;
   int64_t blocks = ceil_div(slots > 0 ? slots : 1, (int64_t)kBlock * U);
-  int64_t cap = (int64_t)cu_count() * g_tune.k2_blocks_per_cu * g_tune.k2_cu_eighths / 8;
+  const bool large = n >= kK2LargeN;
+  const int eighths = g_tune.k2_cu_eighths ? g_tune.k2_cu_eighths : (large ? 7 : 8);
+  const bool drain = g_tune.k2_drain >= 0 ? g_tune.k2_drain != 0 : large;
+  int64_t cap = (int64_t)cu_count() * g_tune.k2_blocks_per_cu * eighths / 8;
   if (cap < 1) cap = 1;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
   uint16_t* o = static_cast<uint16_t*>(p16);
   const dim3 grid((unsigned)blocks);
   if (g_tune.nontemporal) {
-    if (g_tune.k2_drain)
+    if (drain)
       hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, true, true>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n, sc);
     else
       hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, true, false>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n, sc);
   } else {
-    if (g_tune.k2_drain)
+    if (drain)
       hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, false, true>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n, sc);
     else
       hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, false, false>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n, sc);
@@ -662,7 +671,8 @@ void launch_k2_u(float* p, float* m, float* v, void* p16, const void* g, int64_t
 template <int GD, int PD>
 void launch_k2(float* p, float* m, float* v, void* p16, const void* g, int64_t n, const DsxStepScalars* sc,
                hipStream_t s) {
-  switch (g_tune.k2_unroll) {
+  const int unroll = g_tune.k2_unroll ? g_tune.k2_unroll : (n >= kK2LargeN ? 4 : 2);
+  switch (unroll) {
     case 2: launch_k2_u<GD, PD, 2>(p, m, v, p16, g, n, sc, s); break;
     case 8: launch_k2_u<GD, PD, 8>(p, m, v, p16, g, n, sc, s); break;
     default: launch_k2_u<GD, PD, 4>(p, m, v, p16, g, n, sc, s); break;
@@ -797,7 +807,8 @@ const char* dsx_last_error(void) { return g_err; }
 int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll, int nontemporal) {
   if (k1_blocks_per_cu < 1 || k1_blocks_per_cu > 32 || k2_blocks_per_cu < 1 || k2_blocks_per_cu > 64)
     return fail(DSX_EINVAL, "blocks per CU out of range");
-  if (k2_unroll != 2 && k2_unroll != 4 && k2_unroll != 8) return fail(DSX_EINVAL, "k2_unroll must be 2, 4 or 8");
+  if (k2_unroll != 0 && k2_unroll != 2 && k2_unroll != 4 && k2_unroll != 8)
+    return fail(DSX_EINVAL, "k2_unroll must be 0 (by size), 2, 4 or 8");
   g_tune.k1_blocks_per_cu = k1_blocks_per_cu;
   g_tune.k2_blocks_per_cu = k2_blocks_per_cu;
   g_tune.k2_unroll = k2_unroll;
@@ -806,9 +817,10 @@ int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll, in
 }
 
 int dsx_set_tuning_k2(int k2_cu_eighths, int drain) {
-  if (k2_cu_eighths < 1 || k2_cu_eighths > 8) return fail(DSX_EINVAL, "k2_cu_eighths must be in [1, 8]");
+  if (k2_cu_eighths < 0 || k2_cu_eighths > 8) return fail(DSX_EINVAL, "k2_cu_eighths must be in [0, 8]");
+  if (drain < -1 || drain > 1) return fail(DSX_EINVAL, "drain must be -1 (by size), 0 or 1");
   g_tune.k2_cu_eighths = k2_cu_eighths;
-  g_tune.k2_drain = drain ? 1 : 0;
+  g_tune.k2_drain = drain;
   return DSX_OK;
 }
 

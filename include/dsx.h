@@ -160,15 +160,17 @@ const char* dsx_last_error(void);
 
 /* Launch-shape override for the current process (library tuning; no
  * counterpart in the reference): K1 and K2 blocks per CU, K2 slots per
- * thread per trip (2, 4 or 8; default 4) and the nontemporal hint (0/1). */
+ * thread per trip (2, 4 or 8; 0, the default, picks 2 below 3 * 2^27
+ * elements and 4 from there on) and the nontemporal hint (0/1). */
 int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll,
                    int nontemporal);
 
 /* K2's grid and pacing: k2_blocks_per_cu blocks on k2_cu_eighths eighths of
- * the CUs (1..8; default 7), and whether each wave waits for its stores to
- * complete before the next trip's loads (drain, default 1). On MI355X both
- * move K2's 50:50 read/write stream faster: fewer requests in flight keep
- * DRAM's read/write mix efficient. No counterpart in the reference. */
+ * the CUs (1..8; 0, the default, picks 7 for n >= 3 * 2^27 elements and 8
+ * below), and whether each wave waits for its stores to complete before the
+ * next trip's loads (drain 0/1; -1, the default, drains from 3 * 2^27
+ * elements on). On MI355X a large partition's 50:50 read/write stream runs
+ * faster with fewer requests in flight. No counterpart in the reference. */
 int dsx_set_tuning_k2(int k2_cu_eighths, int drain);
 
 /* The same for K3 (dsx_adamw_multi): blocks per CU (the grid is also capped

@@ -458,3 +458,30 @@ def test_multi_tensor_groups(gpu, oracle):
         assert np.array_equal(tens[i][1].cpu().numpy().view(np.uint32), m.view(np.uint32)), i
         assert np.array_equal(tens[i][2].cpu().numpy().view(np.uint32), v.view(np.uint32)), i
         assert np.array_equal(torch16_to_np(tp16[i]), p16), i
+
+
+def test_k2_launch_shapes_give_identical_bits(gpu, oracle):
+    """Every K2 launch shape the tuning calls can select (slots per thread
+    2/4/8, drain on/off, grids on 1, 7 or 8 eighths of the CUs) computes the
+    same bits as the oracle; the automatic shape is restored afterwards."""
+    from distributedspeed_amd import _lib
+    O = oracle
+    n = 3_000_011
+    p, m, v, g16 = make_state(n, 21, BF16, 1e-3)
+    sc = O.step_scalars(O.Hyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1), 4, 1.0, 0.6)
+    rp, rm, rv, rp16 = p.copy(), m.copy(), v.copy(), np.empty(n, np.uint16)
+    O.adamw(rp, rm, rv, rp16, BF16, g16, BF16, sc)
+    try:
+        for unroll in (2, 4, 8):
+            for drain in (0, 1):
+                for eighths in (1, 7, 8):
+                    assert _lib.call("dsx_set_tuning", 2, 1, unroll, 1) == 0
+                    assert _lib.call("dsx_set_tuning_k2", eighths, drain) == 0
+                    _say(f"k2 shape unroll={unroll} drain={drain} eighths={eighths}")
+                    gp, gm, gv, gp16 = _run_k2(gpu, p, m, v, g16, BF16, BF16, sc)
+                    for name, a, b in (("master", gp, rp), ("exp_avg", gm, rm), ("exp_avg_sq", gv, rv)):
+                        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (name, unroll, drain, eighths)
+                    assert np.array_equal(gp16, rp16), (unroll, drain, eighths)
+    finally:
+        _lib.call("dsx_set_tuning", 2, 1, 0, 1)
+        _lib.call("dsx_set_tuning_k2", 0, -1)
