@@ -45,6 +45,8 @@ def _args():
                     help="also time the reference's update as torch ops on this GPU (context line; 0 disables)")
     ap.add_argument("--tuning", default="",
                     help="k1_bpc,k2_bpc,k2_unroll,nt[,k2_cu_eighths,k2_drain] (library launch-shape override)")
+    ap.add_argument("--tuning-multi", default="",
+                    help="k3_bpc,k3_unroll,nt,drain (K3 launch-shape override; k3_bpc 0 picks by chunk count)")
     ap.add_argument("--workload", default="llama8b-shard",
                     choices=["llama8b-shard", "llama-ragged", "llama70b-offload", "gpt2-small", "mlp", "mlp-train"],
                     help="llama8b-shard: the headline flat step (K1/K0/K2); llama-ragged: configs[3]'s 289-tensor "
@@ -596,6 +598,8 @@ def main() -> int:
         _lib.call("dsx_set_tuning", *vals[:4])
         if len(vals) > 4:
             _lib.call("dsx_set_tuning_k2", vals[4], vals[5] if len(vals) > 5 else -1)
+    if a.tuning_multi:
+        _lib.call("dsx_set_tuning_multi", *[int(x) for x in a.tuning_multi.split(",")])
     n = int(a.numel)
     if a.profile_kernels:
         return profile_kernels(n, dev)

@@ -75,7 +75,7 @@ for _s, _n in ((DsxState, 64), (DsxScalerConfig, 32), (DsxAdamwHyper, 56), (DsxS
 SIGNATURES = {
     "dsx_abi_version": (_c.c_int, []),
     "dsx_last_error": (_c.c_char_p, []),
-    "dsx_set_tuning_multi": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int]),
+    "dsx_set_tuning_multi": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int]),
     "dsx_set_tuning": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int]),
     "dsx_set_tuning_k2": (_c.c_int, [_c.c_int, _c.c_int]),
     "dsx_suggest_partials": (_c.c_int32, [_c.c_int64]),

@@ -174,10 +174,14 @@ int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll,
 int dsx_set_tuning_k2(int k2_cu_eighths, int drain);
 
 /* The same for K3 (dsx_adamw_multi): blocks per CU (the grid is also capped
- * at the chunk count; 0, the default, picks blocks per CU and slots per
- * thread from the chunk count), slots per thread per trip (1, 2 or 4) and
- * the nontemporal hint. No counterpart in the reference. */
-int dsx_set_tuning_multi(int k3_blocks_per_cu, int k3_unroll, int nontemporal);
+ * at the chunk count; 0, the default, picks the shape from the chunk count:
+ * one block per CU with 2 slots below 256 chunks per CU, about six chunks
+ * per block with 2 slots and the drain from there on), slots per thread per
+ * trip (1, 2 or 4; used when blocks per CU is set), the nontemporal hint and
+ * K2's per-trip drain (0/1; -1, the default, as the shape decides). No
+ * counterpart in the reference. */
+int dsx_set_tuning_multi(int k3_blocks_per_cu, int k3_unroll, int nontemporal,
+                         int drain);
 
 /* Partials a K1 launch over n elements should use on the current device
  * (a multiple of the CU count, <= DSX_MAX_PARTIALS). */

@@ -123,8 +123,9 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.dsx_set_tuning(0, 8, 4, 1) == EINVAL
     assert lib.dsx_set_tuning_k2(-1, 1) == EINVAL and lib.dsx_set_tuning_k2(9, 0) == EINVAL
     assert lib.dsx_set_tuning_k2(0, 2) == EINVAL and lib.dsx_set_tuning_k2(0, -2) == EINVAL
-    assert lib.dsx_set_tuning_multi(8, 3, 0) == EINVAL
-    assert lib.dsx_set_tuning_multi(-1, 1, 0) == EINVAL
+    assert lib.dsx_set_tuning_multi(8, 3, 0, 0) == EINVAL
+    assert lib.dsx_set_tuning_multi(-1, 1, 0, 0) == EINVAL
+    assert lib.dsx_set_tuning_multi(0, 1, 1, 2) == EINVAL
 
 
 def test_python_layer_mirrors_torch_errors():

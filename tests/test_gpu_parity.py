@@ -485,3 +485,47 @@ def test_k2_launch_shapes_give_identical_bits(gpu, oracle):
     finally:
         _lib.call("dsx_set_tuning", 2, 1, 0, 1)
         _lib.call("dsx_set_tuning_k2", 0, -1)
+
+
+def test_k3_launch_shapes_give_identical_bits(gpu, oracle):
+    """Every K3 shape the tuning can select (one block per CU up to many
+    blocks per CU, 1/2/4 slots, drain on/off, and the automatic choice) is
+    bit-identical to K2 over the same elements of a ragged list that has
+    aligned and unaligned tensors; the automatic shape is restored afterwards."""
+    import torch
+    from distributedspeed_amd import _lib, ops
+    O = oracle
+    sizes = [65536 * 3 + 8, 3, 4096 * 5, 17, 65536 + 1, 4096 * 2]
+    offs, pos = [], 0
+    for i, s in enumerate(sizes):
+        pos += (i % 2)
+        offs.append(pos)
+        pos += s
+    total = pos
+    p, m, v, g16 = make_state(total, 12, BF16, 1e-3)
+    sc = O.step_scalars(O.Hyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1), 2, 1.0, 0.8)
+    gp, gm, gv, gp16 = _run_k2(gpu, p, m, v, g16, BF16, BF16, sc)
+    hs = _lib.DsxStepScalars()
+    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1c", "b2", "val2", "eps", "bc2s", "nss"):
+        setattr(hs, k, getattr(sc, k))
+    covered = np.zeros(total, bool)
+    for o, s in zip(offs, sizes):
+        covered[o:o + s] = True
+    try:
+        for shape in ((0, 1, 1, -1), (1, 1, 1, 0), (1, 2, 1, 1), (1, 4, 1, 0), (8, 1, 1, 1), (64, 2, 1, 1),
+                      (64, 4, 0, 1), (512, 2, 1, 0)):
+            _lib.call("dsx_set_tuning_multi", *shape)
+            _say(f"k3 shape {shape}")
+            tp, tm, tv = (f32_to_torch(a, gpu) for a in (p, m, v))
+            tg = np16_to_torch(g16, BF16, gpu)
+            tp16 = torch.zeros(total, dtype=torch.bfloat16, device=gpu)
+            views = lambda t: [t[o:o + s] for o, s in zip(offs, sizes)]  # noqa: E731
+            table = ops.ChunkTable(views(tp), views(tm), views(tv), views(tp16), views(tg), chunk_elems=4096)
+            ops.adamw_multi(table, ops.scalars_from_host(hs, gpu))
+            torch.cuda.synchronize()
+            for name, a, b in (("master", tp.cpu().numpy(), gp), ("exp_avg", tm.cpu().numpy(), gm),
+                               ("exp_avg_sq", tv.cpu().numpy(), gv)):
+                assert np.array_equal(a[covered].view(np.uint32), b[covered].view(np.uint32)), (name, shape)
+            assert np.array_equal(torch16_to_np(tp16)[covered], gp16[covered]), shape
+    finally:
+        _lib.call("dsx_set_tuning_multi", 0, 1, 1, -1)
