@@ -1042,7 +1042,7 @@ int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t
   // default shape, from sweeps on MI355X over Llama-layout lists of 1.2e8 to
   // 8.3e9 elements (65536-element chunks): up to 256 chunks per CU, one block
   // per CU taking two slots per trip walks the list as one front (like K2's
-  // grid-stride); from 256 chunks per CU on, a grid of about six chunks per
+  // grid-stride); from 256 chunks per CU on, a grid of about four chunks per
   // block, far more blocks than the CUs hold at once, with two slots and K2's
   // drain, is 4-5% faster (the blocks start as others finish).
   const int64_t cus = cu_count();
@@ -1052,7 +1052,7 @@ int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t
   if (bpc == 0) {
     const int64_t per_cu = nchunks / cus;
     const bool many = per_cu >= 256;
-    bpc = many ? per_cu / 6 : 1;
+    bpc = many ? per_cu / 4 : 1;
     unroll = 2;
     drain = g_tune.k3_drain >= 0 ? g_tune.k3_drain > 0 : many;
   }
