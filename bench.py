@@ -48,12 +48,14 @@ def _args():
     ap.add_argument("--tuning-multi", default="",
                     help="k3_bpc,k3_unroll,nt,drain (K3 launch-shape override; k3_bpc 0 picks by chunk count)")
     ap.add_argument("--workload", default="llama8b-shard",
-                    choices=["llama8b-shard", "llama-ragged", "llama70b-offload", "gpt2-small", "mlp", "mlp-train"],
+                    choices=["llama8b-shard", "llama-ragged", "llama70b-offload", "gpt2-small", "mlp", "mlp-train",
+                             "ffn-train"],
                     help="llama8b-shard: the headline flat step (K1/K0/K2); llama-ragged: configs[3]'s 289-tensor "
                          "list through K3; llama70b-offload: configs[4] with state in pinned host memory; "
                          "gpt2-small / mlp: configs[1] / configs[0] through the drop-in optimizer classes, eager, "
                          "graph-replayed and ragged; mlp-train: a whole training iteration of configs[0]'s "
-                         "model, eager and captured in one graph (secondary lines, not the headline)")
+                         "model, eager and captured in one graph; ffn-train: a 0.94e9-parameter training "
+                         "iteration with the two ways grads reach the flat buffer (secondary lines, not the headline)")
     ap.add_argument("--pinned-budget-gib", type=float, default=32.0,
                     help="llama70b-offload: pinned host memory for the fp32 state (the shard shrinks to fit)")
     ap.add_argument("--profile-kernels", action="store_true",
@@ -282,6 +284,74 @@ def bench_mlp_train(a, dev) -> int:
                    "storage": "fp16 params/grads, f32 state"},
         "modes": res, "speedup_graph_over_eager": round(res["eager_us_per_iter"] / res["graph_us_per_iter"], 3)}),
         flush=True)
+    return 0
+
+
+def bench_ffn_train(a, dev) -> int:
+    """The grad-producer side of the step: a 0.94e9-parameter stack of bf16
+    feed-forward blocks (8 x [4096 -> 14336, ReLU, 14336 -> 4096], no bias)
+    trained on 16 synthetic tokens, so weight traffic sets the pace. One
+    iteration = zero_grad, forward, loss, backward, fused step (clip 1.0).
+    Two ways of getting the grads into the flat buffer, alternated in blocks
+    of a.steps iterations on the same model: zero_grad(set_to_none=True)
+    (autograd's grads copied into the flat views by the post-accumulate hook,
+    4 B/elt) and zero_grad(set_to_none=False) (the flat buffer zeroed, then
+    autograd accumulates into it, 8 B/elt)."""
+    import torch
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    torch.manual_seed(0)
+    d, ff, blocks, tokens = 4096, 14336, 8, 16
+    layers = []
+    for _ in range(blocks):
+        layers += [torch.nn.Linear(d, ff, bias=False), torch.nn.ReLU(), torch.nn.Linear(ff, d, bias=False)]
+    model = torch.nn.Sequential(*layers).to(dev, torch.bfloat16)
+    for mod in model:
+        if isinstance(mod, torch.nn.Linear):
+            torch.nn.init.normal_(mod.weight, 0.0, 0.02)
+    n_params = sum(p.numel() for p in model.parameters())
+    opt = AdamWOptimizer(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, max_grad_norm=1.0,
+                         param_dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    x = torch.randn(tokens, d, device=dev, generator=gen).to(torch.bfloat16)
+
+    def iteration(set_to_none):
+        opt.zero_grad(set_to_none=set_to_none)
+        loss = model(x).float().pow(2).mean()
+        loss.backward()
+        opt.step()
+
+    for mode in (True, False):
+        for _ in range(max(1, a.warmup)):
+            iteration(mode)
+    torch.cuda.synchronize()
+    times = {True: [], False: []}
+    for _ in range(3):
+        for mode in (True, False):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(a.steps):
+                iteration(mode)
+            e1.record()
+            torch.cuda.synchronize()
+            times[mode].append(e0.elapsed_time(e1) / a.steps)
+    st = opt.read_state()
+    if st.error or st.last_skip:
+        print(json.dumps({"error": f"state error={st.error} skip={st.last_skip}"}))
+        return 1
+    handed, zeroed = (sorted(times[m])[1] for m in (True, False))
+    print(json.dumps({
+        "metric": "training iteration ms, 0.94e9-parameter bf16 feed-forward stack, 16 tokens",
+        "value": round(handed, 4), "unit": "ms/iter", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "higher_is_better": False, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "ffn stack training iteration (grad-producer side of the step)", "params": n_params,
+                   "blocks": blocks, "d_model": d, "d_ff": ff, "tokens": tokens,
+                   "storage": "bf16 params/grads, f32 state"},
+        "ms_per_iter": {"zero_grad_set_to_none_hook": round(handed, 4), "zero_grad_in_place": round(zeroed, 4)},
+        "runs_ms": {"set_to_none": [round(t, 4) for t in times[True]], "in_place": [round(t, 4) for t in times[False]]},
+        "saving_ms": round(zeroed - handed, 4),
+        "saving_ms_if_4b_per_param_at_8tbs": round(4 * n_params / 8e12 * 1e3, 4),
+    }), flush=True)
     return 0
 
 
@@ -611,6 +681,8 @@ def main() -> int:
         return bench_dropin(a, dev)
     if a.workload == "mlp-train":
         return bench_mlp_train(a, dev)
+    if a.workload == "ffn-train":
+        return bench_ffn_train(a, dev)
     hyper = AdamWHyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     _progress(f"generating {n} elements")
     master, exp_avg, exp_avg_sq, p16, grad = make_inputs(n, 2, dev)

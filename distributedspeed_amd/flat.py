@@ -17,6 +17,20 @@ grads are fp32. With `offload=True` master / exp_avg / exp_avg_sq are pinned
 host tensors instead (the step streams them through HBM; param16 and grad
 stay in HBM), which needs a 16-bit param dtype.
 
+Grads reach the flat buffer one of two ways. After zero_grad(set_to_none=
+False) the views stay bound and autograd accumulates into them: a zeroing
+pass (2 B/elt written) and then, per micro-batch, the view read, the new
+grad read and the sum written (6 B/elt). After zero_grad(set_to_none=True),
+the default, p.grad is None, so autograd hands over the grad it produced
+and a post-accumulate-grad hook copies it into the view (2 B read, 2 B
+written) and rebinds p.grad to the view, which later micro-batches then
+accumulate into: 4 B/elt instead of 8 for the first micro-batch, and the
+copies run during backward. A parameter that received no grad is zeroed in
+its view before the step (check_grads_bound) and takes an AdamW step with a
+zero grad, as torch does after zero_grad(set_to_none=False). Code that
+writes grads straight into the flat buffer keeps the views bound with
+zero_grad(set_to_none=False).
+
 Parameters are laid out group by group in model order; every
 parameter (and so every group) starts on an 8-element boundary, so each
 group's range is 16-byte aligned in every buffer. Padding elements have zero
@@ -24,6 +38,7 @@ grad and zero master and stay zero under AdamW.
 """
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 
 import torch
@@ -33,6 +48,23 @@ ALIGN = 8
 
 def _round_up(x: int, a: int) -> int:
     return (x + a - 1) // a * a
+
+
+def _bind_hook(ref, i: int):
+    """Post-accumulate-grad hook of parameter i: a grad autograd produced
+    outside the flat buffer (p.grad was None) is copied into the parameter's
+    view and p.grad becomes the view again."""
+    def hook(p):
+        part = ref()
+        if part is None:
+            return
+        view = part._grad_views[i]
+        g = p.grad
+        if g is not view:
+            if g is not None and g.data_ptr() != view.data_ptr():
+                view.copy_(g)
+            p.grad = view
+    return hook
 
 
 @dataclass
@@ -95,6 +127,16 @@ class FlatPartition:
             if self.param16 is not None and not self.offload:
                 self.param16.copy_(self.master)  # round to nearest even
         self.rebind()
+        # The hooks reach the partition through a weak reference, so a
+        # parameter that outlives its optimizer does not keep the flat
+        # buffers alive; they are removed when the partition goes.
+        ref = weakref.ref(self)
+        self._hooks = [p.register_post_accumulate_grad_hook(_bind_hook(ref, i))
+                       for i, p in enumerate(self.params) if p.requires_grad]
+
+    def __del__(self):
+        for h in getattr(self, "_hooks", ()):
+            h.remove()
 
     def rebind(self) -> None:
         """Point every param.data / param.grad at its view of the flat buffers."""
@@ -132,8 +174,17 @@ class FlatPartition:
         return {"master": self.master[sl].view(s.shape), "exp_avg": self.exp_avg[sl].view(s.shape),
                 "exp_avg_sq": self.exp_avg_sq[sl].view(s.shape)}
 
-    def zero_grad(self) -> None:
-        self.grad.zero_()
+    def zero_grad(self, set_to_none: bool = False) -> None:
+        """set_to_none: p.grad = None, so the next backward hands its grads
+        over (copied into the views by the hook); otherwise the flat grad
+        buffer is zeroed in place and the views stay bound."""
+        if set_to_none:
+            for p in self.params:
+                p.grad = None
+        else:
+            self.grad.zero_()
+            for p, view in zip(self.params, self._grad_views):
+                p.grad = view
 
     def refresh_params16(self) -> None:
         """param16 <- master (RNE), after the master was loaded."""

@@ -104,9 +104,9 @@ class RaggedParams:
             self._key = key
         return self._table
 
-    def zero_grad(self) -> None:
+    def zero_grad(self, set_to_none: bool = False) -> None:
         """Zero the grads in place (their addresses, and so the chunk table,
-        stay valid)."""
+        stay valid); set_to_none is not honoured here."""
         gs = [p.grad for p in self.params if p.grad is not None]
         if gs:
             torch._foreach_zero_(gs)

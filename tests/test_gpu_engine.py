@@ -196,7 +196,11 @@ def test_gradient_accumulation(gpu, oracle):
     g = torch16_to_np(base.flat.grad).copy()
     engine.step()
     assert engine.global_steps == 1
-    assert float(base.flat.grad.float().abs().sum()) == 0.0  # zeroed after the boundary step
+    # after the boundary step the grads are None (zero_grad(set_to_none=True));
+    # before anything reads the flat buffer, views without a grad are zeroed
+    assert all(p.grad is None for p in base.flat.params)
+    base.flat.check_grads_bound()
+    assert float(base.flat.grad.float().abs().sum()) == 0.0
     p, m, v = p_before.cpu().numpy(), np.zeros(base.flat.numel, np.float32), np.zeros(base.flat.numel, np.float32)
     h = oracle.Hyper(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01)
     oracle.adamw(p, m, v, None, BF16, g, BF16, oracle.step_scalars(h, 1, 1.0, 1.0))
@@ -404,3 +408,43 @@ def test_zero_optimizer_counters_and_accessors(gpu):
     assert opt.current_step == 10 and opt.overflow_count == 3
     opt.current_step = 7
     assert opt.current_step == 7 and opt.base_optimizer.read_state().t == 4
+
+
+def test_grad_hand_over_matches_in_place_zeroing(gpu):
+    """zero_grad(set_to_none=True) (autograd's grads copied into the flat
+    buffer by the post-accumulate hook) and zero_grad(set_to_none=False)
+    (flat buffer zeroed, autograd accumulates into it) train bit-identically:
+    fp16 with a dynamic loss scale, two micro-batches per step, one parameter
+    that never receives a grad."""
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    _say("grad hand-over vs in-place zeroing")
+
+    def build():
+        torch.manual_seed(11)
+        model = torch.nn.Sequential(torch.nn.Linear(64, 96), torch.nn.GELU(), torch.nn.Linear(96, 8)).to(gpu)
+        spare = torch.nn.Parameter(torch.randn(37, device=gpu) * 0.1)  # never used in forward
+        opt = AdamWOptimizer(list(model.parameters()) + [spare], lr=1e-3, weight_decay=0.05, max_grad_norm=1.0,
+                             param_dtype=torch.float16, device=gpu,
+                             loss_scaler=ScalerConfig(mode="dynamic", init_scale=2.0 ** 12, window=1000,
+                                                      hysteresis=1))
+        return model, opt
+
+    runs = []
+    for set_to_none in (True, False):
+        model, opt = build()
+        gen = torch.Generator(device=gpu).manual_seed(3)
+        for _ in range(4):
+            opt.zero_grad(set_to_none=set_to_none)
+            for _ in range(2):
+                x = torch.randn(16, 64, device=gpu, generator=gen).half()
+                loss = model(x).float().pow(2).mean() / 2
+                (loss * opt.loss_scale_tensor()).backward()
+            opt.step()
+        torch.cuda.synchronize()
+        assert opt.read_state().t == 4
+        runs.append({k: getattr(opt.flat, k).clone() for k in ("master", "exp_avg", "exp_avg_sq", "param16")})
+    for k in runs[0]:
+        assert torch.equal(runs[0][k].view(torch.int16 if k == "param16" else torch.int32),
+                           runs[1][k].view(torch.int16 if k == "param16" else torch.int32)), k

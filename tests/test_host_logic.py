@@ -138,6 +138,45 @@ def test_autograd_accumulates_into_flat_views_on_cpu():
     assert float(fp.grad.abs().sum()) == 0.0
 
 
+def test_grads_handed_over_after_set_to_none():
+    """zero_grad(set_to_none=True): autograd's own grads are copied into the
+    flat views by the post-accumulate hook and p.grad is the view again, so a
+    second micro-batch accumulates in the flat buffer; a parameter without a
+    grad is zeroed in its view before the step; set_to_none=False zeroes the
+    buffer in place and keeps the views bound. Values equal plain autograd."""
+    import gc
+    torch.manual_seed(0)
+    lin, unused = torch.nn.Linear(6, 3), torch.nn.Parameter(torch.ones(5))
+    ref = torch.nn.Linear(6, 3)
+    ref.load_state_dict(lin.state_dict())
+    fp = FlatPartition([list(lin.parameters()) + [unused]], torch.device("cpu"), None)
+    views = [fp.grad[s.offset:s.offset + s.numel] for s in fp.slots]
+    fp.grad.fill_(7.0)  # stale values from an earlier step
+    fp.zero_grad(set_to_none=True)
+    assert all(p.grad is None for p in fp.params)
+    xs = [torch.randn(4, 6) for _ in range(2)]
+    for x in xs:
+        lin(x).pow(2).sum().backward()
+        ref(x).pow(2).sum().backward()
+    for p, v in zip(list(lin.parameters()), views):
+        assert p.grad.data_ptr() == v.data_ptr()
+    assert torch.equal(lin.weight.grad, ref.weight.grad) and torch.equal(lin.bias.grad, ref.bias.grad)
+    assert unused.grad is None
+    fp.check_grads_bound()
+    assert unused.grad.data_ptr() == views[2].data_ptr() and float(unused.grad.abs().sum()) == 0.0
+    fp.zero_grad(set_to_none=False)
+    assert float(fp.grad.abs().sum()) == 0.0
+    assert all(p.grad.data_ptr() == v.data_ptr() for p, v in zip(fp.params, views))
+    lin(xs[0]).sum().backward()
+    assert torch.equal(lin.bias.grad, torch.full((3,), 4.0))
+    # the partition can go while the parameters live on: its hooks go with it
+    del fp
+    gc.collect()
+    lin.weight.grad = None
+    lin(xs[0]).sum().backward()
+    assert lin.weight.grad is not None and lin.weight.grad.data_ptr() != views[0].data_ptr()
+
+
 def test_flat_rejects_duplicates_and_bad_dtype():
     p = torch.nn.Parameter(torch.zeros(3))
     with pytest.raises(ValueError):
