@@ -292,65 +292,75 @@ def bench_ffn_train(a, dev) -> int:
     feed-forward blocks (8 x [4096 -> 14336, ReLU, 14336 -> 4096], no bias)
     trained on 16 synthetic tokens, so weight traffic sets the pace. One
     iteration = zero_grad, forward, loss, backward, fused step (clip 1.0).
-    Two ways of getting the grads into the flat buffer, alternated in blocks
-    of a.steps iterations on the same model: zero_grad(set_to_none=True)
-    (autograd's grads copied into the flat views by the post-accumulate hook,
-    4 B/elt) and zero_grad(set_to_none=False) (the flat buffer zeroed, then
-    autograd accumulates into it, 8 B/elt)."""
+    Both storage forms, each with both ways of handling the grads, alternated
+    in blocks of a.steps iterations: zero_grad(set_to_none=True) -- the flat
+    form copies autograd's grads into its buffer in a post-accumulate hook
+    (4 B/elt), the ragged form reads them where autograd put them (0 B/elt)
+    -- and zero_grad(set_to_none=False) -- grads zeroed in place, then
+    autograd accumulates into them (8 B/elt)."""
     import torch
-    from distributedspeed_amd.optimizers import AdamWOptimizer
-    torch.manual_seed(0)
+    from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
     d, ff, blocks, tokens = 4096, 14336, 8, 16
-    layers = []
-    for _ in range(blocks):
-        layers += [torch.nn.Linear(d, ff, bias=False), torch.nn.ReLU(), torch.nn.Linear(ff, d, bias=False)]
-    model = torch.nn.Sequential(*layers).to(dev, torch.bfloat16)
-    for mod in model:
-        if isinstance(mod, torch.nn.Linear):
-            torch.nn.init.normal_(mod.weight, 0.0, 0.02)
-    n_params = sum(p.numel() for p in model.parameters())
-    opt = AdamWOptimizer(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, max_grad_norm=1.0,
-                         param_dtype=torch.bfloat16, device=dev)
+
+    def make(cls):
+        torch.manual_seed(0)
+        layers = []
+        for _ in range(blocks):
+            layers += [torch.nn.Linear(d, ff, bias=False), torch.nn.ReLU(), torch.nn.Linear(ff, d, bias=False)]
+        model = torch.nn.Sequential(*layers).to(dev, torch.bfloat16)
+        for mod in model:
+            if isinstance(mod, torch.nn.Linear):
+                torch.nn.init.normal_(mod.weight, 0.0, 0.02)
+        opt = cls(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, max_grad_norm=1.0,
+                  param_dtype=torch.bfloat16, device=dev)
+        return model, opt
+
+    forms = {"flat": make(AdamWOptimizer), "ragged": make(MultiTensorAdamWOptimizer)}
+    n_params = sum(p.numel() for p in forms["flat"][0].parameters())
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
     x = torch.randn(tokens, d, device=dev, generator=gen).to(torch.bfloat16)
 
-    def iteration(set_to_none):
+    def iteration(form, set_to_none):
+        model, opt = forms[form]
         opt.zero_grad(set_to_none=set_to_none)
-        loss = model(x).float().pow(2).mean()
-        loss.backward()
+        model(x).float().pow(2).mean().backward()
         opt.step()
 
-    for mode in (True, False):
+    modes = [(f, m) for f in ("flat", "ragged") for m in (True, False)]
+    for mode in modes:
         for _ in range(max(1, a.warmup)):
-            iteration(mode)
+            iteration(*mode)
     torch.cuda.synchronize()
-    times = {True: [], False: []}
+    times = {mode: [] for mode in modes}
     for _ in range(3):
-        for mode in (True, False):
+        for mode in modes:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             for _ in range(a.steps):
-                iteration(mode)
+                iteration(*mode)
             e1.record()
             torch.cuda.synchronize()
             times[mode].append(e0.elapsed_time(e1) / a.steps)
-    st = opt.read_state()
-    if st.error or st.last_skip:
-        print(json.dumps({"error": f"state error={st.error} skip={st.last_skip}"}))
-        return 1
-    handed, zeroed = (sorted(times[m])[1] for m in (True, False))
+    for _, opt in forms.values():
+        st = opt.read_state()
+        if st.error or st.last_skip:
+            print(json.dumps({"error": f"state error={st.error} skip={st.last_skip}"}))
+            return 1
+    med = {mode: sorted(v)[1] for mode, v in times.items()}
+    name = {True: "set_to_none", False: "in_place"}
     print(json.dumps({
         "metric": "training iteration ms, 0.94e9-parameter bf16 feed-forward stack, 16 tokens",
-        "value": round(handed, 4), "unit": "ms/iter", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "higher_is_better": False, "dtype": "f32", "data": "synthetic",
+        "value": round(med[("flat", True)], 4), "unit": "ms/iter", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "higher_is_better": False, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "ffn stack training iteration (grad-producer side of the step)", "params": n_params,
                    "blocks": blocks, "d_model": d, "d_ff": ff, "tokens": tokens,
                    "storage": "bf16 params/grads, f32 state"},
-        "ms_per_iter": {"zero_grad_set_to_none_hook": round(handed, 4), "zero_grad_in_place": round(zeroed, 4)},
-        "runs_ms": {"set_to_none": [round(t, 4) for t in times[True]], "in_place": [round(t, 4) for t in times[False]]},
-        "saving_ms": round(zeroed - handed, 4),
-        "saving_ms_if_4b_per_param_at_8tbs": round(4 * n_params / 8e12 * 1e3, 4),
+        "ms_per_iter": {f"{f}_{name[m]}": round(t, 4) for (f, m), t in med.items()},
+        "runs_ms": {f"{f}_{name[m]}": [round(t, 4) for t in v] for (f, m), v in times.items()},
+        "saving_ms": {f: round(med[(f, False)] - med[(f, True)], 4) for f in ("flat", "ragged")},
+        "saving_ms_at_8tbs": {"flat (4 B/param)": round(4 * n_params / 8e12 * 1e3, 4),
+                              "ragged (8 B/param)": round(8 * n_params / 8e12 * 1e3, 4)},
     }), flush=True)
     return 0
 

@@ -383,8 +383,26 @@ class ChunkTable:
             raise RuntimeError(_lib.last_error())
         self.nchunks = int(cnt)
         self.numel = int(sum(numels))
+        self._refs = refs
+        self._gdtype = grads[0].dtype
         self.tensors = torch.frombuffer(bytearray(bytes(refs)), dtype=torch.uint8).to(dev)
         self.chunks = torch.frombuffer(bytearray(bytes(chunks)), dtype=torch.uint8).to(dev)
+
+    def update_grads(self, grads) -> None:
+        """Point the tensor table at new grad tensors (same count, numels and
+        dtype) in place: the chunk table and every launch bound to this table
+        stay valid. The new table is copied from pinned memory on the current
+        stream, so launches already queued read the old one and later ones the
+        new one."""
+        refs = self._refs
+        if len(grads) != len(refs):
+            raise ValueError(f"expected {len(refs)} grads, got {len(grads)}")
+        esz = torch.empty(0, dtype=self._gdtype).element_size()
+        for i, g in enumerate(grads):
+            _need(g, f"grad[{i}]", self._gdtype, refs[i].numel, self.device, esz)
+            refs[i].grad = g.data_ptr()
+        host = torch.frombuffer(bytearray(bytes(refs)), dtype=torch.uint8).pin_memory()
+        self.tensors.copy_(host, non_blocking=True)
 
 
 def plan_unscale_norm_multi(table: ChunkTable, state: torch.Tensor, partials: torch.Tensor, nparts: int) -> Launch:

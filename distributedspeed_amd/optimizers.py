@@ -150,17 +150,18 @@ class _FusedAdamWBase(torch.optim.Optimizer):
             self.state[p] = st
 
     def zero_grad(self, set_to_none: bool = True) -> None:
-        """set_to_none (torch's default): in the flat form p.grad becomes
-        None and the next backward's grads are copied into the flat buffer by
+        """set_to_none (torch's default): p.grad becomes None. In the flat
+        form the next backward's grads are then copied into the flat buffer by
         a post-accumulate-grad hook (4 B/elt instead of zeroing plus
-        accumulating, 8 B/elt). The grads are zeroed in place instead for
+        accumulating, 8 B/elt); in the ragged form they are read where
+        autograd puts them (the tensor table's grad pointers are refreshed at
+        the next step). The grads are zeroed in place instead for
         capturable=True (a captured iteration must not depend on Python-side
-        state) and in the ragged form (its chunk table holds the grads'
-        addresses)."""
+        state)."""
         self.store.zero_grad(set_to_none=set_to_none and self._grads_may_move())
 
     def _grads_may_move(self) -> bool:
-        return False
+        return True
 
     def add_param_group(self, param_group: dict) -> None:
         if getattr(self, "store", None) is not None:

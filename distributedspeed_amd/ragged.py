@@ -88,10 +88,16 @@ class RaggedParams:
                 p.grad = g.to(self.device, self.grad_dtype).contiguous()
 
     def table(self) -> ops.ChunkTable:
-        """The device chunk table for the current storage (rebuilt only when
-        a param's or a grad's address changed)."""
+        """The device chunk table for the current storage: rebuilt when a
+        param's address changed; when only grads moved (autograd's own grads
+        after zero_grad(set_to_none=True)), only the tensor table's grad
+        pointers are refreshed, in place."""
         self.ensure_grads()
         key = tuple((p.data_ptr(), p.grad.data_ptr()) for p in self.params)
+        if (self._table is not None and key != self._key
+                and all(a[0] == b[0] for a, b in zip(key, self._key))):
+            self._table.update_grads([p.grad for p in self.params])
+            self._key = key
         if key != self._key:
             for p, m in zip(self.params, self.master):
                 if p.data.shape != m.shape or (self.param_dtype is None and p.data.data_ptr() != m.data_ptr()):
@@ -105,8 +111,14 @@ class RaggedParams:
         return self._table
 
     def zero_grad(self, set_to_none: bool = False) -> None:
-        """Zero the grads in place (their addresses, and so the chunk table,
-        stay valid); set_to_none is not honoured here."""
+        """set_to_none: p.grad = None, so the next backward's grads are read
+        where autograd puts them (the tensor table's grad pointers are
+        refreshed at the next step; nothing is copied or zeroed); otherwise
+        the grads are zeroed in place and their addresses stay."""
+        if set_to_none:
+            for p in self.params:
+                p.grad = None
+            return
         gs = [p.grad for p in self.params if p.grad is not None]
         if gs:
             torch._foreach_zero_(gs)

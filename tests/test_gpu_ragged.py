@@ -129,3 +129,37 @@ def test_engine_non_contiguous_gradients_matches_contiguous(gpu):
     assert isinstance(opts[1], MultiTensorAdamWOptimizer) and not isinstance(opts[0], MultiTensorAdamWOptimizer)
     _check(opts[0], opts[1], "engine")
     assert opts[1].read_state().t == 5
+
+
+def test_ragged_reads_autograd_grads_in_place_after_set_to_none(gpu):
+    """zero_grad(set_to_none=True) in the ragged form: the next step reads the
+    grads autograd allocated, refreshing only the tensor table's grad
+    pointers (the chunk table object and its bound launches are kept), and
+    trains bit-identically to the flat form; a parameter with no grad gets a
+    zero grad as in the flat form."""
+    import torch
+    from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
+    _say("ragged set_to_none")
+    opts, tables = [], []
+    for cls in (AdamWOptimizer, MultiTensorAdamWOptimizer):
+        torch.manual_seed(7)
+        model = torch.nn.Sequential(torch.nn.Linear(48, 80), torch.nn.GELU(), torch.nn.Linear(80, 8)).to(gpu)
+        spare = torch.nn.Parameter(torch.randn(19, device=gpu) * 0.1)
+        opt = cls(list(model.parameters()) + [spare], lr=1e-3, weight_decay=0.05, max_grad_norm=1.0,
+                  param_dtype=torch.bfloat16, device=gpu)
+        gen = torch.Generator(device=gpu).manual_seed(2)
+        seen = []
+        for _ in range(4):
+            opt.zero_grad(set_to_none=True)
+            assert all(p.grad is None for p in opt.dsx_params)
+            x = torch.randn(12, 48, device=gpu, generator=gen).to(torch.bfloat16)
+            model(x).float().pow(2).mean().backward()
+            opt.step()
+            if cls is MultiTensorAdamWOptimizer:
+                seen.append(opt.store.table())
+        torch.cuda.synchronize()
+        opts.append(opt)
+        tables.append(seen)
+    assert all(t is tables[1][0] for t in tables[1])  # one chunk table throughout
+    _check(opts[0], opts[1], "set_to_none")
+    assert opts[1].read_state().t == 4
