@@ -310,6 +310,68 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm(const void* __restrict
   if (threadIdx.x == 0) partials[blockIdx.x] = s;
 }
 
+// ---- K1 folded into a grad copy ---------------------------------------------------
+// The flat form's post-accumulate hook copies the grad autograd produced into
+// the flat buffer. This kernel makes that copy and does K1's work for the
+// copied elements on the way: one fp64 partial of (f32(g) * inv)^2 per block,
+// exactly as k1_unscale_norm sums them. k_reduce_segments then turns each
+// parameter's block partials into one partial, in a fixed order, so that K0
+// can finalize from one partial per parameter instead of a K1 pass over the
+// whole buffer.
+
+template <int GD, int U>
+__global__ __launch_bounds__(kBlock) void k1_copy_unscale_norm(const void* __restrict__ src, void* __restrict__ dst,
+                                                               int64_t n, const DsxState* __restrict__ state,
+                                                               double* __restrict__ partials) {
+  using G = Grad<GD>;
+  using E = typename G::elem;
+  const float inv = inv_of(state->scale);
+  const u4* s16 = static_cast<const u4*>(src);
+  u4* d16 = static_cast<u4*>(dst);
+  const E* se = static_cast<const E*>(src);
+  E* de = static_cast<E*>(dst);
+  const int64_t nvec = n / G::per16;
+  const int64_t stride = (int64_t)gridDim.x * kBlock * U;
+  double acc = 0.0;
+  for (int64_t i0 = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; i0 < nvec; i0 += stride) {
+    u4 S[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * kBlock;
+      S[u] = (i < nvec) ? ld<true>(s16 + i) : u4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * kBlock;
+      if (i < nvec) st<true>(d16 + i, S[u]);
+      acc = G::sumsq16(S[u], inv, acc);
+    }
+  }
+  const int64_t tail0 = nvec * G::per16;
+  const int64_t gt = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (gt < n - tail0) {
+    const E e = se[tail0 + gt];
+    de[tail0 + gt] = e;
+    const float a = G::one(e) * inv;
+    acc = __builtin_fma((double)a, (double)a, acc);
+  }
+  const double s = block_sum(acc);
+  if (threadIdx.x == 0) partials[blockIdx.x] = s;
+}
+
+// out[b] = sum of partials[offsets[b] .. offsets[b + 1]), by block b, each
+// thread over a fixed stride and the block reduce in a fixed tree: the same
+// bits for the same partials.
+__global__ __launch_bounds__(kBlock) void k_reduce_segments(const double* __restrict__ partials,
+                                                            const int64_t* __restrict__ offsets,
+                                                            double* __restrict__ out) {
+  const int64_t lo = offsets[blockIdx.x], hi = offsets[blockIdx.x + 1];
+  double acc = 0.0;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += kBlock) acc += partials[i];
+  const double s = block_sum(acc);
+  if (threadIdx.x == 0) out[blockIdx.x] = s;
+}
+
 // ---- K0: finalize ------------------------------------------------------------
 
 // Hyper-parameters a device-resident group block may hold: the admissible
@@ -1001,6 +1063,41 @@ int dsx_zero_step_flat(float* master, float* exp_avg, float* exp_avg_sq, void* p
   if (!rc) rc = do_finalize(partials, nparts, state, scaler, one_group(hyper, bc_table, bc_len), out, s);
   if (!rc) rc = do_adamw_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, out, s);
   return rc;
+}
+
+int dsx_copy_unscale_norm(const void* src, void* dst, int grad_dtype, int64_t n, const DsxState* state,
+                          double* partials, int32_t nparts, void* stream) {
+  if (!is_grad_dtype(grad_dtype))
+    return fail(DSX_EINVAL, "grad dtype must be DSX_F16, DSX_BF16 or DSX_F32 (got %d)", grad_dtype);
+  if (n < 0) return fail(DSX_EINVAL, "n must be >= 0");
+  if (n > 0 && (!src || !dst || !aligned16(src) || !aligned16(dst)))
+    return fail(DSX_EINVAL, "src and dst must be non-null and 16-byte aligned");
+  if (!state) return fail(DSX_EINVAL, "null state");
+  int rc = check_parts(partials, nparts);
+  if (rc) return rc;
+  hipStream_t s = as_stream(stream);
+  const dim3 grid((unsigned)nparts);
+  switch (grad_dtype) {
+    case DSX_BF16:
+      hipLaunchKernelGGL((k1_copy_unscale_norm<DSX_BF16, 4>), grid, dim3(kBlock), 0, s, src, dst, n, state, partials);
+      break;
+    case DSX_F16:
+      hipLaunchKernelGGL((k1_copy_unscale_norm<DSX_F16, 4>), grid, dim3(kBlock), 0, s, src, dst, n, state, partials);
+      break;
+    default:
+      hipLaunchKernelGGL((k1_copy_unscale_norm<DSX_F32, 4>), grid, dim3(kBlock), 0, s, src, dst, n, state, partials);
+      break;
+  }
+  return launch_status("dsx_copy_unscale_norm");
+}
+
+int dsx_reduce_segments(const double* partials, const int64_t* offsets, int32_t nseg, double* out, void* stream) {
+  if (nseg < 1 || nseg > DSX_MAX_PARTIALS)
+    return fail(DSX_EINVAL, "nseg must be in [1, %d] (got %d)", DSX_MAX_PARTIALS, nseg);
+  if (!partials || !offsets || !out) return fail(DSX_EINVAL, "null partials, offsets or out");
+  hipLaunchKernelGGL(k_reduce_segments, dim3((unsigned)nseg), dim3(kBlock), 0, as_stream(stream), partials, offsets,
+                     out);
+  return launch_status("dsx_reduce_segments");
 }
 
 int dsx_unscale_norm_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int grad_dtype,

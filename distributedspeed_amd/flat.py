@@ -53,17 +53,25 @@ def _round_up(x: int, a: int) -> int:
 def _bind_hook(ref, i: int):
     """Post-accumulate-grad hook of parameter i: a grad autograd produced
     outside the flat buffer (p.grad was None) is copied into the parameter's
-    view and p.grad becomes the view again."""
+    view -- with the norm's partial sums taken on the way when the partition
+    collects them -- and p.grad becomes the view again. A grad accumulated
+    into the bound view makes any collected partials stale."""
     def hook(p):
         part = ref()
         if part is None:
             return
         view = part._grad_views[i]
         g = p.grad
-        if g is not view:
-            if g is not None and g.data_ptr() != view.data_ptr():
+        if g is view:
+            part._hn_armed = False
+            return
+        if g is not None and g.data_ptr() != view.data_ptr():
+            if not part._copy_with_norm(i, g):
                 view.copy_(g)
-            p.grad = view
+                part._hn_armed = False
+        else:
+            part._hn_armed = False
+        p.grad = view
     return hook
 
 
@@ -130,6 +138,8 @@ class FlatPartition:
         # The hooks reach the partition through a weak reference, so a
         # parameter that outlives its optimizer does not keep the flat
         # buffers alive; they are removed when the partition goes.
+        self._hn_on = False  # norm partials taken by the hooks' copies (enable_hook_norm)
+        self._hn_armed = False
         ref = weakref.ref(self)
         self._hooks = [p.register_post_accumulate_grad_hook(_bind_hook(ref, i))
                        for i, p in enumerate(self.params) if p.requires_grad]
@@ -178,9 +188,14 @@ class FlatPartition:
         """set_to_none: p.grad = None, so the next backward hands its grads
         over (copied into the views by the hook); otherwise the flat grad
         buffer is zeroed in place and the views stay bound."""
+        self._hn_armed = False
         if set_to_none:
             for p in self.params:
                 p.grad = None
+            if self._hn_on:
+                self._hn_fired = [0] * len(self.params)
+                self._hn_version = self.grad._version
+                self._hn_armed = True
         else:
             self.grad.zero_()
             for p, view in zip(self.params, self._grad_views):
@@ -203,3 +218,78 @@ class FlatPartition:
         return {"params": self.param16.numel() * self.param16.element_size() if self.param16 is not None else 0,
                 "grads": self.grad.numel() * self.grad.element_size(),
                 "optimizer_states": state, "optimizer_states_on_host": self.offload}
+
+    # ---- the norm taken by the hooks' copies ---------------------------------------------
+
+    def enable_hook_norm(self, state: torch.Tensor) -> bool:
+        """From now on the hooks copy grads with dsx_copy_unscale_norm, which
+        also writes the norm's fp64 block partials (a segment per parameter,
+        unscaled by the loss scale in `state`, a DsxState). hook_norm_ready()
+        says when they describe the flat buffer exactly; reduce_hook_norm()
+        then sums each segment into hook_norm_partials (one per parameter),
+        from which K0 finalizes without a K1 pass. False (and off) for more
+        parameters than K0 reads."""
+        from . import _lib, ops
+        if not self.params or len(self.params) > _lib.DSX_MAX_PARTIALS:
+            return False
+        counts = [ops.suggest_partials(s.numel) for s in self.slots]
+        offs = [0]
+        for c in counts:
+            offs.append(offs[-1] + c)
+        dev = self.device
+        self._hn_block = torch.zeros(offs[-1], dtype=torch.float64, device=dev)
+        self._hn_offsets = torch.tensor(offs, dtype=torch.int64).to(dev)
+        self.hook_norm_partials = torch.zeros(len(self.params), dtype=torch.float64, device=dev)
+        base = self._hn_block.data_ptr()
+        self._hn_args = [(v.data_ptr(), s.numel, base + 8 * o, c)
+                         for v, s, o, c in zip(self._grad_views, self.slots, offs, counts)]
+        self._hn_state = state.data_ptr()
+        self._hn_state_ref = state
+        self._hn_gdt = ops.grad_code(self.grad_dtype)
+        lib = _lib.load()
+        self._hn_copy = lib.dsx_copy_unscale_norm
+        self._hn_reduce = lib.dsx_reduce_segments
+        self._hn_fired = [0] * len(self.params)
+        self._hn_version = -1
+        self._hn_on = True
+        return True
+
+    def _copy_with_norm(self, i: int, g: torch.Tensor) -> bool:
+        """The hook's copy of parameter i's grad with its norm partials; False
+        when the partials are not being collected or g does not qualify (the
+        hook then copies with torch and the step runs K1)."""
+        if not (self._hn_on and self._hn_armed):
+            return False
+        dst, n, blk, cnt = self._hn_args[i]
+        if (g.dtype != self.grad_dtype or g.device != self.grad.device or g.numel() != n
+                or not g.is_contiguous() or g.data_ptr() % 16):
+            return False
+        from . import _lib, ops
+        rc = self._hn_copy(g.data_ptr(), dst, self._hn_gdt, n, self._hn_state, blk, cnt, ops.stream_of(self.device))
+        if rc:
+            raise _lib.DsxError("dsx_copy_unscale_norm", rc, _lib.last_error())
+        self._hn_fired[i] += 1
+        self._hn_version = self.grad._version
+        return True
+
+    def hook_norm_ready(self) -> bool:
+        """Whether the hooks' partials describe the flat grad buffer: since
+        zero_grad(set_to_none=True) every parameter was copied by the hook with
+        its partials, nothing accumulated into a bound view, and no torch
+        in-place write touched the buffer afterwards (its version counter)."""
+        return (self._hn_on and self._hn_armed and all(self._hn_fired)
+                and self.grad._version == self._hn_version)
+
+    def reduce_hook_norm(self, stream) -> None:
+        """hook_norm_partials[i] <- sum of parameter i's block partials (one
+        small launch, fixed order)."""
+        from . import _lib
+        rc = self._hn_reduce(self._hn_block.data_ptr(), self._hn_offsets.data_ptr(), len(self.params),
+                             self.hook_norm_partials.data_ptr(), stream)
+        if rc:
+            raise _lib.DsxError("dsx_reduce_segments", rc, _lib.last_error())
+
+    def disarm_hook_norm(self) -> None:
+        """The partials were used (or passed over) by a step: the next one
+        needs new grads."""
+        self._hn_armed = False

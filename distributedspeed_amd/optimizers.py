@@ -340,6 +340,12 @@ class AdamWOptimizer(_FusedAdamWBase):
                     sc = self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
                     self._k2.append(ops.plan_adamw_flat(master, m, v, p16, g, sc))
         self.capturable = bool(capturable)
+        # K1 folded into the hooks' copies (eager form only: a captured or
+        # graph-replayed step keeps its K1).
+        self._k0_hook = None
+        if not self.capturable and not self.use_graph and self.flat.enable_hook_norm(self.dstate):
+            self._k0_hook = ops.FinalizeGroups(self.flat.hook_norm_partials, len(self.flat.params), self.dstate,
+                                               self.scalars, len(self.param_groups))
         if self.capturable:
             # K0 reads the per-group values from device memory, so the launches
             # can be recorded into a caller's graph and replayed.
@@ -410,8 +416,14 @@ class AdamWOptimizer(_FusedAdamWBase):
             self._after_finalize()  # after the replay: waits for the graph's K2 too
             return
         s = ops.stream_of(self.device)
-        self._k1(s)
-        self._k0(self.scaler.to_c(), hs, tables, self._t_offsets, bc_len, s)
+        if self._k0_hook is not None and self.flat.hook_norm_ready():
+            # the hooks' copies already took the norm's partials: no K1 pass
+            self.flat.reduce_hook_norm(s)
+            self._k0_hook(self.scaler.to_c(), hs, tables, self._t_offsets, bc_len, s)
+        else:
+            self._k1(s)
+            self._k0(self.scaler.to_c(), hs, tables, self._t_offsets, bc_len, s)
+        self.flat.disarm_hook_norm()
         self._after_finalize()
         if self.streamer is not None:
             # State in pinned host memory: stream it through HBM chunk by chunk.

@@ -216,6 +216,24 @@ int dsx_unscale_norm(const void* grad, int grad_dtype, int64_t n,
                      const DsxState* state, double* partials, int32_t nparts,
                      void* stream);
 
+/* K1 folded into a copy: dst[0..n) = src[0..n) (grad dtype, both 16-byte
+ * aligned, not overlapping) and partials[0..nparts) = per-block sums of
+ * (f32(src) * inv_scale)^2 in fp64, as dsx_unscale_norm sums them. This is
+ * the copy the flat form's post-accumulate hook makes of the grad autograd
+ * produced (replacing the `param.grad` copy of the reference's packing,
+ * Src/zero/stage1.py:137-144, Src/zero/stage2.py:210-218), with the norm of
+ * Src/zero/utils.py:126-154 taken on the way. */
+int dsx_copy_unscale_norm(const void* src, void* dst, int grad_dtype, int64_t n,
+                          const DsxState* state, double* partials,
+                          int32_t nparts, void* stream);
+
+/* out[b] = sum of partials[offsets[b] .. offsets[b+1]) for b < nseg, each in
+ * a fixed order (offsets: nseg + 1 nondecreasing DEVICE int64 indices into
+ * partials): one partial per parameter from the block partials of its
+ * dsx_copy_unscale_norm, for K0. No counterpart in the reference. */
+int dsx_reduce_segments(const double* partials, const int64_t* offsets,
+                        int32_t nseg, double* out, void* stream);
+
 /* ---- K0: finalize ------------------------------------------------------ */
 
 /* Reduce the partials; decide skip (non-finite sum); on a clean step advance

@@ -102,6 +102,16 @@ def test_argument_checks_reject_before_launch(lib):
     # partial count out of range
     assert lib.dsx_unscale_norm(al, 2, 16, al, al, 0, None) == EINVAL
     assert lib.dsx_unscale_norm(al, 2, 16, al, al, _lib.DSX_MAX_PARTIALS + 1, None) == EINVAL
+    # K1 folded into the hand-over copy, and the segment reduce behind it
+    assert lib.dsx_copy_unscale_norm(al, al, 7, 16, al, al, 1, None) == EINVAL
+    assert lib.dsx_copy_unscale_norm(al, al + 2, 2, 16, al, al, 1, None) == EINVAL
+    assert b"aligned" in lib.dsx_last_error()
+    assert lib.dsx_copy_unscale_norm(al, al, 2, -1, al, al, 1, None) == EINVAL
+    assert lib.dsx_copy_unscale_norm(al, al, 2, 16, None, al, 1, None) == EINVAL
+    assert lib.dsx_copy_unscale_norm(al, al, 2, 16, al, al, 0, None) == EINVAL
+    assert lib.dsx_reduce_segments(al, al, 0, al, None) == EINVAL
+    assert lib.dsx_reduce_segments(al, al, _lib.DSX_MAX_PARTIALS + 1, al, None) == EINVAL
+    assert lib.dsx_reduce_segments(None, al, 4, al, None) == EINVAL
     # the graph path's group block: same checks and wording as dsx_finalize_groups
     g = _lib.DsxGroupsDev()
     g.ngroups = 1

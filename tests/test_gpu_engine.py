@@ -448,3 +448,60 @@ def test_grad_hand_over_matches_in_place_zeroing(gpu):
     for k in runs[0]:
         assert torch.equal(runs[0][k].view(torch.int16 if k == "param16" else torch.int32),
                            runs[1][k].view(torch.int16 if k == "param16" else torch.int32)), k
+
+
+def test_norm_taken_by_the_hand_over_copy(gpu):
+    """K1 folded into the hooks' copies: after zero_grad(set_to_none=True) and
+    one backward the step finalizes from the copies' partials (no K1 pass)
+    and trains bit-identically to the K1 path (in-place zeroing), with the
+    norm equal to 1e-12; the step falls back to K1 when the partials may be
+    stale -- a torch in-place edit of a grad after backward, a parameter with
+    no grad, two micro-batches -- and still matches the K1 path."""
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    _say("norm folded into the hand-over copy")
+
+    def build(spare_used):
+        torch.manual_seed(21)
+        model = torch.nn.Sequential(torch.nn.Linear(96, 160), torch.nn.GELU(), torch.nn.Linear(160, 24)).to(gpu)
+        spare = torch.nn.Parameter(torch.randn(29, device=gpu) * 0.1)
+        opt = AdamWOptimizer(list(model.parameters()) + [spare], lr=1e-3, weight_decay=0.05, max_grad_norm=0.5,
+                             param_dtype=torch.float16, device=gpu,
+                             loss_scaler=ScalerConfig(mode="dynamic", init_scale=2.0 ** 10, window=1000,
+                                                      hysteresis=1))
+        return model, spare, opt
+
+    def run(set_to_none, case):
+        model, spare, opt = build(case != "unused")
+        gen = torch.Generator(device=gpu).manual_seed(5)
+        ready, norms = [], []
+        for _ in range(3):
+            opt.zero_grad(set_to_none=set_to_none)
+            for _ in range(2 if case == "accumulate" else 1):
+                x = torch.randn(24, 96, device=gpu, generator=gen).half()
+                out = model(x).float().pow(2).mean()
+                if case != "unused":
+                    out = out + spare.float().pow(2).sum() * 1e-3
+                (out * opt.loss_scale_tensor()).backward()
+            if case == "edit":
+                for p in model.parameters():
+                    p.grad.mul_(0.5)
+            opt.flat.check_grads_bound()
+            ready.append(opt.flat.hook_norm_ready())
+            opt.step()
+            norms.append(float(opt.grad_norm_tensor().item()))
+        torch.cuda.synchronize()
+        state = {k: getattr(opt.flat, k).clone() for k in ("master", "exp_avg", "exp_avg_sq", "param16")}
+        return ready, norms, state
+
+    for case in ("plain", "edit", "unused", "accumulate"):
+        r_fold, n_fold, s_fold = run(True, case)
+        r_k1, n_k1, s_k1 = run(False, case)
+        assert r_k1 == [False] * 3
+        assert r_fold == ([True] * 3 if case == "plain" else [False] * 3), (case, r_fold)
+        for a, b in zip(n_fold, n_k1):
+            assert a == pytest.approx(b, rel=1e-12), case
+        for k in s_fold:
+            dt = torch.int16 if k == "param16" else torch.int32
+            assert torch.equal(s_fold[k].view(dt), s_k1[k].view(dt)), (case, k)
