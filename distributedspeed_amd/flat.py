@@ -25,7 +25,10 @@ the default, p.grad is None, so autograd hands over the grad it produced
 and a post-accumulate-grad hook copies it into the view (2 B read, 2 B
 written) and rebinds p.grad to the view, which later micro-batches then
 accumulate into: 4 B/elt instead of 8 for the first micro-batch, and the
-copies run during backward. A parameter that received no grad is zeroed in
+copies run during backward. When the partition collects the norm
+(enable_hook_norm, the optimizer's eager step), the hook's copy also writes
+the norm's partial sums, and a step whose grads all arrived that way skips
+its own pass over the grads (hook_norm_ready). A parameter that received no grad is zeroed in
 its view before the step (check_grads_bound) and takes an AdamW step with a
 zero grad, as torch does after zero_grad(set_to_none=False). Code that
 writes grads straight into the flat buffer keeps the views bound with
