@@ -69,7 +69,7 @@ def _bind_hook(ref, i: int):
             part._hn_armed = False
             return
         if g is not None and g.data_ptr() != view.data_ptr():
-            if not part._copy_with_norm(i, g):
+            if not (part._hn_armed and part._copy_with_norm(i, g)):
                 view.copy_(g)
                 part._hn_armed = False
         else:
@@ -202,7 +202,8 @@ class FlatPartition:
         else:
             self.grad.zero_()
             for p, view in zip(self.params, self._grad_views):
-                p.grad = view
+                if p.grad is not view:
+                    p.grad = view
 
     def refresh_params16(self) -> None:
         """param16 <- master (RNE), after the master was loaded."""
@@ -252,24 +253,25 @@ class FlatPartition:
         lib = _lib.load()
         self._hn_copy = lib.dsx_copy_unscale_norm
         self._hn_reduce = lib.dsx_reduce_segments
+        self._hn_stream = ops.stream_of
         self._hn_fired = [0] * len(self.params)
         self._hn_version = -1
         self._hn_on = True
         return True
 
     def _copy_with_norm(self, i: int, g: torch.Tensor) -> bool:
-        """The hook's copy of parameter i's grad with its norm partials; False
-        when the partials are not being collected or g does not qualify (the
-        hook then copies with torch and the step runs K1)."""
-        if not (self._hn_on and self._hn_armed):
+        """The hook's copy of parameter i's grad with its norm partials (the
+        caller checked that they are being collected); False when g does not
+        qualify (the hook then copies with torch and the step runs K1).
+        Autograd hands over a grad of the parameter's dtype, device and
+        shape, so what is left to check is its layout."""
+        ptr = g.data_ptr()
+        if ptr & 15 or not g.is_contiguous():
             return False
         dst, n, blk, cnt = self._hn_args[i]
-        if (g.dtype != self.grad_dtype or g.device != self.grad.device or g.numel() != n
-                or not g.is_contiguous() or g.data_ptr() % 16):
-            return False
-        from . import _lib, ops
-        rc = self._hn_copy(g.data_ptr(), dst, self._hn_gdt, n, self._hn_state, blk, cnt, ops.stream_of(self.device))
+        rc = self._hn_copy(ptr, dst, self._hn_gdt, n, self._hn_state, blk, cnt, self._hn_stream(self.device))
         if rc:
+            from . import _lib
             raise _lib.DsxError("dsx_copy_unscale_norm", rc, _lib.last_error())
         self._hn_fired[i] += 1
         self._hn_version = self.grad._version
