@@ -79,6 +79,7 @@ bool is_grad_dtype(int dt) { return dt == DSX_F16 || dt == DSX_BF16 || dt == DSX
 // the small-partition shape; 5e8: 2.51 against 2.55 ms). K1 (read-only) runs
 // best with two blocks per CU. Nontemporal hints help both by a few percent.
 constexpr int64_t kK2LargeN = int64_t(3) << 27;  // K2's large-partition shape from here on
+constexpr int64_t kMaxGridBlocks = int64_t(1) << 22;  // 2^30 work-items of kBlock threads
 
 struct Tuning {
   int k1_blocks_per_cu = 2;
@@ -1155,6 +1156,9 @@ int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t
   }
   int64_t blocks = cus * bpc;
   if (blocks > nchunks) blocks = nchunks;
+  // Blocks take chunks grid-stride, so any grid covers the table; keep it
+  // within HIP's 2^32 work-items per grid dimension.
+  if (blocks > kMaxGridBlocks) blocks = kMaxGridBlocks;
   hipStream_t s = as_stream(stream);
   const dim3 grid((unsigned)blocks);
   switch (grad_dtype) {
