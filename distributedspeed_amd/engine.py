@@ -16,11 +16,14 @@ fused step:
                        overflow) and zero_grad, as DeepSpeed's engine does
                        after a boundary step
   save_checkpoint / load_checkpoint   flat state keyed by parameter name
+  module.load_state_dict  after initialize: the fp32 master is taken from
+                       the loaded params (a post-load hook on the module)
 """
 from __future__ import annotations
 
 import json
 import os
+import weakref
 from typing import Any, Optional
 
 import torch
@@ -76,6 +79,17 @@ class DistributedSpeedEngine(torch.nn.Module):
         zcfg = {"stage": config.zero_optimization.stage,
                 "gradient_accumulation_steps": config.gradient_accumulation_steps}
         self.optimizer = ZeROOptimizer(optimizer, zcfg, list(optimizer.dsx_params))
+        # With 16-bit params the step reads and writes the fp32 master; a state
+        # dict loaded into the module later writes only the params, so the
+        # master follows them (the reference steps the params themselves).
+        opt_ref = weakref.ref(optimizer)
+
+        def _master_follows_params(module, incompatible_keys):
+            opt = opt_ref()
+            if opt is not None:
+                opt.refresh_master()
+
+        self.module.register_load_state_dict_post_hook(_master_follows_params)
         self.lr_scheduler = lr_scheduler
         # DeepSpeed's engine leaves the LR scheduler alone on a step skipped for
         # overflow. Under dynamic loss scaling the engine therefore needs the

@@ -211,6 +211,20 @@ class FlatPartition:
             with torch.no_grad():
                 self.param16.copy_(self.master.to(self.device))
 
+    def refresh_master(self, indices=None) -> None:
+        """master <- fp32(param) for the given parameters (all by default),
+        after the 16-bit params were written from outside the step (a model
+        state dict loaded after construction). The step reads only the
+        master, so it would otherwise write the old values back over them.
+        With fp32 training the params are views into the master: nothing to
+        do."""
+        if self.param16 is None:
+            return
+        with torch.no_grad():
+            for i in (range(len(self.slots)) if indices is None else indices):
+                s = self.slots[i]
+                self.master[s.offset:s.offset + s.numel].copy_(self.param16[s.offset:s.offset + s.numel])
+
     def layout(self) -> list[dict]:
         return [{"name": s.name, "offset": s.offset, "numel": s.numel, "shape": list(s.shape), "group": s.group}
                 for s in self.slots]

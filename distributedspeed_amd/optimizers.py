@@ -224,6 +224,26 @@ class _FusedAdamWBase(torch.optim.Optimizer):
 
     # ---- device-side values, read on demand --------------------------------------------------
 
+    def refresh_master(self) -> None:
+        """Take the fp32 master from the current params. Needed after the
+        16-bit params were written from outside the step, e.g. a model state
+        dict loaded after this optimizer was built (the engine does this by
+        itself for its module); the step reads only the master and would
+        otherwise write the old values back."""
+        self.store.refresh_master()
+
+    def set_scaler_state(self, scale: float, good_steps: int = 0) -> None:
+        """Loss scale and clean-step count of a dynamic scaler (as from a
+        torch GradScaler's state dict); other modes keep their own scale."""
+        if self.scaler.mode != "dynamic":
+            return
+        if not (scale > 0 and math.isfinite(scale)):
+            raise ValueError(f"loss scale must be finite and > 0, got {scale}")
+        hs = self.read_state()
+        hs.scale = float(scale)
+        hs.good_steps = int(good_steps)
+        self.dstate.copy_(torch.frombuffer(bytearray(bytes(hs)), dtype=torch.uint8).to(self.device))
+
     def loss_scale_tensor(self) -> torch.Tensor:
         """The loss scale as a one-element fp32 device tensor (no sync)."""
         return ops.scale_view(self.dstate)
@@ -276,6 +296,10 @@ class _FusedAdamWBase(torch.optim.Optimizer):
                 if k != "params":
                     g[k] = tuple(v) if k == "betas" else v
         st = state_dict["state"]
+        # A torch (or the reference's) state dict holds no master: those
+        # parameters take theirs from the current params, which the caller
+        # loads from the same checkpoint.
+        self.store.refresh_master([i for i in range(len(self.store.params)) if "master" not in st.get(i, {})])
         with torch.no_grad():
             for i in range(len(self.store.params)):
                 if i not in st:

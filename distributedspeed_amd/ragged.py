@@ -134,6 +134,16 @@ class RaggedParams:
             for p, m in zip(self.params, self.master):
                 p.data.copy_(m)
 
+    def refresh_master(self, indices=None) -> None:
+        """master <- fp32(param) for the given parameters (all by default),
+        after the 16-bit params were written from outside the step; with fp32
+        training the param is the master."""
+        if self.param_dtype is None:
+            return
+        with torch.no_grad():
+            for i in (range(len(self.params)) if indices is None else indices):
+                self.master[i].copy_(self.params[i].data)
+
     def storage_bytes(self) -> dict:
         """Bytes held per the layout: 16-bit params (with fp32 training the
         param is the master), grads of the grad dtype, fp32 master/m/v."""

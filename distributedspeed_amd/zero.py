@@ -163,8 +163,13 @@ class ZeROOptimizer:
         sd["current_step"] = int(sd["dsx"]["t"]) + self._step_base
         sd["overflow_count"] = int(sd["dsx"]["overflow_count"]) - self._overflow_base
         sd["gradient_accumulation_count"] = self.gradient_accumulation_count
-        sd["grad_scaler"] = {"scale": sd["dsx"]["scale"], "growth_tracker": sd["dsx"]["good_steps"],
-                             "hysteresis_left": sd["dsx"]["hyst_left"]}
+        # torch's GradScaler.state_dict keys (what the reference stores and
+        # loads), plus the hysteresis count torch's scaler does not have
+        sc = self.base_optimizer.scaler
+        if sc.mode == "dynamic":
+            sd["grad_scaler"] = {"scale": sd["dsx"]["scale"], "growth_factor": sc.growth_factor,
+                                 "backoff_factor": sc.backoff_factor, "growth_interval": sc.window,
+                                 "_growth_tracker": sd["dsx"]["good_steps"], "hysteresis_left": sd["dsx"]["hyst_left"]}
         return sd
 
     def load_state_dict(self, state_dict: Dict[str, Any]) -> None:
@@ -172,9 +177,13 @@ class ZeROOptimizer:
         current_step = state_dict.pop("current_step", None)
         overflow_count = state_dict.pop("overflow_count", None)
         self.gradient_accumulation_count = state_dict.pop("gradient_accumulation_count", 0)
-        state_dict.pop("grad_scaler", None)
+        scaler = state_dict.pop("grad_scaler", None)
         state_dict.pop("zero_stage", None)
         self.base_optimizer.load_state_dict(state_dict)
+        if "dsx" not in state_dict and scaler and "scale" in scaler:
+            # the reference's state dict: its GradScaler's state
+            # (Src/zero/optimizer.py:375-376, 397-398; torch's GradScaler.state_dict keys)
+            self.base_optimizer.set_scaler_state(float(scaler["scale"]), int(scaler.get("_growth_tracker", 0)))
         st = self.base_optimizer.read_state()
         self._step_base = 0 if current_step is None else int(current_step) - int(st.t)
         self._overflow_base = 0 if overflow_count is None else int(st.overflow_count) - int(overflow_count)

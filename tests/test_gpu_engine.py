@@ -254,6 +254,75 @@ def test_checkpoint_round_trip_is_bit_exact(gpu, tmp_path, contiguous):
     assert (s1.scale, s1.t, s1.good_steps, s1.overflow_count) == (s2.scale, s2.t, s2.good_steps, s2.overflow_count)
 
 
+@pytest.mark.parametrize("contiguous", [True, False])
+def test_model_state_loaded_after_initialize_is_kept(gpu, contiguous):
+    """A model state dict loaded into the module after initialize() writes
+    the 16-bit params; the fp32 master follows them, so the next step starts
+    from the loaded weights (the reference steps the params themselves).
+    With lr 0 and no weight decay that step leaves them exactly as loaded;
+    a stale master would write the initial weights back."""
+    import torch
+    import distributedspeed_amd as ds
+    _say(f"model state loaded after initialize, contiguous_gradients={contiguous}")
+    cfg = {"fp16": {"enabled": True, "hysteresis": 1},
+           "optimizer": {"type": "AdamW", "params": {"lr": 0.0, "weight_decay": 0.0}},
+           "zero_optimization": {"stage": 2, "contiguous_gradients": contiguous}}
+    engine, _, _, _ = ds.initialize(_mlp(5), cfg)
+    target = {k: v.clone() for k, v in _mlp(6).half().state_dict().items()}
+    engine.module.load_state_dict(target)
+    x = torch.randn(16, 784, device=gpu)
+    engine.backward(engine(x).float().pow(2).mean())
+    engine.step()
+    after = engine.module.state_dict()
+    for k, v in target.items():
+        assert torch.equal(after[k].cpu(), v), k
+
+
+def test_reference_format_state_dict_loads(gpu):
+    """The reference's ZeROOptimizer.state_dict() over torch.optim.AdamW
+    (Src/zero/optimizer.py:356-381: torch's AdamW state dict plus
+    zero_stage, current_step, overflow_count, gradient_accumulation_count
+    and a torch GradScaler's state dict) loads into the fused optimizer: the
+    moments by parameter index, the master from the params, the step count,
+    the overflow count and the dynamic loss scale. The state dict written
+    back carries torch's GradScaler keys, which torch's GradScaler loads."""
+    import torch
+    import distributedspeed_amd as ds
+    _say("reference-format state dict")
+    ref_model = _mlp(7).to(gpu)
+    topt = torch.optim.AdamW(ref_model.parameters(), lr=1e-3, weight_decay=0.01)
+    gen = torch.Generator(device=gpu).manual_seed(4)
+    for _ in range(3):
+        ref_model(torch.randn(8, 784, device=gpu, generator=gen)).pow(2).mean().backward()
+        topt.step()
+        topt.zero_grad()
+    gs = torch.amp.GradScaler("cuda", init_scale=4096.0)
+    gs_sd = gs.state_dict()
+    gs_sd["_growth_tracker"] = 7
+    ref_sd = topt.state_dict()
+    ref_sd.update(zero_stage=2, current_step=3, overflow_count=1, gradient_accumulation_count=0, grad_scaler=gs_sd)
+
+    model = _mlp(8)
+    model.load_state_dict({k: v.detach().cpu() for k, v in ref_model.state_dict().items()})
+    cfg = {"fp16": {"enabled": True, "initial_scale_power": 16, "hysteresis": 1},
+           "optimizer": {"type": "AdamW", "params": {"lr": 1e-3, "weight_decay": 0.01}}}
+    engine, opt, _, _ = ds.initialize(model, cfg)
+    opt.load_state_dict(ref_sd)
+    assert opt.current_step == 3 and opt.overflow_count == 1
+    assert opt.loss_scale == 4096.0 and opt.base_optimizer.read_state().good_steps == 7
+    base = opt.base_optimizer
+    for i, p in enumerate(ref_model.parameters()):
+        v = base.store.views_of(i)
+        assert torch.equal(v["exp_avg"].cpu(), topt.state[p]["exp_avg"].cpu()), i
+        assert torch.equal(v["exp_avg_sq"].cpu(), topt.state[p]["exp_avg_sq"].cpu()), i
+        assert torch.equal(v["master"].cpu(), p.detach().half().float().cpu()), i
+
+    back = opt.state_dict()["grad_scaler"]
+    gs2 = torch.amp.GradScaler("cuda", init_scale=1.0)
+    gs2.load_state_dict(back)
+    assert gs2.get_scale() == 4096.0 and gs2.state_dict()["_growth_tracker"] == 7
+
+
 def test_initialize_refuses_multi_rank(gpu, monkeypatch):
     import distributedspeed_amd as ds
     monkeypatch.setenv("WORLD_SIZE", "2")
