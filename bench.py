@@ -44,7 +44,8 @@ def _args():
     ap.add_argument("--torch-gpu", type=int, default=1,
                     help="also time the reference's update as torch ops on this GPU (context line; 0 disables)")
     ap.add_argument("--tuning", default="",
-                    help="k1_bpc,k2_bpc,k2_unroll,nt[,k2_cu_eighths,k2_drain] (library launch-shape override)")
+                    help="k1_bpc,k2_bpc,k2_unroll,nt[,k2_cu_eighths,k2_drain] (library launch-shape override; "
+                         "the default is 2,0,0,1,0,-1: 0 and -1 pick by size)")
     ap.add_argument("--tuning-multi", default="",
                     help="k3_bpc,k3_unroll,nt,drain (K3 launch-shape override; k3_bpc 0 picks by chunk count)")
     ap.add_argument("--workload", default="llama8b-shard",

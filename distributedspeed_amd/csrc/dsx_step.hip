@@ -69,9 +69,12 @@ bool is_grad_dtype(int dt) { return dt == DSX_F16 || dt == DSX_BF16 || dt == DSX
 // ---- launch shape ----------------------------------------------------------
 
 // Defaults from launch-shape sweeps of the library's kernels on MI355X over
-// partitions of 1.9e6 to 1.0e9 elements. K2 (one 256-thread block per CU
-// unless said otherwise) has two regimes. Up to ~2.5e8 elements, 2 slots per
-// thread per trip with a block on every CU is best. From ~5e8 elements up,
+// partitions of 1.0e6 to 1.0e9 elements. K2 (256-thread blocks) has three
+// regimes. Up to 32 blocks per CU of one trip each (2 slots per thread: up to
+// 16.8e6 elements), every block makes one trip, so that all loads are in
+// flight at once (2-12% faster than one block per CU from 2 Mi to 16 Mi
+// elements; the same at 1 Mi and 32 Mi). Up to ~2.5e8 elements, one block per
+// CU with 2 slots per thread per trip is best. From ~5e8 elements up,
 // K2's 50:50 read/write stream runs best when the chip issues fewer requests
 // than it could: 4 slots per thread, each wave waiting for its own stores to
 // complete before it loads the next trip ("drain"), and blocks on only 7 of
@@ -80,12 +83,15 @@ bool is_grad_dtype(int dt) { return dt == DSX_F16 || dt == DSX_BF16 || dt == DSX
 // best with two blocks per CU. Nontemporal hints help both by a few percent.
 constexpr int64_t kK2LargeN = int64_t(3) << 27;  // K2's large-partition shape from here on
 constexpr int64_t kMaxGridBlocks = int64_t(1) << 22;  // 2^30 work-items of kBlock threads
+constexpr int64_t kK2OneTripPerCu = 32;  // K2's one-trip grid up to this many blocks per CU
 
 struct Tuning {
   int k1_blocks_per_cu = 2;
-  int k2_blocks_per_cu = 1;
-  // K2's shape; 0 (-1 for the drain) picks by n: below kK2LargeN 8 eighths,
-  // 2 slots, no drain; from kK2LargeN on 7 eighths, 4 slots, drain.
+  // K2's shape; 0 (-1 for the drain) picks by n: below kK2LargeN 2 slots,
+  // no drain, and one trip per block while that takes at most
+  // kK2OneTripPerCu blocks per CU, else one block per CU on 8 eighths; from
+  // kK2LargeN on one block per CU on 7 eighths, 4 slots, drain.
+  int k2_blocks_per_cu = 0;
   int k2_cu_eighths = 0;  // blocks on this many eighths of the CUs
   int k2_unroll = 0;      // slots per thread per trip: 2, 4 or 8
   int k2_drain = -1;      // wait for a trip's stores before the next trip's loads
@@ -710,11 +716,18 @@ template <int GD, int PD, int U>
 void launch_k2_u(float* p, float* m, float* v, void* p16, const void* g, int64_t n, const DsxStepScalars* sc,
                  hipStream_t s) {
   const int64_t slots = n >> 2;
-  int64_t blocks = ceil_div(slots > 0 ? slots : 1, (int64_t)kBlock * U);
+  int64_t blocks = ceil_div(slots > 0 ? slots : 1, (int64_t)kBlock * U);  // one trip each
   const bool large = n >= kK2LargeN;
   const int eighths = g_tune.k2_cu_eighths ? g_tune.k2_cu_eighths : (large ? 7 : 8);
   const bool drain = g_tune.k2_drain >= 0 ? g_tune.k2_drain != 0 : large;
-  int64_t cap = (int64_t)cu_count() * g_tune.k2_blocks_per_cu * eighths / 8;
+  const int64_t cus = cu_count();
+  int64_t cap;
+  if (g_tune.k2_blocks_per_cu > 0)
+    cap = cus * g_tune.k2_blocks_per_cu * eighths / 8;
+  else if (!large && blocks <= cus * kK2OneTripPerCu)
+    cap = blocks;
+  else
+    cap = cus * eighths / 8;
   if (cap < 1) cap = 1;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
@@ -877,7 +890,7 @@ int dsx_abi_version(void) { return DSX_ABI_VERSION; }
 const char* dsx_last_error(void) { return g_err; }
 
 int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll, int nontemporal) {
-  if (k1_blocks_per_cu < 1 || k1_blocks_per_cu > 32 || k2_blocks_per_cu < 1 || k2_blocks_per_cu > 64)
+  if (k1_blocks_per_cu < 1 || k1_blocks_per_cu > 32 || k2_blocks_per_cu < 0 || k2_blocks_per_cu > 64)
     return fail(DSX_EINVAL, "blocks per CU out of range");
   if (k2_unroll != 0 && k2_unroll != 2 && k2_unroll != 4 && k2_unroll != 8)
     return fail(DSX_EINVAL, "k2_unroll must be 0 (by size), 2, 4 or 8");

@@ -159,9 +159,11 @@ int         dsx_abi_version(void);
 const char* dsx_last_error(void);
 
 /* Launch-shape override for the current process (library tuning; no
- * counterpart in the reference): K1 and K2 blocks per CU, K2 slots per
- * thread per trip (2, 4 or 8; 0, the default, picks 2 below 3 * 2^27
- * elements and 4 from there on) and the nontemporal hint (0/1). */
+ * counterpart in the reference): K1 blocks per CU (default 2), K2 blocks per
+ * CU (0, the default, picks by n: below 3 * 2^27 elements one trip per block
+ * while that takes at most 32 blocks per CU, else one block per CU), K2
+ * slots per thread per trip (2, 4 or 8; 0, the default, picks 2 below
+ * 3 * 2^27 elements and 4 from there on) and the nontemporal hint (0/1). */
 int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll,
                    int nontemporal);
 

@@ -461,7 +461,8 @@ def test_multi_tensor_groups(gpu, oracle):
 
 
 def test_k2_launch_shapes_give_identical_bits(gpu, oracle):
-    """Every K2 launch shape the tuning calls can select (slots per thread
+    """Every K2 launch shape the tuning calls can select (one block per CU
+    or the automatic grid -- here one trip per block --, slots per thread
     2/4/8, drain on/off, grids on 1, 7 or 8 eighths of the CUs) computes the
     same bits as the oracle; the automatic shape is restored afterwards."""
     from distributedspeed_amd import _lib
@@ -472,18 +473,20 @@ def test_k2_launch_shapes_give_identical_bits(gpu, oracle):
     rp, rm, rv, rp16 = p.copy(), m.copy(), v.copy(), np.empty(n, np.uint16)
     O.adamw(rp, rm, rv, rp16, BF16, g16, BF16, sc)
     try:
-        for unroll in (2, 4, 8):
-            for drain in (0, 1):
-                for eighths in (1, 7, 8):
-                    assert _lib.call("dsx_set_tuning", 2, 1, unroll, 1) == 0
-                    assert _lib.call("dsx_set_tuning_k2", eighths, drain) == 0
-                    _say(f"k2 shape unroll={unroll} drain={drain} eighths={eighths}")
-                    gp, gm, gv, gp16 = _run_k2(gpu, p, m, v, g16, BF16, BF16, sc)
-                    for name, a, b in (("master", gp, rp), ("exp_avg", gm, rm), ("exp_avg_sq", gv, rv)):
-                        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (name, unroll, drain, eighths)
-                    assert np.array_equal(gp16, rp16), (unroll, drain, eighths)
+        for bpc in (0, 1):
+            for unroll in (2, 4, 8):
+                for drain in (0, 1):
+                    for eighths in (1, 7, 8):
+                        assert _lib.call("dsx_set_tuning", 2, bpc, unroll, 1) == 0
+                        assert _lib.call("dsx_set_tuning_k2", eighths, drain) == 0
+                        case = (bpc, unroll, drain, eighths)
+                        _say(f"k2 shape bpc={bpc} unroll={unroll} drain={drain} eighths={eighths}")
+                        gp, gm, gv, gp16 = _run_k2(gpu, p, m, v, g16, BF16, BF16, sc)
+                        for name, a, b in (("master", gp, rp), ("exp_avg", gm, rm), ("exp_avg_sq", gv, rv)):
+                            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (name,) + case
+                        assert np.array_equal(gp16, rp16), case
     finally:
-        _lib.call("dsx_set_tuning", 2, 1, 0, 1)
+        _lib.call("dsx_set_tuning", 2, 0, 0, 1)
         _lib.call("dsx_set_tuning_k2", 0, -1)
 
 
