@@ -37,7 +37,7 @@ def _args():
     ap.add_argument("--numel", type=int, default=HEADLINE_NUMEL)
     ap.add_argument("--cpu-sample", type=int, default=128 * 1024 * 1024,
                     help="elements in the CPU-baseline sample (0 disables it)")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU time budget of the port's timed steps (torch's gets half)")
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                       "k2_adamw_flat_llama8b_shard_traffic.json"))
@@ -573,7 +573,7 @@ def torch_gpu_reference(master, grad16, hyper, ours_ms: float, steps: int = 5) -
     return res
 
 
-def cpu_baseline(n_sample: int, hyper, seconds: float = 8.0) -> dict | None:
+def cpu_baseline(n_sample: int, hyper, seconds: float = 12.0) -> dict | None:
     """The C oracle (a CPU port of the step: the norm as 1024 compensated
     block sums, the AdamW loop, both on OpenMP threads) on a bounded sample,
     on this host's cores, stepping until `seconds` of timed work (at least 3 steps);
