@@ -219,6 +219,35 @@ def test_torch_adamw_is_adopted(gpu):
         ds.initialize(_mlp(4), {}, optimizer=torch.optim.SGD(_mlp(4).parameters(), lr=0.1))
 
 
+@pytest.mark.parametrize("cls_name", ["AdamWOptimizer", "MultiTensorAdamWOptimizer"])
+def test_rebuilt_from_param_groups_and_defaults(gpu, cls_name):
+    """The ZeRO stages rebuild their optimizer as
+    type(opt)(groups, **opt.defaults) (Src/zero/stage1.py:358). A fused
+    optimizer rebuilt that way takes the parameters over (their storage and
+    grads move to it) and steps bit for bit as one built fresh over the same
+    weights; attributes of the base optimizer reach through ZeROOptimizer."""
+    import torch
+    from distributedspeed_amd import optimizers as O
+    from distributedspeed_amd.zero import ZeROOptimizer
+    _say(f"rebuilt from param_groups and defaults: {cls_name}")
+    cls = getattr(O, cls_name)
+    m1, m2 = _mlp(11).to(gpu), _mlp(11).to(gpu)
+    o1 = cls(m1.parameters(), lr=1e-3, betas=(0.8, 0.95), weight_decay=0.01)
+    rebuilt = type(o1)(o1.param_groups, **o1.defaults)
+    fresh = cls(m2.parameters(), lr=1e-3, betas=(0.8, 0.95), weight_decay=0.01)
+    assert rebuilt.defaults == fresh.defaults == o1.defaults
+    x = torch.randn(8, 784, device=gpu)
+    for model, opt in ((m1, rebuilt), (m2, fresh)):
+        for _ in range(3):
+            opt.zero_grad()
+            model(x).pow(2).mean().backward()
+            opt.step()
+    for a, b in zip(m1.parameters(), m2.parameters()):
+        assert torch.equal(a.detach(), b.detach())
+    z = ZeROOptimizer(rebuilt, {"stage": 1})
+    assert z.numel == rebuilt.numel and z.layout() == rebuilt.layout() and z.defaults == rebuilt.defaults
+
+
 @pytest.mark.parametrize("contiguous", [True, False])
 def test_checkpoint_round_trip_is_bit_exact(gpu, tmp_path, contiguous):
     import torch
