@@ -747,6 +747,20 @@ def main() -> int:
     k2_gbs = K2_BYTES * n / (k2_ms * 1e-3) / 1e9
     k1_gbs = K1_BYTES * n / (k1_ms * 1e-3) / 1e9
 
+    # K2's own access pattern without its math: the same bytes in the same
+    # launch shape on the same buffers (dsx_traffic_probe_flat), timed after
+    # the measured steps. K2 at or above it means the math costs nothing and
+    # the memory system sets the bound.
+    _progress("traffic probe")
+    pev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(a.steps)]
+    for i in range(a.steps):
+        pev[i][0].record()
+        ops.traffic_probe_flat(master, exp_avg, exp_avg_sq, p16, grad)
+        pev[i][1].record()
+    torch.cuda.synchronize()
+    probe_ms = sum(e[0].elapsed_time(e[1]) for e in pev) / a.steps
+    probe_gbs = K2_BYTES * n / (probe_ms * 1e-3) / 1e9
+
     traffic = None
     if os.path.exists(a.traffic):
         try:
@@ -783,6 +797,9 @@ def main() -> int:
         "kernels_ms": {"k1_unscale_norm": round(k1_ms, 4), "k0_finalize": round(k0_ms, 4),
                        "k2_adamw_flat": round(k2_ms, 4)},
         "k1_gbs": round(k1_gbs, 1),
+        "k2_traffic_probe": {"what": "K2's loads, stores and launch shape without the AdamW math, same buffers",
+                             "ms": round(probe_ms, 4), "gbs": round(probe_gbs, 1),
+                             "k2_over_probe": round(k2_gbs / probe_gbs, 4)},
         "roofline": {"bound": "hbm", "achieved": round(k2_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k2_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k2_adamw_flat", "algorithmic_bytes_per_launch": K2_BYTES * n},

@@ -91,6 +91,7 @@ SIGNATURES = {
     "dsx_finalize_dev": (_c.c_int, [_P, _c.c_int32, _P, DsxScalerConfig, _P, _c.c_int32, _P, _P]),
     "dsx_groups_upload": (_c.c_int, [_P, _P, _P]),
     "dsx_adamw_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, _P]),
+    "dsx_traffic_probe_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int64, _P]),
     "dsx_zero_step_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, DsxScalerConfig,
                                       DsxAdamwHyper, _P, _c.c_int32, _P, _c.c_int32, _P, _P]),
     "dsx_unscale_norm_multi": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _P, _P, _c.c_int32, _P]),

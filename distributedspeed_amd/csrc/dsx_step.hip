@@ -525,15 +525,21 @@ __global__ void k_state_init(DsxState* state, float scale, int32_t hysteresis) {
 
 // ---- K2: AdamW + cast over a flat partition ----------------------------------
 
-template <int GD, int PD, int U, bool NT, bool DRAIN>
-__global__ __launch_bounds__(kBlock) void k2_adamw_flat(float* __restrict__ p, float* __restrict__ m,
-                                                        float* __restrict__ v, uint16_t* __restrict__ p16,
-                                                        const void* __restrict__ gv, int64_t n,
-                                                        const DsxStepScalars* __restrict__ scp) {
+// The slot loop of K2. MATH = false is the traffic probe: the same loads,
+// stores, cast and launch shape with the AdamW math left out, so that K2 can
+// be timed against its own access pattern (the values written back are the
+// ones read, and p16 gets the cast of the unchanged master).
+template <int GD, int PD, int U, bool NT, bool DRAIN, bool MATH>
+__device__ __forceinline__ void k2_flat_body(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
+                                             uint16_t* __restrict__ p16, const void* __restrict__ gv, int64_t n,
+                                             const DsxStepScalars* __restrict__ scp) {
   using G = Grad<GD>;
   using GS = typename G::slot4;
-  if (scp->skip) return;
-  const Sc s = load_sc(*scp);
+  Sc s = {};
+  if constexpr (MATH) {
+    if (scp->skip) return;
+    s = load_sc(*scp);
+  }
   f4* p4 = reinterpret_cast<f4*>(p);
   f4* m4 = reinterpret_cast<f4*>(m);
   f4* v4 = reinterpret_cast<f4*>(v);
@@ -560,10 +566,15 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_flat(float* __restrict__ p, f
     for (int u = 0; u < U; ++u) {
       const int64_t i = i0 + (int64_t)u * kBlock;
       if (i < nvec) {
-        float gf[4];
-        G::four(Gs[u], gf);
         f4 pp = P[u], mm = M[u], vv = V[u];
-        adamw4(gf, pp, mm, vv, s);
+        if constexpr (MATH) {
+          float gf[4];
+          G::four(Gs[u], gf);
+          adamw4(gf, pp, mm, vv, s);
+        } else {
+          // opaque to the compiler: every load and store stays, as in K2
+          asm volatile("" : "+v"(pp), "+v"(mm), "+v"(vv) : "v"(Gs[u]));
+        }
         st<NT>(p4 + i, pp);
         st<NT>(m4 + i, mm);
         st<NT>(v4 + i, vv);
@@ -579,10 +590,30 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_flat(float* __restrict__ p, f
   if (gt < n - tail0) {
     const int64_t e = tail0 + gt;
     float pe = p[e], me = m[e], ve = v[e];
-    adamw_elt(G::one(g[e]), pe, me, ve, s);
+    if constexpr (MATH) {
+      adamw_elt(G::one(g[e]), pe, me, ve, s);
+    } else {
+      asm volatile("" : "+v"(pe), "+v"(me), "+v"(ve) : "v"(G::one(g[e])));
+    }
     p[e] = pe; m[e] = me; v[e] = ve;
     if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
   }
+}
+
+template <int GD, int PD, int U, bool NT, bool DRAIN>
+__global__ __launch_bounds__(kBlock) void k2_adamw_flat(float* __restrict__ p, float* __restrict__ m,
+                                                        float* __restrict__ v, uint16_t* __restrict__ p16,
+                                                        const void* __restrict__ gv, int64_t n,
+                                                        const DsxStepScalars* __restrict__ scp) {
+  k2_flat_body<GD, PD, U, NT, DRAIN, true>(p, m, v, p16, gv, n, scp);
+}
+
+template <int GD, int PD, int U, bool NT, bool DRAIN>
+__global__ __launch_bounds__(kBlock) void k2_traffic_probe(float* __restrict__ p, float* __restrict__ m,
+                                                           float* __restrict__ v, uint16_t* __restrict__ p16,
+                                                           const void* __restrict__ gv, int64_t n,
+                                                           const DsxStepScalars* __restrict__ scp) {
+  k2_flat_body<GD, PD, U, NT, DRAIN, false>(p, m, v, p16, gv, n, scp);
 }
 
 // ---- K3: ragged lists ----------------------------------------------------------
@@ -712,9 +743,21 @@ void launch_k1(const void* g, int64_t n, const DsxState* st, double* partials, i
     hipLaunchKernelGGL((k1_unscale_norm<GD, 4, false>), dim3(nparts), dim3(kBlock), 0, s, g, n, st, partials);
 }
 
+template <int GD, int PD, int U, bool NT, bool DRAIN>
+void k2_launch_one(bool probe, dim3 grid, hipStream_t s, float* p, float* m, float* v, uint16_t* o, const void* g,
+                   int64_t n, const DsxStepScalars* sc) {
+  if constexpr (GD == PD) {  // the probe is built for 16-bit training only
+    if (probe) {
+      hipLaunchKernelGGL((k2_traffic_probe<GD, PD, U, NT, DRAIN>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n, sc);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, NT, DRAIN>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n, sc);
+}
+
 template <int GD, int PD, int U>
 void launch_k2_u(float* p, float* m, float* v, void* p16, const void* g, int64_t n, const DsxStepScalars* sc,
-                 hipStream_t s) {
+                 hipStream_t s, bool probe) {
   const int64_t slots = n >> 2;
   int64_t blocks = ceil_div(slots > 0 ? slots : 1, (int64_t)kBlock * U);  // one trip each
   const bool large = n >= kK2LargeN;
@@ -735,25 +778,25 @@ void launch_k2_u(float* p, float* m, float* v, void* p16, const void* g, int64_t
   const dim3 grid((unsigned)blocks);
   if (g_tune.nontemporal) {
     if (drain)
-      hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, true, true>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n, sc);
+      k2_launch_one<GD, PD, U, true, true>(probe, grid, s, p, m, v, o, g, n, sc);
     else
-      hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, true, false>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n, sc);
+      k2_launch_one<GD, PD, U, true, false>(probe, grid, s, p, m, v, o, g, n, sc);
   } else {
     if (drain)
-      hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, false, true>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n, sc);
+      k2_launch_one<GD, PD, U, false, true>(probe, grid, s, p, m, v, o, g, n, sc);
     else
-      hipLaunchKernelGGL((k2_adamw_flat<GD, PD, U, false, false>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n, sc);
+      k2_launch_one<GD, PD, U, false, false>(probe, grid, s, p, m, v, o, g, n, sc);
   }
 }
 
 template <int GD, int PD>
 void launch_k2(float* p, float* m, float* v, void* p16, const void* g, int64_t n, const DsxStepScalars* sc,
-               hipStream_t s) {
+               hipStream_t s, bool probe) {
   const int unroll = g_tune.k2_unroll ? g_tune.k2_unroll : (n >= kK2LargeN ? 4 : 2);
   switch (unroll) {
-    case 2: launch_k2_u<GD, PD, 2>(p, m, v, p16, g, n, sc, s); break;
-    case 8: launch_k2_u<GD, PD, 8>(p, m, v, p16, g, n, sc, s); break;
-    default: launch_k2_u<GD, PD, 4>(p, m, v, p16, g, n, sc, s); break;
+    case 2: launch_k2_u<GD, PD, 2>(p, m, v, p16, g, n, sc, s, probe); break;
+    case 8: launch_k2_u<GD, PD, 8>(p, m, v, p16, g, n, sc, s, probe); break;
+    default: launch_k2_u<GD, PD, 4>(p, m, v, p16, g, n, sc, s, probe); break;
   }
 }
 
@@ -829,9 +872,9 @@ DsxGroupsDev one_group(const DsxAdamwHyper& hp, const double* bc, int32_t bc_len
 
 template <int GD>
 void k2_by_param(int pd, float* p, float* m, float* v, void* p16, const void* g, int64_t n,
-                 const DsxStepScalars* sc, hipStream_t s) {
-  if (pd == DSX_BF16) launch_k2<GD, DSX_BF16>(p, m, v, p16, g, n, sc, s);
-  else launch_k2<GD, DSX_F16>(p, m, v, p16, g, n, sc, s);
+                 const DsxStepScalars* sc, hipStream_t s, bool probe = false) {
+  if (pd == DSX_BF16) launch_k2<GD, DSX_BF16>(p, m, v, p16, g, n, sc, s, probe);
+  else launch_k2<GD, DSX_F16>(p, m, v, p16, g, n, sc, s, probe);
 }
 
 int do_adamw_flat(float* p, float* m, float* v, void* p16, int pdt, const void* g, int gdt, int64_t n,
@@ -1059,6 +1102,21 @@ int dsx_adamw_flat(float* master, float* exp_avg, float* exp_avg_sq, void* param
   if (!scalars) return fail(DSX_EINVAL, "null scalars");
   return do_adamw_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, scalars,
                        as_stream(stream));
+}
+
+int dsx_traffic_probe_flat(float* master, float* exp_avg, float* exp_avg_sq, void* param16, int dtype,
+                           const void* grad, int64_t n, void* stream) {
+  int rc = check_flat(master, exp_avg, exp_avg_sq, param16, dtype, grad, dtype, n);
+  if (rc) return rc;
+  if (!is16(dtype)) return fail(DSX_EINVAL, "the traffic probe takes DSX_F16 or DSX_BF16 (got %d)", dtype);
+  if (!param16) return fail(DSX_EINVAL, "the traffic probe needs param16");
+  if (n == 0) return DSX_OK;
+  hipStream_t s = as_stream(stream);
+  if (dtype == DSX_BF16)
+    k2_by_param<DSX_BF16>(DSX_BF16, master, exp_avg, exp_avg_sq, param16, grad, n, nullptr, s, true);
+  else
+    k2_by_param<DSX_F16>(DSX_F16, master, exp_avg, exp_avg_sq, param16, grad, n, nullptr, s, true);
+  return launch_status("dsx_traffic_probe_flat");
 }
 
 int dsx_zero_step_flat(float* master, float* exp_avg, float* exp_avg_sq, void* param16, int param_dtype,

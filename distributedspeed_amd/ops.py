@@ -188,6 +188,21 @@ def plan_adamw_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: tor
                   gdt, ctypes.c_int64(n), _ptr(scalars))
 
 
+def traffic_probe_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
+                       param16: torch.Tensor, grad: torch.Tensor) -> None:
+    """Measurement only: K2's traffic in K2's launch shape without the AdamW
+    math (values written back unchanged, param16 = RNE(master)); grad and
+    param16 of one 16-bit type."""
+    dev = _device(master)
+    n = master.numel()
+    for name, t in (("master", master), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
+        _need(t, name, torch.float32, n, dev)
+    _need(grad, "grad", None, n, dev)
+    _need(param16, "param16", grad.dtype, n, dev)
+    Launch("dsx_traffic_probe_flat", _ptr(master), _ptr(exp_avg), _ptr(exp_avg_sq), _ptr(param16),
+           dtype_code(param16.dtype), _ptr(grad), ctypes.c_int64(n))(_stream(dev))
+
+
 def zero_step_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
                    param16: torch.Tensor | None, grad: torch.Tensor, state: torch.Tensor,
                    scaler: DsxScalerConfig, hyper: DsxAdamwHyper, bc_table: torch.Tensor, bc_len: int,

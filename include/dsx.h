@@ -308,6 +308,18 @@ int dsx_adamw_flat(float* master, float* exp_avg, float* exp_avg_sq,
                    int grad_dtype, int64_t n, const DsxStepScalars* scalars,
                    void* stream);
 
+/* Measurement only, no counterpart in the reference: K2's exact traffic
+ * (grad, master, exp_avg and exp_avg_sq read; master, exp_avg, exp_avg_sq
+ * and param16 written: 28 B per element) in K2's launch shape for n, with
+ * the AdamW math left out. Writes back the values it reads and param16 =
+ * RNE(master), so on a partition whose param16 is the cast of its master it
+ * changes nothing. dtype is the grad and param16 type (F16 or BF16);
+ * param16 is required. Timing it beside dsx_adamw_flat tells how close K2
+ * runs to the ceiling of its own access pattern. */
+int dsx_traffic_probe_flat(float* master, float* exp_avg, float* exp_avg_sq,
+                           void* param16, int dtype, const void* grad,
+                           int64_t n, void* stream);
+
 /* K1 -> K0 -> K2 over one flat partition: the whole engine.step() of
  * Src/zero/optimizer.py:212-274 for stage 1/2 at world size 1. `partials`
  * has room for nparts doubles; `out` receives this step's scalars. */

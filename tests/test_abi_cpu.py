@@ -102,6 +102,11 @@ def test_argument_checks_reject_before_launch(lib):
     # partial count out of range
     assert lib.dsx_unscale_norm(al, 2, 16, al, al, 0, None) == EINVAL
     assert lib.dsx_unscale_norm(al, 2, 16, al, al, _lib.DSX_MAX_PARTIALS + 1, None) == EINVAL
+    # the traffic probe: 16-bit grads and params only, param16 required
+    assert lib.dsx_traffic_probe_flat(al, al, al, al, 0, al, 16, None) == EINVAL
+    assert lib.dsx_traffic_probe_flat(al, al, al, None, 2, al, 16, None) == EINVAL
+    assert lib.dsx_traffic_probe_flat(al, al, al, al + 2, 2, al, 16, None) == EINVAL
+    assert lib.dsx_traffic_probe_flat(al, al, al, al, 2, al, -1, None) == EINVAL
     # K1 folded into the hand-over copy, and the segment reduce behind it
     assert lib.dsx_copy_unscale_norm(al, al, 7, 16, al, al, 1, None) == EINVAL
     assert lib.dsx_copy_unscale_norm(al, al + 2, 2, 16, al, al, 1, None) == EINVAL

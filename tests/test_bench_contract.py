@@ -44,3 +44,5 @@ def test_bench_line_contract(gpu):
     cb = d["cpu_baseline"]
     assert cb["kind"] in ("port", "reference") and cb["cores"] >= 1 and cb["value"] > 0 and cb["sample"]
     assert d["torch_gpu_reference_path"]["foreach_ms_per_step"] > 0
+    tp = d["k2_traffic_probe"]
+    assert tp["ms"] > 0 and abs(tp["k2_over_probe"] - rf["achieved"] / tp["gbs"]) < 1e-3

@@ -460,6 +460,31 @@ def test_multi_tensor_groups(gpu, oracle):
         assert np.array_equal(torch16_to_np(tp16[i]), p16), i
 
 
+def test_traffic_probe_changes_nothing(gpu):
+    """dsx_traffic_probe_flat (K2's traffic without its math, for bench.py)
+    writes back what it reads: on a partition whose param16 is the cast of
+    its master every buffer keeps its bits, in both 16-bit types, through the
+    vector slots and the tail, in the small and the large launch shapes."""
+    import torch
+    from distributedspeed_amd import ops
+    for n, dt in ((1_000_003, torch.bfloat16), (3_000_011, torch.float16), (402_653_187, torch.bfloat16)):
+        _say(f"traffic probe n={n} {dt}")
+        gen = torch.Generator(device=gpu).manual_seed(n)
+        master = torch.randn(n, device=gpu, generator=gen)
+        m = torch.randn(n, device=gpu, generator=gen)
+        v = torch.rand(n, device=gpu, generator=gen)
+        p16 = master.to(dt)
+        g = torch.randn(n, device=gpu, generator=gen).to(dt)
+        bits = [t.view(torch.int32 if t.dtype == torch.float32 else torch.int16) for t in (master, m, v, p16, g)]
+        before = [b.clone() for b in bits]
+        ops.traffic_probe_flat(master, m, v, p16, g)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("master", "exp_avg", "exp_avg_sq", "param16", "grad"), bits, before):
+            assert torch.equal(a, b), (n, name)
+        del master, m, v, p16, g, bits, before
+        torch.cuda.empty_cache()
+
+
 def test_k2_launch_shapes_give_identical_bits(gpu, oracle):
     """Every K2 launch shape the tuning calls can select (one block per CU
     or the automatic grid -- here one trip per block --, slots per thread
