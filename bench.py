@@ -60,13 +60,14 @@ def _args():
     ap.add_argument("--pinned-budget-gib", type=float, default=32.0,
                     help="llama70b-offload: pinned host memory for the fp32 state (the shard shrinks to fit)")
     ap.add_argument("--profile-kernels", action="store_true",
-                    help="for rocprofv3 --pmc runs: launch K1, K0, K2 three times each and one 1 GiB fp32 "
-                         "copy (the byte-counter calibration), then exit without timing")
+                    help="for rocprofv3 --pmc runs: launch K1, K0, K2 and the traffic probe three times each "
+                         "and one 1 GiB fp32 copy (the byte-counter calibration), then exit without timing")
     return ap.parse_args()
 
 
 def profile_kernels(n: int, dev) -> int:
-    """Three dispatches of each kernel of the step plus a plain copy kernel of
+    """Three dispatches of each kernel of the step and of the traffic probe,
+    plus a plain copy kernel of
     known size (2^28 fp32 = 1 GiB read and 1 GiB written), so that
     FETCH_SIZE / WRITE_SIZE per dispatch can be scaled by what the counters
     report for the copy."""
@@ -83,6 +84,8 @@ def profile_kernels(n: int, dev) -> int:
         ops.unscale_norm(grad, fs.state, fs.partials, fs.nparts)
         ops.finalize(fs.partials, fs.nparts, fs.state, sc, hc, fs.bc.table, fs.bc.length, fs.scalars)
         ops.adamw_flat(master, exp_avg, exp_avg_sq, p16, grad, fs.scalars)
+    for _ in range(3):
+        ops.traffic_probe_flat(master, exp_avg, exp_avg_sq, p16, grad)
     torch.cuda.synchronize()
     del master, exp_avg, exp_avg_sq, p16, grad
     src = torch.ones(1 << 28, dtype=torch.float32, device=dev)

@@ -3,7 +3,7 @@
     python -m distributedspeed_amd.rocprof_summary \
         --trace DIR (from --kernel-trace --stats) \
         --fetch DIR (from --pmc FETCH_SIZE) --write DIR (from --pmc WRITE_SIZE) \
-        --numel N --out-md FILE --out-json FILE --command "..."
+        --numel N --out-md FILE --out-json FILE --command "..." [--title T --intro TEXT]
 
 Byte counters are scaled by what they report for a plain copy kernel of
 known size in the same run (the 1 GiB fp32 copy `bench.py --profile-kernels`
@@ -21,7 +21,7 @@ import json
 import os
 
 KERNELS = {"k2_adamw_flat": 28, "k1_unscale_norm": 2, "k0_finalize": 0, "k2_adamw_multi": 28,
-           "k1_unscale_norm_multi": 2}
+           "k1_unscale_norm_multi": 2, "k2_traffic_probe": 28}
 COPY_NAME = "__amd_rocclr_copyBuffer"
 COPY_BYTES = 1 << 30
 
@@ -103,8 +103,9 @@ def summarise(trace_dir, fetch_dir, write_dir, numel) -> dict:
     return res
 
 
-def markdown(res: dict, command: str, title: str) -> str:
-    lines = [f"# {title}", "", "Commands (run on one MI355X, from the repository root as $R):", "",
+def markdown(res: dict, command: str, title: str, intro: str = "") -> str:
+    lines = [f"# {title}", ""] + ([intro.strip(), ""] if intro.strip() else []) + [
+             "Commands (run on one MI355X, from the repository root as $R):", "",
              "```", command.strip(), "```", "",
              f"Byte-counter calibration: a {COPY_BYTES >> 20} MiB fp32 copy reads FETCH_SIZE "
              f"{res['copy_fetch_kib']:.1f} KiB and WRITE_SIZE {res['copy_write_kib']:.1f} KiB per dispatch, "
@@ -134,12 +135,13 @@ def main() -> None:
     ap.add_argument("--out-json", required=True)
     ap.add_argument("--command", default="")
     ap.add_argument("--title", default="rocprofv3 summary")
+    ap.add_argument("--intro", default="", help="a paragraph placed under the title")
     a = ap.parse_args()
     res = summarise(a.trace, a.fetch, a.write, a.numel)
     with open(a.out_json, "w") as f:
         json.dump(res, f, indent=1)
     with open(a.out_md, "w") as f:
-        f.write(markdown(res, a.command, a.title))
+        f.write(markdown(res, a.command, a.title, a.intro))
     print(json.dumps({k: res[k] for k in ("k2_hbm_bytes_per_launch", "k1_hbm_bytes_per_launch", "fetch_scale")}))
 
 
