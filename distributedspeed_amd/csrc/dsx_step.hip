@@ -84,6 +84,7 @@ bool is_grad_dtype(int dt) { return dt == DSX_F16 || dt == DSX_BF16 || dt == DSX
 constexpr int64_t kK2LargeN = int64_t(3) << 27;  // K2's large-partition shape from here on
 constexpr int64_t kMaxGridBlocks = int64_t(1) << 22;  // 2^30 work-items of kBlock threads
 constexpr int64_t kK2OneTripPerCu = 32;  // K2's one-trip grid up to this many blocks per CU
+constexpr int64_t kK3OneChunkPerCu = 20;  // K3: one chunk per block up to this many chunks per CU
 
 struct Tuning {
   int k1_blocks_per_cu = 2;
@@ -1208,12 +1209,15 @@ int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t
   if (!scalars) return fail(DSX_EINVAL, "null scalars");
   if (nchunks == 0) return DSX_OK;
   // Chunks are handed out statically (block b takes b, b + grid, ...). The
-  // default shape, from sweeps on MI355X over Llama-layout lists of 1.2e8 to
-  // 8.3e9 elements (65536-element chunks): up to 256 chunks per CU, one block
-  // per CU taking two slots per trip walks the list as one front (like K2's
+  // default shape, from sweeps on MI355X over ragged lists of 1e6 to 8.3e9
+  // elements, two slots per trip throughout: up to 20 chunks per CU, one
+  // chunk per block (all of a small list in flight at once: 1-11% faster
+  // from 2 Mi to 16 Mi elements in 4096-element chunks, 2.5% slower at 30
+  // chunks per CU); up to 256 chunks per
+  // CU, one block per CU walking the list as one front (like K2's
   // grid-stride); from 256 chunks per CU on, a grid of about four chunks per
-  // block, far more blocks than the CUs hold at once, with two slots and K2's
-  // drain, is 4-5% faster (the blocks start as others finish).
+  // block, far more blocks than the CUs hold at once, with K2's drain, is
+  // 4-5% faster (the blocks start as others finish).
   const int64_t cus = cu_count();
   int64_t bpc = g_tune.k3_blocks_per_cu;
   int unroll = g_tune.k3_unroll;
@@ -1221,7 +1225,10 @@ int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t
   if (bpc == 0) {
     const int64_t per_cu = nchunks / cus;
     const bool many = per_cu >= 256;
-    bpc = many ? per_cu / 4 : 1;
+    if (nchunks <= kK3OneChunkPerCu * cus)
+      bpc = ceil_div(nchunks, cus);  // one chunk per block
+    else
+      bpc = many ? per_cu / 4 : 1;
     unroll = 2;
     drain = g_tune.k3_drain >= 0 ? g_tune.k3_drain > 0 : many;
   }

@@ -176,9 +176,10 @@ int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll,
 int dsx_set_tuning_k2(int k2_cu_eighths, int drain);
 
 /* The same for K3 (dsx_adamw_multi): blocks per CU (the grid is also capped
- * at the chunk count; 0, the default, picks the shape from the chunk count:
- * one block per CU with 2 slots below 256 chunks per CU, about four chunks
- * per block with 2 slots and the drain from there on), slots per thread per
+ * at the chunk count; 0, the default, picks the shape from the chunk count,
+ * always with 2 slots: one chunk per block up to 20 chunks per CU, one block
+ * per CU below 256 chunks per CU, about four chunks per block with the drain
+ * from there on), slots per thread per
  * trip (1, 2 or 4; used when blocks per CU is set), the nontemporal hint and
  * K2's per-trip drain (0/1; -1, the default, as the shape decides). No
  * counterpart in the reference. */
