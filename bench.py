@@ -46,6 +46,8 @@ def _args():
     ap.add_argument("--tuning", default="",
                     help="k1_bpc,k2_bpc,k2_unroll,nt[,k2_cu_eighths,k2_drain] (library launch-shape override; "
                          "the default is 2,0,0,1,0,-1: 0 and -1 pick by size)")
+    ap.add_argument("--k2-chunk", type=int, default=None,
+                    help="K2 part size in elements (dsx_set_tuning_k2_chunk; 0: one launch; default: the library's 2^25)")
     ap.add_argument("--tuning-multi", default="",
                     help="k3_bpc,k3_unroll,nt,drain (K3 launch-shape override; k3_bpc 0 picks by chunk count)")
     ap.add_argument("--workload", default="llama8b-shard",
@@ -63,6 +65,13 @@ def _args():
                     help="for rocprofv3 --pmc runs: launch K1, K0, K2 and the traffic probe three times each "
                          "and one 1 GiB fp32 copy (the byte-counter calibration), then exit without timing")
     return ap.parse_args()
+
+
+def k2_parts(n: int, chunk) -> int:
+    """Consecutive dispatches one dsx_adamw_flat call issues over n elements
+    (the library splits K2 into parts of about 2^25 elements by default)."""
+    chunk = (1 << 25) if chunk is None else chunk
+    return -(-n // chunk) if chunk > 0 and n > chunk else 1
 
 
 def profile_kernels(n: int, dev) -> int:
@@ -686,6 +695,8 @@ def main() -> int:
             _lib.call("dsx_set_tuning_k2", vals[4], vals[5] if len(vals) > 5 else -1)
     if a.tuning_multi:
         _lib.call("dsx_set_tuning_multi", *[int(x) for x in a.tuning_multi.split(",")])
+    if a.k2_chunk is not None:
+        _lib.call("dsx_set_tuning_k2_chunk", a.k2_chunk)
     n = int(a.numel)
     if a.profile_kernels:
         return profile_kernels(n, dev)
@@ -805,7 +816,8 @@ def main() -> int:
                              "k2_over_probe": round(k2_gbs / probe_gbs, 4)},
         "roofline": {"bound": "hbm", "achieved": round(k2_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k2_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k2_adamw_flat", "algorithmic_bytes_per_launch": K2_BYTES * n},
+                     "kernel": "k2_adamw_flat", "algorithmic_bytes_per_launch": K2_BYTES * n,
+                     "dispatches_per_launch": k2_parts(n, a.k2_chunk)},
         "cpu_baseline": cpu,
         "torch_gpu_reference_path": torch_gpu,
         "wall_s_timed": round(wall, 3),

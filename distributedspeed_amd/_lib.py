@@ -78,6 +78,7 @@ SIGNATURES = {
     "dsx_set_tuning_multi": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int]),
     "dsx_set_tuning": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int]),
     "dsx_set_tuning_k2": (_c.c_int, [_c.c_int, _c.c_int]),
+    "dsx_set_tuning_k2_chunk": (_c.c_int, [_c.c_int64]),
     "dsx_copy_unscale_norm": (_c.c_int, [_P, _P, _c.c_int, _c.c_int64, _P, _P, _c.c_int32, _P]),
     "dsx_reduce_segments": (_c.c_int, [_P, _P, _c.c_int32, _P, _P]),
     "dsx_suggest_partials": (_c.c_int32, [_c.c_int64]),

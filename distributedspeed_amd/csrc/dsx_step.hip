@@ -101,6 +101,13 @@ struct Tuning {
   int k3_unroll = 1;         // slots per thread per trip in K3: 1, 2 or 4 (when not chosen)
   int k3_nontemporal = 1;
   int k3_drain = -1;         // the K2 drain in K3's slot loop (-1: as the default shape decides)
+  // K2 over a partition above this many elements runs as consecutive
+  // launches of about this many (0: one launch). One launch over a large
+  // partition loses bandwidth as it grows (1.0e9 elements: 5.52 TB/s, 4.3e9:
+  // 5.36); launches of 32 Mi elements in the mid-size shape hold 5.97-6.03
+  // TB/s from 48 Mi to 4 Gi elements (16 Mi parts lose to launch gaps, 256 Mi
+  // parts lose the gain).
+  int64_t k2_chunk_elems = int64_t(1) << 25;
 };
 Tuning g_tune;
 
@@ -878,15 +885,36 @@ void k2_by_param(int pd, float* p, float* m, float* v, void* p16, const void* g,
   else launch_k2<GD, DSX_F16>(p, m, v, p16, g, n, sc, s, probe);
 }
 
+// K2 (or its traffic probe) over n elements as consecutive launches of at
+// most ~g_tune.k2_chunk_elems elements each (equal parts, multiples of 1024
+// elements, so every part stays 16-byte aligned and only the last has a
+// tail). Each part takes the launch shape of its own size.
+void k2_dispatch(float* p, float* m, float* v, void* p16, int pdt, const void* g, int gdt, int64_t n,
+                 const DsxStepScalars* sc, hipStream_t s, bool probe) {
+  const int pd = p16 ? pdt : DSX_F16;  // pd only selects the cast when p16 != NULL
+  const int64_t want = g_tune.k2_chunk_elems;
+  int64_t part = n;
+  if (want > 0 && n > want) part = ceil_div(ceil_div(n, ceil_div(n, want)), 1024) * 1024;
+  const int64_t gsz = gdt == DSX_F32 ? 4 : 2;
+  for (int64_t a = 0; a < n; a += part) {
+    const int64_t len = n - a < part ? n - a : part;
+    float* pa = p + a;
+    float* ma = m + a;
+    float* va = v + a;
+    void* oa = p16 ? static_cast<void*>(static_cast<uint16_t*>(p16) + a) : nullptr;
+    const void* ga = static_cast<const char*>(g) + a * gsz;
+    switch (gdt) {
+      case DSX_BF16: k2_by_param<DSX_BF16>(pd, pa, ma, va, oa, ga, len, sc, s, probe); break;
+      case DSX_F16: k2_by_param<DSX_F16>(pd, pa, ma, va, oa, ga, len, sc, s, probe); break;
+      default: k2_by_param<DSX_F32>(pd, pa, ma, va, oa, ga, len, sc, s, probe); break;
+    }
+  }
+}
+
 int do_adamw_flat(float* p, float* m, float* v, void* p16, int pdt, const void* g, int gdt, int64_t n,
                   const DsxStepScalars* sc, hipStream_t s) {
   if (n == 0) return DSX_OK;
-  const int pd = p16 ? pdt : DSX_F16;  // pd only selects the cast when p16 != NULL
-  switch (gdt) {
-    case DSX_BF16: k2_by_param<DSX_BF16>(pd, p, m, v, p16, g, n, sc, s); break;
-    case DSX_F16: k2_by_param<DSX_F16>(pd, p, m, v, p16, g, n, sc, s); break;
-    default: k2_by_param<DSX_F32>(pd, p, m, v, p16, g, n, sc, s); break;
-  }
+  k2_dispatch(p, m, v, p16, pdt, g, gdt, n, sc, s, false);
   return launch_status("dsx_adamw_flat");
 }
 
@@ -950,6 +978,14 @@ int dsx_set_tuning_k2(int k2_cu_eighths, int drain) {
   if (drain < -1 || drain > 1) return fail(DSX_EINVAL, "drain must be -1 (by size), 0 or 1");
   g_tune.k2_cu_eighths = k2_cu_eighths;
   g_tune.k2_drain = drain;
+  return DSX_OK;
+}
+
+int dsx_set_tuning_k2_chunk(int64_t chunk_elems) {
+  if (chunk_elems < 0) return fail(DSX_EINVAL, "chunk_elems must be >= 0 (0: one launch)");
+  if (chunk_elems > 0 && chunk_elems < (int64_t(1) << 20))
+    return fail(DSX_EINVAL, "chunk_elems must be 0 or at least 2^20");
+  g_tune.k2_chunk_elems = chunk_elems;
   return DSX_OK;
 }
 
@@ -1112,11 +1148,7 @@ int dsx_traffic_probe_flat(float* master, float* exp_avg, float* exp_avg_sq, voi
   if (!is16(dtype)) return fail(DSX_EINVAL, "the traffic probe takes DSX_F16 or DSX_BF16 (got %d)", dtype);
   if (!param16) return fail(DSX_EINVAL, "the traffic probe needs param16");
   if (n == 0) return DSX_OK;
-  hipStream_t s = as_stream(stream);
-  if (dtype == DSX_BF16)
-    k2_by_param<DSX_BF16>(DSX_BF16, master, exp_avg, exp_avg_sq, param16, grad, n, nullptr, s, true);
-  else
-    k2_by_param<DSX_F16>(DSX_F16, master, exp_avg, exp_avg_sq, param16, grad, n, nullptr, s, true);
+  k2_dispatch(master, exp_avg, exp_avg_sq, param16, dtype, grad, dtype, n, nullptr, as_stream(stream), true);
   return launch_status("dsx_traffic_probe_flat");
 }
 

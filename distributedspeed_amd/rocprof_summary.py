@@ -70,7 +70,17 @@ def counter_per_dispatch(pmc_dir: str) -> dict:
     return dict(out)
 
 
-def summarise(trace_dir, fetch_dir, write_dir, numel) -> dict:
+# Kernels the library issues as consecutive dispatches over parts of the
+# partition (dsx_set_tuning_k2_chunk): one call of the entry point is that
+# many dispatches, and the figures below are per call.
+PARTED = ("k2_adamw_flat", "k2_traffic_probe")
+
+
+def parts_per_call(numel: int, part_elems: int) -> int:
+    return -(-numel // part_elems) if part_elems > 0 and numel > part_elems else 1
+
+
+def summarise(trace_dir, fetch_dir, write_dir, numel, part_elems: int = 1 << 25) -> dict:
     stats = kernel_stats(trace_dir)
     fetch = counter_per_dispatch(fetch_dir)
     write = counter_per_dispatch(write_dir)
@@ -79,16 +89,19 @@ def summarise(trace_dir, fetch_dir, write_dir, numel) -> dict:
     f_scale = COPY_BYTES / (f_copy * 1024)
     w_scale = COPY_BYTES / (w_copy * 1024)
     res = {"numel": int(numel), "fetch_scale": f_scale, "write_scale": w_scale,
-           "copy_fetch_kib": f_copy, "copy_write_kib": w_copy, "kernels": {}}
+           "copy_fetch_kib": f_copy, "copy_write_kib": w_copy, "part_elems": int(part_elems), "kernels": {}}
     for k, per_elt in KERNELS.items():
         if k not in fetch and k not in stats:
             continue
-        d = {}
+        parts = parts_per_call(numel, part_elems) if k in PARTED else 1
+        d = {"dispatches_per_call": parts}
         if k in stats:
-            d.update(avg_ms=stats[k]["avg_ns"] / 1e6, calls=stats[k]["calls"], pct=stats[k]["pct"])
+            # per call: the dispatches' own durations, without the gaps between them
+            d.update(avg_ms=stats[k]["avg_ns"] * parts / 1e6, avg_dispatch_ms=stats[k]["avg_ns"] / 1e6,
+                     calls=stats[k]["calls"] // parts, dispatches=stats[k]["calls"], pct=stats[k]["pct"])
         if k in fetch and k in write:
-            fb = sum(fetch[k]) / len(fetch[k]) * 1024 * f_scale
-            wb = sum(write[k]) / len(write[k]) * 1024 * w_scale
+            fb = sum(fetch[k]) / len(fetch[k]) * 1024 * f_scale * parts
+            wb = sum(write[k]) / len(write[k]) * 1024 * w_scale * parts
             d.update(fetch_bytes=fb, write_bytes=wb, hbm_bytes=fb + wb)
             if per_elt:
                 d["algorithmic_bytes"] = per_elt * numel
@@ -111,12 +124,15 @@ def markdown(res: dict, command: str, title: str, intro: str = "") -> str:
              f"{res['copy_fetch_kib']:.1f} KiB and WRITE_SIZE {res['copy_write_kib']:.1f} KiB per dispatch, "
              f"so FETCH_SIZE is scaled by {res['fetch_scale']:.4f} and WRITE_SIZE by {res['write_scale']:.4f}.", "",
              f"n = {res['numel']:,} elements.", "",
-             "| kernel | calls | avg ms | algorithmic GB | achieved GB/s | % of 8 TB/s | HBM read GB | HBM write GB | traffic / algorithmic |",
-             "|---|---|---|---|---|---|---|---|---|"]
+             "Figures are per call of the entry point; K2 and its probe issue `dispatches / call` consecutive "
+             "dispatches over parts of the partition, and `avg ms` is the sum of their durations (without the gaps "
+             "between them).", "",
+             "| kernel | calls | dispatches / call | avg ms | algorithmic GB | achieved GB/s | % of 8 TB/s | HBM read GB | HBM write GB | traffic / algorithmic |",
+             "|---|---|---|---|---|---|---|---|---|---|"]
     for k, d in res["kernels"].items():
         alg = d.get("algorithmic_bytes")
-        lines.append("| {} | {} | {} | {} | {} | {} | {} | {} | {} |".format(
-            k, d.get("calls", ""), f"{d['avg_ms']:.4f}" if "avg_ms" in d else "",
+        lines.append("| {} | {} | {} | {} | {} | {} | {} | {} | {} | {} |".format(
+            k, d.get("calls", ""), d.get("dispatches_per_call", 1), f"{d['avg_ms']:.4f}" if "avg_ms" in d else "",
             f"{alg / 1e9:.3f}" if alg else "", f"{d['achieved_gbs']:.0f}" if "achieved_gbs" in d else "",
             f"{100 * d['frac_of_8tbs']:.1f}" if "frac_of_8tbs" in d else "",
             f"{d['fetch_bytes'] / 1e9:.3f}" if "fetch_bytes" in d else "",
@@ -131,13 +147,15 @@ def main() -> None:
     ap.add_argument("--fetch", required=True)
     ap.add_argument("--write", required=True)
     ap.add_argument("--numel", type=int, required=True)
+    ap.add_argument("--part-elems", type=int, default=1 << 25,
+                    help="the library's K2 part size (dsx_set_tuning_k2_chunk; 0: one dispatch per call)")
     ap.add_argument("--out-md", required=True)
     ap.add_argument("--out-json", required=True)
     ap.add_argument("--command", default="")
     ap.add_argument("--title", default="rocprofv3 summary")
     ap.add_argument("--intro", default="", help="a paragraph placed under the title")
     a = ap.parse_args()
-    res = summarise(a.trace, a.fetch, a.write, a.numel)
+    res = summarise(a.trace, a.fetch, a.write, a.numel, a.part_elems)
     with open(a.out_json, "w") as f:
         json.dump(res, f, indent=1)
     with open(a.out_md, "w") as f:

@@ -175,6 +175,16 @@ int dsx_set_tuning(int k1_blocks_per_cu, int k2_blocks_per_cu, int k2_unroll,
  * faster with fewer requests in flight. No counterpart in the reference. */
 int dsx_set_tuning_k2(int k2_cu_eighths, int drain);
 
+/* K2 over a partition of more than chunk_elems elements runs as consecutive
+ * launches of at most about chunk_elems elements (equal parts, multiples of
+ * 1024 elements), each with the launch shape of its own size; 0 runs one
+ * launch. Default 2^25: on MI355X one launch over a large partition loses
+ * bandwidth as the partition grows, while 32 Mi-element launches hold the
+ * mid-size rate. Applies to dsx_adamw_flat, dsx_zero_step_flat and
+ * dsx_traffic_probe_flat. chunk_elems must be 0 or >= 2^20. No counterpart
+ * in the reference. */
+int dsx_set_tuning_k2_chunk(int64_t chunk_elems);
+
 /* The same for K3 (dsx_adamw_multi): blocks per CU (the grid is also capped
  * at the chunk count; 0, the default, picks the shape from the chunk count,
  * always with 2 slots: one chunk per block up to 20 chunks per CU, one block

@@ -139,6 +139,7 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.dsx_set_tuning(2, -1, 0, 1) == EINVAL and lib.dsx_set_tuning(2, 65, 0, 1) == EINVAL
     assert lib.dsx_set_tuning_k2(-1, 1) == EINVAL and lib.dsx_set_tuning_k2(9, 0) == EINVAL
     assert lib.dsx_set_tuning_k2(0, 2) == EINVAL and lib.dsx_set_tuning_k2(0, -2) == EINVAL
+    assert lib.dsx_set_tuning_k2_chunk(-1) == EINVAL and lib.dsx_set_tuning_k2_chunk(1000) == EINVAL
     assert lib.dsx_set_tuning_multi(8, 3, 0, 0) == EINVAL
     assert lib.dsx_set_tuning_multi(-1, 1, 0, 0) == EINVAL
     assert lib.dsx_set_tuning_multi(0, 1, 1, 2) == EINVAL

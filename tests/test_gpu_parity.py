@@ -485,6 +485,30 @@ def test_traffic_probe_changes_nothing(gpu):
         torch.cuda.empty_cache()
 
 
+def test_k2_in_parts_gives_identical_bits(gpu, oracle):
+    """K2 issued as consecutive launches over parts of the partition
+    (dsx_set_tuning_k2_chunk; the default splits above 2^25 elements)
+    computes the oracle's bits: parts of ~2^20 elements, the last one
+    shorter and holding the ragged tail, in both 16-bit types; one launch
+    (chunk 0) agrees too; the default is restored afterwards."""
+    from distributedspeed_amd import _lib
+    O = oracle
+    try:
+        for n, dt, chunk in ((3_000_011, BF16, 1 << 20), (2_621_443, F16, 1 << 20), (3_000_011, BF16, 0)):
+            p, m, v, g16 = make_state(n, 23, dt, 1e-3)
+            sc = O.step_scalars(O.Hyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1), 3, 1.0, 0.7)
+            rp, rm, rv, rp16 = p.copy(), m.copy(), v.copy(), np.empty(n, np.uint16)
+            O.adamw(rp, rm, rv, rp16, dt, g16, dt, sc)
+            assert _lib.call("dsx_set_tuning_k2_chunk", chunk) == 0
+            _say(f"k2 in parts n={n} dtype={dt} chunk={chunk}")
+            gp, gm, gv, gp16 = _run_k2(gpu, p, m, v, g16, dt, dt, sc)
+            for name, a, b in (("master", gp, rp), ("exp_avg", gm, rm), ("exp_avg_sq", gv, rv)):
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (name, n, chunk)
+            assert np.array_equal(gp16, rp16), (n, chunk)
+    finally:
+        _lib.call("dsx_set_tuning_k2_chunk", 1 << 25)
+
+
 def test_k2_launch_shapes_give_identical_bits(gpu, oracle):
     """Every K2 launch shape the tuning calls can select (one block per CU
     or the automatic grid -- here one trip per block --, slots per thread
