@@ -47,7 +47,7 @@ def _args():
                     help="k1_bpc,k2_bpc,k2_unroll,nt[,k2_cu_eighths,k2_drain] (library launch-shape override; "
                          "the default is 2,0,0,1,0,-1: 0 and -1 pick by size)")
     ap.add_argument("--k2-chunk", type=int, default=None,
-                    help="K2 part size in elements (dsx_set_tuning_k2_chunk; 0: one launch; default: the library's 2^25)")
+                    help="K2 part size in elements (dsx_set_tuning_k2_chunk; 0: one launch; default: the library's 2^26)")
     ap.add_argument("--tuning-multi", default="",
                     help="k3_bpc,k3_unroll,nt,drain (K3 launch-shape override; k3_bpc 0 picks by chunk count)")
     ap.add_argument("--workload", default="llama8b-shard",
@@ -69,8 +69,8 @@ def _args():
 
 def k2_parts(n: int, chunk) -> int:
     """Consecutive dispatches one dsx_adamw_flat call issues over n elements
-    (the library splits K2 into parts of about 2^25 elements by default)."""
-    chunk = (1 << 25) if chunk is None else chunk
+    (the library splits K2 into parts of about 2^26 elements by default)."""
+    chunk = (1 << 26) if chunk is None else chunk
     return -(-n // chunk) if chunk > 0 and n > chunk else 1
 
 

@@ -104,10 +104,10 @@ struct Tuning {
   // K2 over a partition above this many elements runs as consecutive
   // launches of about this many (0: one launch). One launch over a large
   // partition loses bandwidth as it grows (1.0e9 elements: 5.52 TB/s, 4.3e9:
-  // 5.36); launches of 32 Mi elements in the mid-size shape hold 5.97-6.03
-  // TB/s from 48 Mi to 4 Gi elements (16 Mi parts lose to launch gaps, 256 Mi
-  // parts lose the gain).
-  int64_t k2_chunk_elems = int64_t(1) << 25;
+  // 5.36); launches of 32-64 Mi elements in the mid-size shape hold 5.9-6.0
+  // TB/s from 64 Mi to 4 Gi elements (16 Mi parts lose to launch gaps, 256 Mi
+  // parts lose the gain; splitting below 64 Mi gains nothing).
+  int64_t k2_chunk_elems = int64_t(1) << 26;
 };
 Tuning g_tune;
 

@@ -80,7 +80,7 @@ def parts_per_call(numel: int, part_elems: int) -> int:
     return -(-numel // part_elems) if part_elems > 0 and numel > part_elems else 1
 
 
-def summarise(trace_dir, fetch_dir, write_dir, numel, part_elems: int = 1 << 25) -> dict:
+def summarise(trace_dir, fetch_dir, write_dir, numel, part_elems: int = 1 << 26) -> dict:
     stats = kernel_stats(trace_dir)
     fetch = counter_per_dispatch(fetch_dir)
     write = counter_per_dispatch(write_dir)
@@ -147,7 +147,7 @@ def main() -> None:
     ap.add_argument("--fetch", required=True)
     ap.add_argument("--write", required=True)
     ap.add_argument("--numel", type=int, required=True)
-    ap.add_argument("--part-elems", type=int, default=1 << 25,
+    ap.add_argument("--part-elems", type=int, default=1 << 26,
                     help="the library's K2 part size (dsx_set_tuning_k2_chunk; 0: one dispatch per call)")
     ap.add_argument("--out-md", required=True)
     ap.add_argument("--out-json", required=True)

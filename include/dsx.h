@@ -178,8 +178,8 @@ int dsx_set_tuning_k2(int k2_cu_eighths, int drain);
 /* K2 over a partition of more than chunk_elems elements runs as consecutive
  * launches of at most about chunk_elems elements (equal parts, multiples of
  * 1024 elements), each with the launch shape of its own size; 0 runs one
- * launch. Default 2^25: on MI355X one launch over a large partition loses
- * bandwidth as the partition grows, while 32 Mi-element launches hold the
+ * launch. Default 2^26: on MI355X one launch over a large partition loses
+ * bandwidth as the partition grows, while 64 Mi-element launches hold the
  * mid-size rate. Applies to dsx_adamw_flat, dsx_zero_step_flat and
  * dsx_traffic_probe_flat. chunk_elems must be 0 or >= 2^20. No counterpart
  * in the reference. */

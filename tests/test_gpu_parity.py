@@ -487,7 +487,7 @@ def test_traffic_probe_changes_nothing(gpu):
 
 def test_k2_in_parts_gives_identical_bits(gpu, oracle):
     """K2 issued as consecutive launches over parts of the partition
-    (dsx_set_tuning_k2_chunk; the default splits above 2^25 elements)
+    (dsx_set_tuning_k2_chunk; the default splits above 2^26 elements)
     computes the oracle's bits: parts of ~2^20 elements, the last one
     shorter and holding the ragged tail, in both 16-bit types; one launch
     (chunk 0) agrees too; the default is restored afterwards."""
@@ -506,7 +506,7 @@ def test_k2_in_parts_gives_identical_bits(gpu, oracle):
                 assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (name, n, chunk)
             assert np.array_equal(gp16, rp16), (n, chunk)
     finally:
-        _lib.call("dsx_set_tuning_k2_chunk", 1 << 25)
+        _lib.call("dsx_set_tuning_k2_chunk", 1 << 26)
 
 
 def test_k2_launch_shapes_give_identical_bits(gpu, oracle):
