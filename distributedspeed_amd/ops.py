@@ -102,14 +102,16 @@ class Launch:
     """One entry point with its arguments checked and bound once; calling it
     with a stream handle enqueues the launch. For buffers that never move
     (a flat partition) this takes the per-step host cost down to the ctypes
-    call itself."""
+    call itself. `keep` holds the tensors (or tables) whose addresses are
+    bound, so that they live as long as the launch does."""
 
-    __slots__ = ("name", "fn", "args")
+    __slots__ = ("name", "fn", "args", "keep")
 
-    def __init__(self, name: str, *args):
+    def __init__(self, name: str, *args, keep=()):
         self.name = name
         self.fn = getattr(_lib.load(), name)
         self.args = args
+        self.keep = tuple(keep)
 
     def __call__(self, stream: ctypes.c_void_p) -> None:
         rc = self.fn(*self.args, stream)
@@ -143,7 +145,7 @@ def plan_unscale_norm(grad: torch.Tensor, state: torch.Tensor, partials: torch.T
     if nparts > partials.numel():
         raise ValueError("nparts exceeds the partials buffer")
     return Launch("dsx_unscale_norm", _ptr(grad), gdt, ctypes.c_int64(grad.numel()), _ptr(state), _ptr(partials),
-                  int(nparts))
+                  int(nparts), keep=(grad, state, partials))
 
 
 def unscale_norm(grad: torch.Tensor, state: torch.Tensor, partials: torch.Tensor, nparts: int | None = None) -> None:
@@ -185,7 +187,7 @@ def plan_adamw_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: tor
         pdt = dtype_code(param16.dtype)
     _need(scalars, "scalars", torch.uint8, SCALARS_BYTES, dev, 8)
     return Launch("dsx_adamw_flat", _ptr(master), _ptr(exp_avg), _ptr(exp_avg_sq), _ptr(param16), pdt, _ptr(grad),
-                  gdt, ctypes.c_int64(n), _ptr(scalars))
+                  gdt, ctypes.c_int64(n), _ptr(scalars), keep=(master, exp_avg, exp_avg_sq, param16, grad, scalars))
 
 
 def traffic_probe_flat(master: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
@@ -266,6 +268,7 @@ class FinalizeGroups:
         _need(out, "scalars", torch.uint8, SCALARS_BYTES * ngroups, dev, 8)
         self.k = ngroups
         self.name = "dsx_finalize_groups"
+        self._keep = (partials, state, out)  # their addresses are bound below
         self.head = (_ptr(partials), int(nparts), _ptr(state))
         self.fn = getattr(_lib.load(), self.name)
         self.out = _ptr(out)
@@ -346,14 +349,16 @@ def plan_finalize_dev(partials: torch.Tensor, nparts: int, state: torch.Tensor, 
     _need(groups_dev, "groups", torch.uint8, GROUPS_BYTES, dev, 8)
     _need(out, "scalars", torch.uint8, SCALARS_BYTES * max_groups, dev, 8)
     return Launch("dsx_finalize_dev", _ptr(partials), int(nparts), _ptr(state), scaler, _ptr(groups_dev),
-                  int(max_groups), _ptr(out))
+                  int(max_groups), _ptr(out), keep=(partials, state, groups_dev, out))
 
 
 # ---- ragged lists (K3) --------------------------------------------------------------
 
 class ChunkTable:
     """Device-resident tensor and chunk tables of a ragged list (built once;
-    the tensors must stay alive and in place while the table is used).
+    the tensors must stay in place while the table is used). The table keeps
+    the state and parameter tensors alive; the grads must be alive whenever
+    a launch that reads them runs (update_grads re-points the table).
 
     masters/exp_avgs/exp_avg_sqs are fp32; grads share one dtype (fp16, bf16
     or fp32); params16 (optional) share one 16-bit dtype; groups[i] is the
@@ -398,6 +403,12 @@ class ChunkTable:
             raise RuntimeError(_lib.last_error())
         self.nchunks = int(cnt)
         self.numel = int(sum(numels))
+        # The table holds raw addresses: it keeps the state and parameter
+        # tensors alive. Not the grads: after zero_grad(set_to_none=True) the
+        # old grads must be freeable during the next backward; nothing reads
+        # them before update_grads points the table at the new ones.
+        self._held = (list(masters), list(exp_avgs), list(exp_avg_sqs),
+                      list(params16) if params16 is not None else None)
         self._refs = refs
         self._gdtype = grads[0].dtype
         self.tensors = torch.frombuffer(bytearray(bytes(refs)), dtype=torch.uint8).to(dev)
@@ -427,7 +438,7 @@ def plan_unscale_norm_multi(table: ChunkTable, state: torch.Tensor, partials: to
     if nparts > partials.numel():
         raise ValueError("nparts exceeds the partials buffer")
     return Launch("dsx_unscale_norm_multi", _ptr(table.tensors), _ptr(table.chunks), ctypes.c_int64(table.nchunks),
-                  table.gdt, _ptr(state), _ptr(partials), int(nparts))
+                  table.gdt, _ptr(state), _ptr(partials), int(nparts), keep=(table, state, partials))
 
 
 def unscale_norm_multi(table: ChunkTable, state: torch.Tensor, partials: torch.Tensor, nparts: int) -> None:
@@ -441,7 +452,7 @@ def plan_adamw_multi(table: ChunkTable, scalars: torch.Tensor) -> Launch:
     if scalars.numel() < SCALARS_BYTES * table.ngroups:
         raise ValueError(f"scalars must hold {table.ngroups} DsxStepScalars")
     return Launch("dsx_adamw_multi", _ptr(table.tensors), _ptr(table.chunks), ctypes.c_int64(table.nchunks),
-                  table.pdt, table.gdt, _ptr(scalars))
+                  table.pdt, table.gdt, _ptr(scalars), keep=(table, scalars))
 
 
 def adamw_multi(table: ChunkTable, scalars: torch.Tensor) -> None:

@@ -31,7 +31,7 @@ from typing import Iterable
 import torch
 from torch.optim import optimizer as _topt
 
-from . import ops
+from . import _lib, ops
 from ._lib import DSX_MAX_GROUPS, DsxAdamwHyper
 from .flat import FlatPartition
 from .flat_step import BiasCorrectionTable, ScalerConfig
@@ -492,18 +492,44 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
     def _plans(self):
         table = self.store.table()
         if table is not self._plans_for:  # rebuilt after storage moved: bind again
+            st = self.store
             self._k1 = ops.plan_unscale_norm_multi(table, self.dstate, self.partials, self.nparts)
-            self._k3 = ops.plan_adamw_multi(table, self.scalars)
+            k3_table = st.small_table if st.k2_tensors else table
+            self._k3 = ops.plan_adamw_multi(k3_table, self.scalars) if k3_table is not None else None
+            # K2 per large tensor: everything but the grad is bound here; the
+            # grad's address is read at each step (autograd's grads move).
+            pdt = ops.dtype_code(st.param_dtype) if st.param_dtype is not None else ops.DSX_F16
+            gdt = ops.grad_code(st.grad_dtype)
+            base = self.scalars.data_ptr()
+            self._k2_each = [(st.params[i], st.master[i].data_ptr(), st.exp_avg[i].data_ptr(),
+                              st.exp_avg_sq[i].data_ptr(),
+                              st.params[i].data.data_ptr() if st.param_dtype is not None else None,
+                              st.master[i].numel(), base + ops.SCALARS_BYTES * st.group_of[i])
+                             for i in st.k2_tensors]
+            self._k2_meta = (pdt, gdt)
             self._plans_for = table
         return self._k1, self._k3
+
+    def _k2_tensors(self, s) -> None:
+        """K2 (dsx_adamw_flat) over each large tensor of the list."""
+        if not self._k2_each:
+            return
+        fn = _lib.load().dsx_adamw_flat
+        pdt, gdt = self._k2_meta
+        for p, mp, ep, vp, pp, n, sp in self._k2_each:
+            rc = fn(mp, ep, vp, pp, pdt, p.grad.data_ptr(), gdt, n, sp, s)
+            if rc:
+                raise _lib.DsxError("dsx_adamw_flat", rc, _lib.last_error())
 
     def launch_norm(self) -> None:
         k1, _ = self._plans()
         k1(ops.stream_of(self.device))
 
     def step_fused(self) -> None:
-        """K1 (list) -> K0 -> K3 on the current stream; no host synchronisation
-        (a chunk-table rebuild, after storage moved, uploads the new table)."""
+        """K1 (list) -> K0 -> K3 on the current stream (with K2 for each large
+        tensor when the list is in K3's one-block-per-CU range); no host
+        synchronisation (a chunk-table rebuild, after storage moved, uploads
+        the new table)."""
         self._note_stepped()
         k1, k3 = self._plans()
         self.steps_issued += 1
@@ -512,7 +538,9 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
         k1(s)
         self._k0(self.scaler.to_c(), hs, tables, self._t_offsets, bc_len, s)
         self._after_finalize()
-        k3(s)
+        self._k2_tensors(s)
+        if k3 is not None:
+            k3(s)
 
 
 def adopt_torch_optimizer(opt: torch.optim.Optimizer, contiguous: bool = True, **kwargs) -> _FusedAdamWBase:

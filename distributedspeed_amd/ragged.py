@@ -21,6 +21,17 @@ import torch
 from . import ops
 
 
+# Tensors of at least this many elements step through K2 one by one (the
+# rest through K3) when the whole list would put K3 in its one-block-per-CU
+# regime (K3_SPLIT_RANGE chunks per CU). Measured on MI355X: a 12-layer Llama
+# list (2.9e9 elements, 174 chunks per CU) 15.66 -> 13.64 ms; configs[1]'s
+# GPT-2-small list (30 per CU) 0.6437 -> 0.6404 ms; configs[3]'s list (496
+# per CU, K3's many-blocks regime) is faster as one K3 launch (37.72 against
+# 38.72 ms) and stays so.
+K2_TENSOR_ELEMS = 1 << 24
+K3_SPLIT_RANGE = (20, 256)
+
+
 def auto_chunk_elems(numel: int) -> int:
     """Chunk size for a list of `numel` elements: 65536 for large lists; for
     smaller ones a power of two down to 4096, so that the list still splits
@@ -76,16 +87,22 @@ class RaggedParams:
         self.ngroups = len(groups)
         self._table = None
         self._key = None
+        self.k2_tensors: list[int] = []  # tensors the step runs through K2 (decided with each table)
+        self.small_table = None  # K3's table over the other tensors when k2_tensors is not empty
 
     def ensure_grads(self) -> None:
         """Give every param a contiguous grad of the grad dtype on the device
-        (zeros where autograd produced none, as the flat form does)."""
+        (zeros where autograd produced none, as the flat form does), 16-byte
+        aligned for the tensors of K2's size (K2 takes them one by one)."""
         for p in self.params:
             g = p.grad
             if g is None:
                 p.grad = torch.zeros_like(p, dtype=self.grad_dtype)
             elif g.dtype != self.grad_dtype or g.device != self.device or not g.is_contiguous():
                 p.grad = g.to(self.device, self.grad_dtype).contiguous()
+        for p, m in zip(self.params, self.master):
+            if m.numel() >= K2_TENSOR_ELEMS and p.grad.data_ptr() % 16:
+                p.grad = p.grad.clone()  # a fresh allocation is aligned
 
     def table(self) -> ops.ChunkTable:
         """The device chunk table for the current storage: rebuilt when a
@@ -97,6 +114,8 @@ class RaggedParams:
         if (self._table is not None and key != self._key
                 and all(a[0] == b[0] for a, b in zip(key, self._key))):
             self._table.update_grads([p.grad for p in self.params])
+            if self.small_table is not None:
+                self.small_table.update_grads([self.params[i].grad for i in self._small])
             self._key = key
         if key != self._key:
             for p, m in zip(self.params, self.master):
@@ -107,8 +126,29 @@ class RaggedParams:
             p16 = None if self.param_dtype is None else [p.data for p in self.params]
             self._table = ops.ChunkTable(self.master, self.exp_avg, self.exp_avg_sq, p16,
                                          [p.grad for p in self.params], self.group_of, self.chunk_elems)
+            self._split(p16)
             self._key = key
         return self._table
+
+    def _split(self, p16) -> None:
+        """Choose the tensors that step through K2 for the table just built,
+        and build K3's table over the rest."""
+        cus = torch.cuda.get_device_properties(self.device).multi_processor_count
+        per_cu = self._table.nchunks / cus
+        big = []
+        if K3_SPLIT_RANGE[0] <= per_cu < K3_SPLIT_RANGE[1]:
+            big = [i for i, m in enumerate(self.master) if m.numel() >= K2_TENSOR_ELEMS]
+        self.k2_tensors = big
+        taken = set(big)
+        self._small = [i for i in range(len(self.params)) if i not in taken]
+        self.small_table = None
+        if big and self._small:
+            sub = self._small
+            n_small = sum(self.master[i].numel() for i in sub)
+            self.small_table = ops.ChunkTable(
+                [self.master[i] for i in sub], [self.exp_avg[i] for i in sub], [self.exp_avg_sq[i] for i in sub],
+                None if p16 is None else [p16[i] for i in sub], [self.params[i].grad for i in sub],
+                [self.group_of[i] for i in sub], auto_chunk_elems(n_small))
 
     def zero_grad(self, set_to_none: bool = False) -> None:
         """set_to_none: p.grad = None, so the next backward's grads are read

@@ -79,6 +79,57 @@ def test_ragged_matches_flat(gpu, dtype_name):
     assert st.t == (9 if dtype == torch.float16 else 12)
 
 
+def test_ragged_large_tensors_through_k2_match_flat(gpu):
+    """A list in K3's one-block-per-CU range (here ~29 chunks per CU) steps
+    its tensors of >= 2^24 elements through K2 one by one and the rest
+    through K3: bit-identical to the flat form over four steps with fp16
+    grads, a dynamic loss scale with an overflow skip at step 2, two groups
+    and clipping; a large tensor's grad given as a misaligned view is
+    realigned (copied) before K2 reads it."""
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
+    from distributedspeed_amd.ragged import K2_TENSOR_ELEMS
+    _say("ragged: large tensors through K2")
+    shapes = [(4096, 4096), (3000, 4001), (4099,), (1024, 1023)]
+    gen = torch.Generator(device=gpu).manual_seed(31)
+    init = [torch.randn(*sh, device=gpu, generator=gen) * 0.02 for sh in shapes]
+    grads = [[(torch.randn(*sh, device=gpu, generator=gen) * 1e-3 * 1024).half() for sh in shapes] for _ in range(4)]
+    grads[1][2][7] = float("inf")
+
+    def make(cls):
+        ps = [torch.nn.Parameter(t.clone()) for t in init]
+        groups = [{"params": ps[:2]}, {"params": ps[2:], "lr": 3e-4, "weight_decay": 0.0}]
+        return ps, cls(groups, lr=1e-3, weight_decay=0.01, param_dtype=torch.float16, device=gpu, max_grad_norm=1.0,
+                       loss_scaler=ScalerConfig(mode="dynamic", init_scale=1024.0, hysteresis=1))
+
+    pf, flat = make(AdamWOptimizer)
+    pr, rag = make(MultiTensorAdamWOptimizer)
+    for step in range(4):
+        for i, (a, b) in enumerate(zip(pf, pr)):
+            a.grad = grads[step][i].clone()
+            if i == 0:
+                buf = torch.empty(grads[step][i].numel() + 8, dtype=torch.float16, device=gpu)
+                view = buf[1:1 + grads[step][i].numel()].view(shapes[0])
+                view.copy_(grads[step][i])
+                assert view.data_ptr() % 16
+                b.grad = view
+            else:
+                b.grad = grads[step][i].clone()
+        flat.step()
+        rag.step()
+        if step == 0:
+            assert rag.store.k2_tensors == [0] and K2_TENSOR_ELEMS <= shapes[0][0] * shapes[0][1]
+            assert rag.store.small_table is not None and rag.store.small_table.nchunks > 0
+    torch.cuda.synchronize()
+    assert flat.read_state().overflow_count == rag.read_state().overflow_count == 1
+    for i in range(len(shapes)):
+        vf, vr = flat.store.views_of(i), rag.store.views_of(i)
+        for name in ("master", "exp_avg", "exp_avg_sq"):
+            assert torch.equal(vf[name].view(torch.int32), vr[name].view(torch.int32)), (i, name)
+        assert torch.equal(pf[i].detach().view(torch.int16), pr[i].detach().view(torch.int16)), (i, "param16")
+
+
 def test_ragged_misaligned_grads_and_table_rebuild(gpu):
     """Grads at odd element offsets take the kernels' unaligned paths; a
     grad replaced between steps moves storage and rebuilds the table."""
@@ -163,3 +214,36 @@ def test_ragged_reads_autograd_grads_in_place_after_set_to_none(gpu):
     assert all(t is tables[1][0] for t in tables[1])  # one chunk table throughout
     _check(opts[0], opts[1], "set_to_none")
     assert opts[1].read_state().t == 4
+
+
+def test_bound_launches_keep_their_buffers_alive(gpu):
+    """A launch bound by ops.plan_* holds raw device addresses; it keeps the
+    objects behind them alive (a chunk table and, through it, the state and
+    parameter tensors; a flat partition's buffers), so a caller that drops
+    its own references cannot leave the launch pointing at freed memory. No
+    kernel runs here: only object lifetimes are checked."""
+    import gc
+    import weakref
+    import torch
+    from distributedspeed_amd import ops
+    _say("bound launches keep their buffers alive")
+    ts = [torch.zeros(n, device=gpu) for n in (1000, 4096)]
+    table = ops.ChunkTable(ts, [torch.zeros_like(t) for t in ts], [torch.zeros_like(t) for t in ts],
+                           [t.half() for t in ts], [t.half() for t in ts])
+    scalars = torch.zeros(ops.SCALARS_BYTES, dtype=torch.uint8, device=gpu)
+    k3 = ops.plan_adamw_multi(table, scalars)
+    wt, wm = weakref.ref(table), weakref.ref(ts[0])
+    del table, ts
+    gc.collect()
+    assert wt() is not None and wm() is not None
+    del k3
+    gc.collect()
+    assert wt() is None
+    p, g = torch.zeros(4096, device=gpu), torch.zeros(4096, device=gpu, dtype=torch.float16)
+    k2 = ops.plan_adamw_flat(p, torch.zeros_like(p), torch.zeros_like(p), None, g, scalars)
+    wp = weakref.ref(p)
+    del p, g
+    gc.collect()
+    assert wp() is not None
+    del k2
+
