@@ -466,8 +466,10 @@ class AdamWOptimizer(_FusedAdamWBase):
 class MultiTensorAdamWOptimizer(_FusedAdamWBase):
     """The ragged form: parameters keep their own storage and autograd's
     grads; the step runs over the tensor list through a chunk table (K1 over
-    the list, K0, K3), two streaming launches whatever the number of tensors.
-    Chosen by zero_optimization.contiguous_gradients = false."""
+    the list, K0, K3), two streaming launches whatever the number of tensors;
+    a mid-size list takes its large tensors through K2 one by one (see
+    ragged.K2_TENSOR_ELEMS). Chosen by zero_optimization.contiguous_gradients
+    = false."""
 
     def __init__(self, params: Iterable, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
                  weight_decay: float = 1e-2, *, max_grad_norm: float = 0.0, param_dtype: torch.dtype | None = None,

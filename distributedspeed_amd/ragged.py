@@ -6,7 +6,9 @@ AdamW's per-tensor loop, Src/zero/stage1.py:522-525); here every parameter
 keeps its own storage and its own autograd-allocated grad, and the step runs
 over the list through a device chunk table (dsx_unscale_norm_multi /
 dsx_adamw_multi): one launch each for the norm and the update whatever the
-number of tensors.
+number of tensors. When the list falls in K3's one-block-per-CU range, its
+tensors of at least K2_TENSOR_ELEMS elements step through K2
+(dsx_adamw_flat) one by one instead, and K3 takes the rest.
 
 Per parameter: master / exp_avg / exp_avg_sq are fp32 tensors of the
 parameter's shape owned here; with a 16-bit param dtype, param.data is the
