@@ -358,3 +358,20 @@ def test_more_than_sixteen_groups_is_refused():
     groups = [{"params": [torch.nn.Parameter(torch.zeros(2))]} for _ in range(17)]
     with pytest.raises(ValueError, match="at most 16 parameter groups"):
         AdamWOptimizer(groups)
+
+
+def test_k2_parts_per_call_follow_the_library_rule():
+    """K2 above the part size runs as ceil(n / part) consecutive dispatches
+    (dsx_set_tuning_k2_chunk; default 2^26): the rocprof summary and bench.py
+    turn per-dispatch figures into per-call ones with the same count."""
+    import os
+    import sys
+    from distributedspeed_amd.rocprof_summary import parts_per_call
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    from bench import k2_parts
+    assert parts_per_call(1003782656, 1 << 26) == 15 == k2_parts(1003782656, None)
+    assert parts_per_call(124439808, 1 << 26) == 2 == k2_parts(124439808, None)
+    assert parts_per_call(1 << 26, 1 << 26) == 1 == k2_parts(1 << 26, None)
+    assert parts_per_call(1003782656, 0) == 1 == k2_parts(1003782656, 0)
+    assert parts_per_call(1003782656, 1 << 25) == 30 == k2_parts(1003782656, 1 << 25)
+
