@@ -22,6 +22,8 @@ DSX_STATE_ERR_BC_TABLE = 1
 DSX_STATE_ERR_GROUPS = 2
 DSX_MAX_PARTIALS = 8192
 DSX_MAX_GROUPS = 16
+DSX_NOALLOC_MAX_PARTIALS = 8192
+DSX_NOALLOC_SCRATCH_BYTES = 8 * DSX_NOALLOC_MAX_PARTIALS + 256
 ABI_VERSION = 1
 
 _c = ctypes
@@ -95,6 +97,8 @@ SIGNATURES = {
     "dsx_traffic_probe_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int64, _P]),
     "dsx_zero_step_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, DsxScalerConfig,
                                       DsxAdamwHyper, _P, _c.c_int32, _P, _c.c_int32, _P, _P]),
+    "dsx_zero_step_flat_noalloc": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P,
+                                              DsxScalerConfig, DsxAdamwHyper, _P, _c.c_int32, _c.c_int32, _P, _P]),
     "dsx_unscale_norm_multi": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _P, _P, _c.c_int32, _P]),
     "dsx_adamw_multi": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _c.c_int, _P, _P]),
 }

@@ -26,6 +26,8 @@
 #include <string.h>
 #include <math.h>
 
+#include <mutex>
+
 #include "dsx.h"
 
 static_assert(sizeof(DsxState) == 64, "DsxState layout");
@@ -35,6 +37,16 @@ static_assert(sizeof(DsxStepScalars) == 64, "DsxStepScalars layout");
 static_assert(sizeof(DsxTensorRef) == 56, "DsxTensorRef layout");
 static_assert(sizeof(DsxChunk) == 24, "DsxChunk layout");
 static_assert(sizeof(DsxGroupsDev) == 1112, "DsxGroupsDev layout");
+
+// Scratch of dsx_zero_step_flat_noalloc: K1's fp64 partials, then K0's step
+// scalars. One copy per GPU, held until the process ends. Host code never
+// uses this name as an address (on the host it is a stand-in, not device
+// memory): it passes the pointer hipGetSymbolAddress returns for the current
+// device (noalloc_scratch below).
+constexpr size_t kScratchScalarsOffset = sizeof(double) * DSX_NOALLOC_MAX_PARTIALS;
+static_assert(kScratchScalarsOffset % 256 == 0, "step scalars start 256-byte aligned");
+static_assert(kScratchScalarsOffset + sizeof(DsxStepScalars) <= DSX_NOALLOC_SCRATCH_BYTES, "scratch layout");
+static __device__ __align__(256) unsigned char scratch[DSX_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -951,6 +963,60 @@ void launch_k3(int pd, int unroll, bool drain, dim3 grid, const DsxTensorRef* t,
   else launch_k3_p<GD, DSX_F16>(unroll, drain, grid, t, c, nc, sc, s);
 }
 
+// Argument checks of the flat step, shared by dsx_zero_step_flat and its
+// no-allocation variant (everything but the scratch buffers).
+int check_zero_step(const float* master, const float* m, const float* v, const void* p16, int pdt, const void* g,
+                    int gdt, int64_t n, const DsxState* state, const DsxScalerConfig& scaler,
+                    const DsxAdamwHyper& hyper, const double* bc_table, int32_t bc_len) {
+  int rc = check_flat(master, m, v, p16, pdt, g, gdt, n);
+  if (!rc) rc = check_scaler(scaler);
+  if (!rc) rc = check_hyper(hyper);
+  if (rc) return rc;
+  if (!state) return fail(DSX_EINVAL, "null state");
+  if (bc_len < 0 || (bc_len > 0 && !bc_table)) return fail(DSX_EINVAL, "bad bias-correction table");
+  return DSX_OK;
+}
+
+int zero_step_flat(float* master, float* m, float* v, void* p16, int pdt, const void* g, int gdt, int64_t n,
+                   DsxState* state, const DsxScalerConfig& scaler, const DsxAdamwHyper& hyper,
+                   const double* bc_table, int32_t bc_len, double* partials, int32_t nparts, DsxStepScalars* out,
+                   hipStream_t s) {
+  int rc = do_unscale_norm(g, gdt, n, state, partials, nparts, s);
+  if (!rc) rc = do_finalize(partials, nparts, state, scaler, one_group(hyper, bc_table, bc_len), out, s);
+  if (!rc) rc = do_adamw_flat(master, m, v, p16, pdt, g, gdt, n, out, s);
+  return rc;
+}
+
+// The address of `scratch` on the current device, resolved once per device
+// with hipGetSymbolAddress (each GPU holds its own copy at its own address)
+// and checked to be the device the stream runs on.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kMaxDevices];
+
+int noalloc_scratch(hipStream_t s, unsigned char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail((int)e, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(DSX_EINVAL, "device %d out of range [0, %d)", dev, kMaxDevices);
+  hipDevice_t sdev = -1;
+  e = hipStreamGetDevice(s, &sdev);
+  if (e != hipSuccess) return fail((int)e, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+  if ((int)sdev != dev)
+    return fail(DSX_EINVAL, "the stream belongs to device %d but device %d is current", (int)sdev, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(e != hipSuccess ? (int)e : DSX_EINVAL, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<unsigned char*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return DSX_OK;
+}
+
 }  // namespace
 
 // ---- C ABI ---------------------------------------------------------------------
@@ -1156,18 +1222,40 @@ int dsx_zero_step_flat(float* master, float* exp_avg, float* exp_avg_sq, void* p
                        const void* grad, int grad_dtype, int64_t n, DsxState* state, DsxScalerConfig scaler,
                        DsxAdamwHyper hyper, const double* bc_table, int32_t bc_len, double* partials,
                        int32_t nparts, DsxStepScalars* out, void* stream) {
-  int rc = check_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n);
+  int rc = check_zero_step(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, state, scaler,
+                           hyper, bc_table, bc_len);
   if (!rc) rc = check_parts(partials, nparts);
-  if (!rc) rc = check_scaler(scaler);
-  if (!rc) rc = check_hyper(hyper);
   if (rc) return rc;
-  if (!state || !out) return fail(DSX_EINVAL, "null state or scalars");
-  if (bc_len < 0 || (bc_len > 0 && !bc_table)) return fail(DSX_EINVAL, "bad bias-correction table");
+  if (!out) return fail(DSX_EINVAL, "null scalars");
+  return zero_step_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, state, scaler, hyper,
+                        bc_table, bc_len, partials, nparts, out, as_stream(stream));
+}
+
+int dsx_zero_step_flat_noalloc(float* master, float* exp_avg, float* exp_avg_sq, void* param16, int param_dtype,
+                               const void* grad, int grad_dtype, int64_t n, DsxState* state, DsxScalerConfig scaler,
+                               DsxAdamwHyper hyper, const double* bc_table, int32_t bc_len, int32_t nparts,
+                               DsxStepScalars* out, void* stream) {
+  int rc = check_zero_step(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, state, scaler,
+                           hyper, bc_table, bc_len);
+  if (rc) return rc;
+  if (nparts > DSX_NOALLOC_MAX_PARTIALS)
+    return fail(DSX_EINVAL, "nparts %d exceeds the library scratch of %d partials", nparts, DSX_NOALLOC_MAX_PARTIALS);
+  if (nparts < 0) return fail(DSX_EINVAL, "nparts must be >= 0 (0: the library's choice; got %d)", nparts);
+  if (nparts == 0) {
+    nparts = dsx_suggest_partials(n);
+    if (nparts < 1) nparts = 1;
+    if (nparts > DSX_NOALLOC_MAX_PARTIALS) nparts = DSX_NOALLOC_MAX_PARTIALS;
+  }
   hipStream_t s = as_stream(stream);
-  rc = do_unscale_norm(grad, grad_dtype, n, state, partials, nparts, s);
-  if (!rc) rc = do_finalize(partials, nparts, state, scaler, one_group(hyper, bc_table, bc_len), out, s);
-  if (!rc) rc = do_adamw_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, out, s);
-  return rc;
+  unsigned char* base = nullptr;
+  rc = noalloc_scratch(s, &base);
+  if (rc) return rc;
+  // Every partial K0 reads is written by this step's K1 (one per block) and
+  // every scalar K2 reads by this step's K0, so nothing needs clearing.
+  double* partials = reinterpret_cast<double*>(base);
+  DsxStepScalars* sc = out ? out : reinterpret_cast<DsxStepScalars*>(base + kScratchScalarsOffset);
+  return zero_step_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, state, scaler, hyper,
+                        bc_table, bc_len, partials, nparts, sc, s);
 }
 
 int dsx_copy_unscale_norm(const void* src, void* dst, int grad_dtype, int64_t n, const DsxState* state,

@@ -76,6 +76,11 @@ extern "C" {
 /* upper bound on the parameter groups of one dsx_finalize_groups call */
 #define DSX_MAX_GROUPS 16
 
+/* The library's own scratch per GPU (dsx_zero_step_flat_noalloc): room for
+ * DSX_NOALLOC_MAX_PARTIALS fp64 partials followed by one DsxStepScalars. */
+#define DSX_NOALLOC_MAX_PARTIALS 8192
+#define DSX_NOALLOC_SCRATCH_BYTES (8 * DSX_NOALLOC_MAX_PARTIALS + 256)
+
 /* Device-resident optimizer + loss-scaler state (64 bytes). */
 typedef struct DsxState {
   float   scale;          /* loss scale the next backward multiplies by      */
@@ -341,6 +346,29 @@ int dsx_zero_step_flat(float* master, float* exp_avg, float* exp_avg_sq,
                        const double* bc_table, int32_t bc_len,
                        double* partials, int32_t nparts, DsxStepScalars* out,
                        void* stream);
+
+/* dsx_zero_step_flat that allocates nothing and takes no scratch buffer:
+ * K1's partials and (when out is NULL) K0's step scalars live in a static
+ * device array of the library, DSX_NOALLOC_SCRATCH_BYTES per GPU, held until
+ * the process ends. No counterpart in the reference; it is for callers that
+ * cannot allocate device memory (code recorded into a HIP graph, tight
+ * serving loops, harnesses that forbid hipMalloc). The caller still passes
+ * the inputs and outputs (the flat buffers, state, bc_table; out may be NULL).
+ * nparts: 0 picks dsx_suggest_partials(n); above DSX_NOALLOC_MAX_PARTIALS is
+ * rejected with DSX_EINVAL. `stream` must belong to the current device. The
+ * first call on each device resolves the array's address
+ * (hipGetSymbolAddress), so make it outside stream capture. Calls share their
+ * GPU's array: calls that overlap on one GPU (different streams, or host
+ * threads without ordering) race. Results are bit-identical to
+ * dsx_zero_step_flat with the same nparts. */
+int dsx_zero_step_flat_noalloc(float* master, float* exp_avg,
+                               float* exp_avg_sq, void* param16,
+                               int param_dtype, const void* grad,
+                               int grad_dtype, int64_t n, DsxState* state,
+                               DsxScalerConfig scaler, DsxAdamwHyper hyper,
+                               const double* bc_table, int32_t bc_len,
+                               int32_t nparts, DsxStepScalars* out,
+                               void* stream);
 
 /* ---- K3: ragged lists (multi-tensor apply) ---------------------------- */
 

@@ -133,6 +133,16 @@ def test_argument_checks_reject_before_launch(lib):
     g.bc_table[0] = None
     assert lib.dsx_groups_upload(ctypes.byref(g), al, None) == EINVAL
     assert lib.dsx_groups_upload(ctypes.byref(g), al + 4, None) == EINVAL
+    # the no-allocation step: partial counts beyond its scratch, negative counts
+    hp = _lib.DsxAdamwHyper(1e-3, 0.9, 0.999, 1e-8, 0.0, 0.0, 1e-6)
+    assert lib.dsx_zero_step_flat_noalloc(al, al, al, al, 2, al, 2, 16, al, scfg, hp, al, 1,
+                                          _lib.DSX_NOALLOC_MAX_PARTIALS + 1, None, None) == EINVAL
+    assert b"exceeds the library scratch" in lib.dsx_last_error()
+    assert lib.dsx_zero_step_flat_noalloc(al, al, al, al, 2, al, 2, 16, al, scfg, hp, al, 1, -1, None,
+                                          None) == EINVAL
+    assert lib.dsx_zero_step_flat_noalloc(al + 4, al, al, al, 2, al, 2, 16, al, scfg, hp, al, 1, 0, None,
+                                          None) == EINVAL
+    assert b"aligned" in lib.dsx_last_error()
     # tuning validation
     assert lib.dsx_set_tuning(8, 8, 3, 1) == EINVAL
     assert lib.dsx_set_tuning(0, 8, 4, 1) == EINVAL
