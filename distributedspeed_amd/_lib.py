@@ -34,7 +34,7 @@ class DsxState(_c.Structure):
     _fields_ = [("scale", _c.c_float), ("good_steps", _c.c_int32), ("hyst_left", _c.c_int32),
                 ("t", _c.c_int32), ("iter", _c.c_int64), ("overflow_count", _c.c_int64),
                 ("error", _c.c_int32), ("last_skip", _c.c_int32), ("last_norm", _c.c_double),
-                ("reserved", _c.c_int64 * 2)]
+                ("clip_once_coef", _c.c_float), ("clip_once", _c.c_int32), ("reserved", _c.c_int64)]
 
 
 class DsxScalerConfig(_c.Structure):
@@ -88,6 +88,9 @@ SIGNATURES = {
     "dsx_build_chunks": (_c.c_int64, [_P, _c.c_int32, _c.c_int64, _P, _c.c_int64]),
     "dsx_state_init": (_c.c_int, [_P, _c.c_float, _c.c_int32, _P]),
     "dsx_unscale_norm": (_c.c_int, [_P, _c.c_int, _c.c_int64, _P, _P, _c.c_int32, _P]),
+    "dsx_norm_partials": (_c.c_int, [_P, _c.c_int, _c.c_int64, _P, _c.c_double, _P, _c.c_int32, _P]),
+    "dsx_norm_partials_multi": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _P, _c.c_double, _P, _c.c_int32, _P]),
+    "dsx_clip_prepare": (_c.c_int, [_P, _c.c_int32, _c.c_double, _c.c_double, _c.c_double, _P, _P, _P]),
     "dsx_finalize": (_c.c_int, [_P, _c.c_int32, _P, DsxScalerConfig, DsxAdamwHyper, _P, _c.c_int32, _P, _P]),
     "dsx_finalize_groups": (_c.c_int, [_P, _c.c_int32, _P, DsxScalerConfig, _P, _P, _P, _c.c_int32, _c.c_int32,
                                        _P, _P]),

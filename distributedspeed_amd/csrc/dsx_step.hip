@@ -295,6 +295,59 @@ __device__ __forceinline__ double block_sum(double x) {
   return s;
 }
 
+// ---- norms other than L2 (clip_grad_norm_'s norm_type) -----------------------
+// kNormSq: sum of x^2 (the L2 norm's square, as K1); kNormAbs: sum of |x|
+// (p = 1); kNormMax: max |x|, NaN if any x is NaN (p = inf, as
+// tensor.abs().max()); kNormPow: sum of |x|^p in fp64 (any other p > 0).
+// x is the unscaled fp32 grad; every accumulation is in fp64.
+enum NormKind { kNormSq = 0, kNormAbs = 1, kNormMax = 2, kNormPow = 3 };
+
+template <int K>
+__device__ __forceinline__ double norm_comb(double a, double b) {
+  if constexpr (K == kNormMax) return (b > a || b != b) ? b : a;  // a NaN stays (b > NaN is false)
+  else return a + b;
+}
+
+template <int K>
+__device__ __forceinline__ double norm_acc(double acc, float x, double p) {
+  if constexpr (K == kNormSq) return __builtin_fma((double)x, (double)x, acc);
+  else if constexpr (K == kNormAbs) return acc + fabs((double)x);
+  else if constexpr (K == kNormMax) return norm_comb<K>(acc, fabs((double)x));
+  else return acc + pow(fabs((double)x), p);
+}
+
+// The elements of one 16-byte slot (8 16-bit grads or 4 fp32 grads).
+template <int GD, int K>
+__device__ __forceinline__ double norm_acc16(const u4& s, float inv, double p, double acc) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if constexpr (GD == DSX_F32) {
+      acc = norm_acc<K>(acc, __uint_as_float(s[k]) * inv, p);
+    } else {
+      acc = norm_acc<K>(acc, h2f<GD>(s[k]) * inv, p);
+      acc = norm_acc<K>(acc, h2f<GD>(s[k] >> 16) * inv, p);
+    }
+  }
+  return acc;
+}
+
+// Reduce over the block with norm_comb<K>; the result is valid in thread 0.
+template <int K>
+__device__ __forceinline__ double block_reduce(double x) {
+  __shared__ double lds[kWaves];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = norm_comb<K>(x, __shfl_xor(x, off, 64));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = x;
+  __syncthreads();
+  double s = 0.0;
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s = norm_comb<K>(s, lds[w]);
+  }
+  return s;
+}
+
 __device__ __forceinline__ float inv_of(float scale) {
   // torch: GradScaler's inv_scale = scale.double().reciprocal().float();
   // the reference's static path multiplies by the Python double 1/loss_scale.
@@ -335,6 +388,97 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm(const void* __restrict
   }
   const double s = block_sum(acc);
   if (threadIdx.x == 0) partials[blockIdx.x] = s;
+}
+
+// ---- K1 for clip_grad_norm_'s norm types -----------------------------------
+// The same pass as K1 with the per-element term and the block combine of
+// NormKind K: per-block partials of sum |x|^p (or max |x|), x = f32(g) * inv.
+
+template <int GD, int K>
+__global__ __launch_bounds__(kBlock) void k1_norm(const void* __restrict__ gv, int64_t n,
+                                                  const DsxState* __restrict__ state, double p,
+                                                  double* __restrict__ partials) {
+  using G = Grad<GD>;
+  constexpr int U = 4;
+  const float inv = inv_of(state->scale);
+  const u4* g16 = static_cast<const u4*>(gv);
+  const typename G::elem* g = static_cast<const typename G::elem*>(gv);
+  const int64_t nvec = n / G::per16;
+  const int64_t stride = (int64_t)gridDim.x * kBlock * U;
+  double acc = 0.0;
+  for (int64_t i0 = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; i0 < nvec; i0 += stride) {
+    u4 S[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * kBlock;
+      S[u] = (i < nvec) ? ld<true>(g16 + i) : u4{0u, 0u, 0u, 0u};  // zeros add nothing to any kind
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc = norm_acc16<GD, K>(S[u], inv, p, acc);
+  }
+  const int64_t tail0 = nvec * G::per16;
+  const int64_t gt = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (gt < n - tail0) acc = norm_acc<K>(acc, G::one(g[tail0 + gt]) * inv, p);
+  const double s = block_reduce<K>(acc);
+  if (threadIdx.x == 0) partials[blockIdx.x] = s;
+}
+
+template <int GD, int K>
+__global__ __launch_bounds__(kBlock) void k1_norm_multi(const DsxTensorRef* __restrict__ tensors,
+                                                        const DsxChunk* __restrict__ chunks, int64_t nchunks,
+                                                        const DsxState* __restrict__ state, double p,
+                                                        double* __restrict__ partials) {
+  using G = Grad<GD>;
+  constexpr int U = 4;
+  const float inv = inv_of(state->scale);
+  double acc = 0.0;
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const DsxChunk ch = chunks[c];
+    const typename G::elem* g = static_cast<const typename G::elem*>(tensors[ch.tensor].grad) + ch.start;
+    const int64_t len = ch.len;
+    int64_t done = 0;
+    if (aligned16(g)) {
+      const u4* g16 = reinterpret_cast<const u4*>(g);
+      const int64_t nvec = len / G::per16;
+      for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += kBlock * U) {
+        u4 S[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t i = i0 + (int64_t)u * kBlock;
+          S[u] = (i < nvec) ? ld<true>(g16 + i) : u4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc = norm_acc16<GD, K>(S[u], inv, p, acc);
+      }
+      done = nvec * G::per16;
+    }
+    for (int64_t e = done + threadIdx.x; e < len; e += kBlock) acc = norm_acc<K>(acc, G::one(g[e]) * inv, p);
+  }
+  const double s = block_reduce<K>(acc);
+  if (threadIdx.x == 0) partials[blockIdx.x] = s;
+}
+
+// clip_grad_norm_'s decision, one block: the partials of NormKind K -> the
+// norm (sqrt for p = 2, total^(1/p) for other finite p, the total itself for
+// p = 1 and p = inf) into *norm_out, and the coefficient the next K0 applies
+// instead of the configured clip: max_norm / (norm + clip_eps) in double,
+// rounded to fp32, iff norm > max_norm (Src/zero/utils.py:209-214), else 1.
+template <int K>
+__global__ __launch_bounds__(kBlock) void k_clip_prepare(const double* __restrict__ partials, int32_t nparts,
+                                                         double p, double max_norm, double clip_eps,
+                                                         DsxState* __restrict__ state, double* __restrict__ norm_out) {
+  double x = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += kBlock) x = norm_comb<K>(x, partials[i]);
+  const double total = block_reduce<K>(x);
+  if (threadIdx.x != 0) return;
+  double norm = total;
+  if constexpr (K == kNormSq) norm = sqrt(total);
+  else if constexpr (K == kNormPow) norm = pow(total, 1.0 / p);
+  float coef = 1.0f;
+  if (norm > max_norm) coef = (float)(max_norm / (norm + clip_eps));
+  *norm_out = norm;
+  state->clip_once_coef = coef;
+  state->clip_once = 1;
 }
 
 // ---- K1 folded into a grad copy ---------------------------------------------------
@@ -434,12 +578,17 @@ __device__ void finalize_body(double sumsq, DsxState* __restrict__ state, const 
       }
     }
   }
+  // A coefficient armed by clip_grad_norm_ (dsx_clip_prepare) replaces the
+  // configured clip for this one step, applied or skipped, and is consumed.
   float coef = 1.0f;
-  if (ng > 0) {
+  if (ng > 0 && !skip) {
     const DsxAdamwHyper& h0 = grp.hyper[0];
-    if (!skip && h0.max_grad_norm > 0.0 && norm > h0.max_grad_norm)
+    if (s.clip_once)
+      coef = s.clip_once_coef;
+    else if (h0.max_grad_norm > 0.0 && norm > h0.max_grad_norm)
       coef = (float)(h0.max_grad_norm / (norm + h0.clip_eps));
   }
+  s.clip_once = 0;
   for (int k = 0; k < nout; ++k) {
     const bool live = k < ng;
     DsxStepScalars o = {};
@@ -963,6 +1112,43 @@ void launch_k3(int pd, int unroll, bool drain, dim3 grid, const DsxTensorRef* t,
   else launch_k3_p<GD, DSX_F16>(unroll, drain, grid, t, c, nc, sc, s);
 }
 
+int norm_kind(double p, int* kind) {
+  if (!(p > 0.0)) return fail(DSX_EINVAL, "norm_type must be > 0 (finite or inf), got %g", p);
+  *kind = __builtin_isinf(p) ? kNormMax : p == 2.0 ? kNormSq : p == 1.0 ? kNormAbs : kNormPow;
+  return DSX_OK;
+}
+
+template <int GD, int K>
+void launch_norm_k(bool multi, const void* g, int64_t n, const DsxTensorRef* t, const DsxChunk* c, int64_t nc,
+                   const DsxState* st, double p, double* partials, int nparts, hipStream_t s) {
+  const dim3 grid((unsigned)nparts), blk(kBlock);
+  if (multi)
+    hipLaunchKernelGGL((k1_norm_multi<GD, K>), grid, blk, 0, s, t, c, nc, st, p, partials);
+  else
+    hipLaunchKernelGGL((k1_norm<GD, K>), grid, blk, 0, s, g, n, st, p, partials);
+}
+
+template <int GD>
+void launch_norm(int kind, bool multi, const void* g, int64_t n, const DsxTensorRef* t, const DsxChunk* c,
+                 int64_t nc, const DsxState* st, double p, double* partials, int nparts, hipStream_t s) {
+  switch (kind) {
+    case kNormSq: launch_norm_k<GD, kNormSq>(multi, g, n, t, c, nc, st, p, partials, nparts, s); break;
+    case kNormAbs: launch_norm_k<GD, kNormAbs>(multi, g, n, t, c, nc, st, p, partials, nparts, s); break;
+    case kNormMax: launch_norm_k<GD, kNormMax>(multi, g, n, t, c, nc, st, p, partials, nparts, s); break;
+    default: launch_norm_k<GD, kNormPow>(multi, g, n, t, c, nc, st, p, partials, nparts, s); break;
+  }
+}
+
+int do_norm(int gdt, int kind, bool multi, const void* g, int64_t n, const DsxTensorRef* t, const DsxChunk* c,
+            int64_t nc, const DsxState* st, double p, double* partials, int nparts, hipStream_t s) {
+  switch (gdt) {
+    case DSX_BF16: launch_norm<DSX_BF16>(kind, multi, g, n, t, c, nc, st, p, partials, nparts, s); break;
+    case DSX_F16: launch_norm<DSX_F16>(kind, multi, g, n, t, c, nc, st, p, partials, nparts, s); break;
+    default: launch_norm<DSX_F32>(kind, multi, g, n, t, c, nc, st, p, partials, nparts, s); break;
+  }
+  return launch_status(multi ? "dsx_norm_partials_multi" : "dsx_norm_partials");
+}
+
 // Argument checks of the flat step, shared by dsx_zero_step_flat and its
 // no-allocation variant (everything but the scratch buffers).
 int check_zero_step(const float* master, const float* m, const float* v, const void* p16, int pdt, const void* g,
@@ -1129,6 +1315,68 @@ int dsx_unscale_norm(const void* grad, int grad_dtype, int64_t n, const DsxState
   int rc = check_parts(partials, nparts);
   if (rc) return rc;
   return do_unscale_norm(grad, grad_dtype, n, state, partials, nparts, as_stream(stream));
+}
+
+int dsx_norm_partials(const void* grad, int grad_dtype, int64_t n, const DsxState* state, double norm_type,
+                      double* partials, int32_t nparts, void* stream) {
+  if (!is_grad_dtype(grad_dtype))
+    return fail(DSX_EINVAL, "grad dtype must be DSX_F16, DSX_BF16 or DSX_F32 (got %d)", grad_dtype);
+  if (n < 0) return fail(DSX_EINVAL, "n must be >= 0");
+  if (n > 0 && (!grad || !aligned16(grad))) return fail(DSX_EINVAL, "grad must be non-null and 16-byte aligned");
+  if (!state) return fail(DSX_EINVAL, "null state");
+  int kind = 0;
+  int rc = norm_kind(norm_type, &kind);
+  if (!rc) rc = check_parts(partials, nparts);
+  if (rc) return rc;
+  return do_norm(grad_dtype, kind, false, grad, n, nullptr, nullptr, 0, state, norm_type, partials, nparts,
+                 as_stream(stream));
+}
+
+int dsx_norm_partials_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int grad_dtype,
+                            const DsxState* state, double norm_type, double* partials, int32_t nparts,
+                            void* stream) {
+  if (!is_grad_dtype(grad_dtype))
+    return fail(DSX_EINVAL, "grad dtype must be DSX_F16, DSX_BF16 or DSX_F32 (got %d)", grad_dtype);
+  if (nchunks < 0 || (nchunks > 0 && (!tensors || !chunks))) return fail(DSX_EINVAL, "bad chunk table");
+  if (!state) return fail(DSX_EINVAL, "null state");
+  int kind = 0;
+  int rc = norm_kind(norm_type, &kind);
+  if (!rc) rc = check_parts(partials, nparts);
+  if (rc) return rc;
+  return do_norm(grad_dtype, kind, true, nullptr, 0, tensors, chunks, nchunks, state, norm_type, partials, nparts,
+                 as_stream(stream));
+}
+
+int dsx_clip_prepare(const double* partials, int32_t nparts, double norm_type, double max_norm, double clip_eps,
+                     DsxState* state, double* norm_out, void* stream) {
+  int kind = 0;
+  int rc = norm_kind(norm_type, &kind);
+  if (!rc) rc = check_parts(partials, nparts);
+  if (rc) return rc;
+  if (!(max_norm >= 0.0)) return fail(DSX_EINVAL, "max_norm must be >= 0, got %g", max_norm);
+  if (!(clip_eps >= 0.0)) return fail(DSX_EINVAL, "Invalid clip_eps: %g", clip_eps);
+  if (!state || !norm_out) return fail(DSX_EINVAL, "null state or norm_out");
+  hipStream_t s = as_stream(stream);
+  const dim3 grid(1), blk(kBlock);
+  switch (kind) {
+    case kNormSq:
+      hipLaunchKernelGGL(k_clip_prepare<kNormSq>, grid, blk, 0, s, partials, nparts, norm_type, max_norm, clip_eps,
+                         state, norm_out);
+      break;
+    case kNormAbs:
+      hipLaunchKernelGGL(k_clip_prepare<kNormAbs>, grid, blk, 0, s, partials, nparts, norm_type, max_norm, clip_eps,
+                         state, norm_out);
+      break;
+    case kNormMax:
+      hipLaunchKernelGGL(k_clip_prepare<kNormMax>, grid, blk, 0, s, partials, nparts, norm_type, max_norm, clip_eps,
+                         state, norm_out);
+      break;
+    default:
+      hipLaunchKernelGGL(k_clip_prepare<kNormPow>, grid, blk, 0, s, partials, nparts, norm_type, max_norm, clip_eps,
+                         state, norm_out);
+      break;
+  }
+  return launch_status("dsx_clip_prepare");
 }
 
 int dsx_finalize(const double* partials, int32_t nparts, DsxState* state, DsxScalerConfig scaler,

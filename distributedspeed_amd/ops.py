@@ -153,6 +153,47 @@ def unscale_norm(grad: torch.Tensor, state: torch.Tensor, partials: torch.Tensor
     plan_unscale_norm(grad, state, partials, nparts)(_stream(grad.device))
 
 
+def norm_type_of(norm_type) -> float:
+    """clip_grad_norm_'s norm_type as a float: any p > 0 or inf (also the
+    string "inf", as torch.nn.utils.clip_grad_norm_ takes it)."""
+    try:
+        p = float(norm_type)
+    except (TypeError, ValueError):
+        raise ValueError(f"norm_type must be a number > 0 or inf, got {norm_type!r}") from None
+    if not p > 0:  # also NaN
+        raise ValueError(f"norm_type must be > 0 (finite or inf), got {norm_type!r}")
+    return p
+
+
+def plan_norm_partials(grad: torch.Tensor, state: torch.Tensor, norm_type: float, partials: torch.Tensor,
+                       nparts: int) -> Launch:
+    """K1 for a norm of type norm_type: partials[:nparts] = per-block fp64
+    sums of |grad * inv_scale|^p (maxima for p = inf)."""
+    dev = _device(grad)
+    _need(grad, "grad", None, None, dev)
+    gdt = grad_code(grad.dtype)
+    _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
+    _need(partials, "partials", torch.float64, None, dev, 8)
+    if not 1 <= nparts <= partials.numel():
+        raise ValueError("nparts must be in [1, partials.numel()]")
+    return Launch("dsx_norm_partials", _ptr(grad), gdt, ctypes.c_int64(grad.numel()), _ptr(state),
+                  ctypes.c_double(norm_type_of(norm_type)), _ptr(partials), int(nparts), keep=(grad, state, partials))
+
+
+def clip_prepare(partials: torch.Tensor, nparts: int, norm_type: float, max_norm: float, clip_eps: float,
+                 state: torch.Tensor, norm_out: torch.Tensor) -> None:
+    """The norm from plan_norm_partials' partials into norm_out (fp64, one
+    element) and the one-shot clip coefficient the next finalize applies."""
+    dev = _device(state)
+    _need(partials, "partials", torch.float64, None, dev, 8)
+    if not 1 <= nparts <= partials.numel():
+        raise ValueError("nparts must be in [1, partials.numel()]")
+    _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
+    _need(norm_out, "norm_out", torch.float64, 1, dev, 8)
+    _lib.call("dsx_clip_prepare", _ptr(partials), int(nparts), ctypes.c_double(norm_type_of(norm_type)),
+              ctypes.c_double(max_norm), ctypes.c_double(clip_eps), _ptr(state), _ptr(norm_out), _stream(dev))
+
+
 def finalize(partials: torch.Tensor, nparts: int, state: torch.Tensor, scaler: DsxScalerConfig,
              hyper: DsxAdamwHyper, bc_table: torch.Tensor, bc_len: int, out: torch.Tensor) -> None:
     """K0: norm, skip decision, clip coefficient, step scalars, scaler update."""
@@ -439,6 +480,19 @@ def plan_unscale_norm_multi(table: ChunkTable, state: torch.Tensor, partials: to
         raise ValueError("nparts exceeds the partials buffer")
     return Launch("dsx_unscale_norm_multi", _ptr(table.tensors), _ptr(table.chunks), ctypes.c_int64(table.nchunks),
                   table.gdt, _ptr(state), _ptr(partials), int(nparts), keep=(table, state, partials))
+
+
+def plan_norm_partials_multi(table: ChunkTable, state: torch.Tensor, norm_type: float, partials: torch.Tensor,
+                             nparts: int) -> Launch:
+    """plan_norm_partials over a ragged list's chunk table."""
+    dev = table.device
+    _need(state, "state", torch.uint8, STATE_BYTES, dev, 8)
+    _need(partials, "partials", torch.float64, None, dev, 8)
+    if not 1 <= nparts <= partials.numel():
+        raise ValueError("nparts must be in [1, partials.numel()]")
+    return Launch("dsx_norm_partials_multi", _ptr(table.tensors), _ptr(table.chunks), ctypes.c_int64(table.nchunks),
+                  table.gdt, _ptr(state), ctypes.c_double(norm_type_of(norm_type)), _ptr(partials), int(nparts),
+                  keep=(table, state, partials))
 
 
 def unscale_norm_multi(table: ChunkTable, state: torch.Tensor, partials: torch.Tensor, nparts: int) -> None:

@@ -222,6 +222,34 @@ class _FusedAdamWBase(torch.optim.Optimizer):
         bc_len = min(t.length for t in tabs)
         return hs, [t.table for t in tabs], bc_len
 
+    # ---- clip_grad_norm_ ---------------------------------------------------------------------
+
+    def clip_grad_norm_(self, max_norm: float, norm_type: float = 2.0) -> torch.Tensor:
+        """The reference's contract (Src/zero/optimizer.py:324-341, which the
+        stages implement at Src/zero/stage1.py:549-582 and
+        Src/zero/stage2.py:683-725, and Src/zero/utils.py:187-216): the norm of
+        type norm_type (any p > 0, or inf) of the current unscaled grads is
+        taken now, and the grads are clipped once by max_norm / (norm + 1e-6)
+        if norm > max_norm. The grads are not rewritten here: the coefficient
+        is armed in the device state and the next fused step applies it (in
+        fp32, inside K2) instead of the configured max_grad_norm; the step
+        after that clips by the configured max_grad_norm again. A skipped
+        (overflow) step consumes it too. Returns the pre-clip norm as a 0-dim
+        fp32 device tensor, with no host synchronisation."""
+        p = ops.norm_type_of(norm_type)
+        max_norm = float(max_norm)
+        if not max_norm >= 0:
+            raise ValueError(f"max_norm must be >= 0, got {max_norm}")
+        s = ops.stream_of(self.device)
+        self._norm_launch(p)(s)
+        if getattr(self, "_clip_norm", None) is None:
+            self._clip_norm = torch.zeros(1, dtype=torch.float64, device=self.device)
+        ops.clip_prepare(self.partials, self.nparts, p, max_norm, self.clip_eps, self.dstate, self._clip_norm)
+        return self._clip_norm[0].to(torch.float32)
+
+    def _norm_launch(self, p: float) -> ops.Launch:
+        raise NotImplementedError
+
     # ---- device-side values, read on demand --------------------------------------------------
 
     def refresh_master(self) -> None:
@@ -421,6 +449,10 @@ class AdamWOptimizer(_FusedAdamWBase):
         self.flat.check_grads_bound()
         self._k1(ops.stream_of(self.device))
 
+    def _norm_launch(self, p: float) -> ops.Launch:
+        self.flat.check_grads_bound()
+        return ops.plan_norm_partials(self.flat.grad, self.dstate, p, self.partials, self.nparts)
+
     def step_fused(self) -> None:
         """K1 -> K0 -> K2 on the current stream; no host synchronisation."""
         self._note_stepped()
@@ -526,6 +558,10 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
     def launch_norm(self) -> None:
         k1, _ = self._plans()
         k1(ops.stream_of(self.device))
+
+    def _norm_launch(self, p: float) -> ops.Launch:
+        self._plans()
+        return ops.plan_norm_partials_multi(self.store.table(), self.dstate, p, self.partials, self.nparts)
 
     def step_fused(self) -> None:
         """K1 (list) -> K0 -> K3 on the current stream (with K2 for each large

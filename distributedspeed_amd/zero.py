@@ -109,14 +109,14 @@ class ZeROOptimizer:
         scaled.backward(retain_graph=retain_graph)
 
     def clip_grad_norm_(self, max_norm: float, norm_type: float = 2.0) -> torch.Tensor:
-        """Sets the clipping threshold of the fused step and returns the
-        current (unscaled) grad norm as a device tensor. The reference
-        multiplies the grads in place here; the fused step applies the same
-        coefficient max_norm / (norm + 1e-6) in fp32 inside K2 instead."""
-        if norm_type != 2.0:
-            raise NotImplementedError("the fused step computes the L2 norm only")
-        self.base_optimizer.max_grad_norm = float(max_norm)
-        return self.grad_norm()
+        """Clips the current grads once, as the reference does
+        (Src/zero/optimizer.py:324-341 -> Src/zero/utils.py:187-216): the
+        norm of type norm_type (p > 0 or inf) is taken now and returned as a
+        0-dim device tensor (the pre-clip norm); if it exceeds max_norm, the
+        next fused step multiplies the grads by max_norm / (norm + 1e-6) in
+        place of the configured clip, which applies again from the step
+        after. See AdamWOptimizer.clip_grad_norm_."""
+        return self.base_optimizer.clip_grad_norm_(max_norm, norm_type)
 
     def grad_norm(self) -> torch.Tensor:
         """sqrt(sum of squared unscaled grads) of the current grads, computed

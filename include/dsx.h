@@ -92,7 +92,9 @@ typedef struct DsxState {
   int32_t error;          /* DSX_STATE_ERR_* bits, sticky                    */
   int32_t last_skip;      /* 1 if the last finalize skipped                  */
   double  last_norm;      /* global grad norm seen by the last finalize      */
-  int64_t reserved[2];
+  float   clip_once_coef; /* clip coefficient armed by dsx_clip_prepare      */
+  int32_t clip_once;      /* 1: the next finalize applies clip_once_coef     */
+  int64_t reserved;
 } DsxState;
 
 /* Loss-scaler configuration (by value). */
@@ -252,11 +254,44 @@ int dsx_copy_unscale_norm(const void* src, void* dst, int grad_dtype, int64_t n,
 int dsx_reduce_segments(const double* partials, const int64_t* offsets,
                         int32_t nseg, double* out, void* stream);
 
+/* ---- clip_grad_norm_: norms of any type, one-shot clip ---------------- */
+
+/* partials[0..nparts) = per-block fp64 partials of the norm of type
+ * norm_type over x = f32(g) * inv_scale (inv_scale as dsx_unscale_norm):
+ * sums of x^2 (norm_type 2), of |x| (1), of |x|^norm_type (any other finite
+ * norm_type > 0, pow in fp64), or maxima of |x| (norm_type = +inf; NaN if
+ * any x is NaN). norm_type must be > 0 (finite or +inf). Replaces
+ * compute_norm, Src/zero/utils.py:126-154 (inf: :141-143, p: :146-152), and
+ * the stages' p-norms, Src/zero/stage1.py:596-600, Src/zero/stage2.py:690-695. */
+int dsx_norm_partials(const void* grad, int grad_dtype, int64_t n,
+                      const DsxState* state, double norm_type, double* partials,
+                      int32_t nparts, void* stream);
+
+/* The same over the chunks of a tensor list. */
+int dsx_norm_partials_multi(const DsxTensorRef* tensors, const DsxChunk* chunks,
+                            int64_t nchunks, int grad_dtype,
+                            const DsxState* state, double norm_type,
+                            double* partials, int32_t nparts, void* stream);
+
+/* One block: the norm of type norm_type from dsx_norm_partials' partials
+ * (sqrt of the sum for 2, sum^(1/p) for other finite p, the sum for 1, the
+ * maximum for inf) into *norm_out (device double), and arms state's one-shot
+ * clip: the next finalize multiplies the grads by max_norm / (norm +
+ * clip_eps) (rounded to fp32; 1 unless norm > max_norm) instead of applying
+ * the configured max_grad_norm, whether that step is applied or skipped,
+ * and disarms it. max_norm >= 0. Replaces the in-place clip of
+ * clip_grad_norm_, Src/zero/optimizer.py:324-341 -> Src/zero/utils.py:187-216,
+ * Src/zero/stage1.py:549-582, Src/zero/stage2.py:683-725. */
+int dsx_clip_prepare(const double* partials, int32_t nparts, double norm_type,
+                     double max_norm, double clip_eps, DsxState* state,
+                     double* norm_out, void* stream);
+
 /* ---- K0: finalize ------------------------------------------------------ */
 
 /* Reduce the partials; decide skip (non-finite sum); on a clean step advance
  * t and emit the step scalars (clip coefficient max_norm/(norm+clip_eps) if
- * norm > max_norm); update the loss scaler. bc_table holds bc_len pairs
+ * norm > max_norm, or the one dsx_clip_prepare armed); update the loss
+ * scaler. bc_table holds bc_len pairs
  * {1 - beta1^t, (1 - beta2^t)^0.5} for t = 1..bc_len, computed on the host
  * in double exactly as torch/optim/adam.py:529-535 does.
  * Replaces Src/zero/optimizer.py:212-274 (skip/clip/update order),

@@ -12,7 +12,11 @@ Parts and what pins each (tests/test_oracle_*.py):
   * fp16/bf16 casts: numpy float16 and torch bfloat16 conversion over every
     16-bit pattern, every tie and a random sample.
   * norm (dsxo_sumsq): numpy float64 brute force and torch.linalg.vector_norm.
-  * clip coefficient: the closed form of Src/zero/utils.py:211-214.
+  * norms of type p (norm_p, clip_grad_norm_'s norm_type): torch's fp64
+    vector_norm, the reference's per-tensor formula restated in torch, closed
+    forms, and planted mistakes that must fail.
+  * clip coefficients: the closed form of Src/zero/utils.py:211-214, for the
+    configured clip (clip_coef) and the explicit call (clip_once_coef).
   * loss scaler (LossScalerSpec): torch._amp_update_scale_ for hysteresis=1,
     hand-derived sequences for hysteresis > 1 and min_loss_scale.
   * skip semantics: state bit-identical after a skipped step, t not advanced.
@@ -158,8 +162,52 @@ def bias_corrections(beta1: float, beta2: float, t: int) -> tuple[float, float]:
 
 
 def clip_coef(norm: float, max_norm: float, clip_eps: float = 1e-6) -> float:
-    """Src/zero/utils.py:211-214: coefficient applied iff norm > max_norm."""
+    """Src/zero/utils.py:211-214: coefficient applied iff norm > max_norm
+    (the configured max_grad_norm; 0 disables it)."""
     if max_norm > 0 and norm > max_norm:
+        return float(np.float32(max_norm / (norm + clip_eps)))
+    return 1.0
+
+
+def unscaled(g16: np.ndarray, dt: int, inv_scale: float) -> np.ndarray:
+    """f32(g) * f32(inv_scale), elementwise in fp32 (the unscale of K1/K2)."""
+    x = g16 if dt == F32 else widen16(g16, dt)
+    return (np.ascontiguousarray(x, np.float32) * np.float32(inv_scale)).astype(np.float32)
+
+
+def norm_p(g16: np.ndarray, dt: int, inv_scale: float, norm_type: float) -> float:
+    """compute_norm (Src/zero/utils.py:126-154) of the unscaled grads, exact
+    up to the final rounding: p = inf is max |x| (NaN if any x is NaN, as
+    tensor.abs().max()); p = 2 is sqrt of the exactly rounded sum of x^2;
+    other p > 0 is (sum |x|^p)^(1/p) with each |x|^p in fp64 and the sum
+    exactly rounded (math.fsum). Parity unpinned by the reference itself
+    (its arithmetic is torch's fp32 per-tensor norm); pinned here against
+    torch.linalg.vector_norm in fp64, the reference's per-tensor formula in
+    torch, and closed forms (tests/test_oracle_casts_norm.py)."""
+    p = float(norm_type)
+    if not p > 0:
+        raise ValueError(f"norm_type must be > 0 (finite or inf), got {norm_type}")
+    x = unscaled(g16, dt, inv_scale).astype(np.float64)
+    if x.size == 0:
+        return 0.0
+    a = np.abs(x)
+    if np.isnan(a).any():
+        return float("nan")
+    if math.isinf(p):
+        return float(a.max())
+    if p == 2.0:
+        return math.sqrt(math.fsum(a * a))
+    if p == 1.0:
+        return math.fsum(a)
+    with np.errstate(over="ignore"):
+        return math.fsum(a ** p) ** (1.0 / p)
+
+
+def clip_once_coef(norm: float, max_norm: float, clip_eps: float = 1e-6) -> float:
+    """The explicit clip_grad_norm_(max_norm) call, Src/zero/utils.py:209-214:
+    max_norm / (norm + clip_eps) iff norm > max_norm (no other condition:
+    max_norm = 0 zeroes the grads), applied as an fp32 scalar."""
+    if norm > max_norm:
         return float(np.float32(max_norm / (norm + clip_eps)))
     return 1.0
 
@@ -278,7 +326,10 @@ class ZeroStepOracle:
         self.t = 0
         self.overflow_count = 0
 
-    def step(self, g16: np.ndarray) -> StepResult:
+    def step(self, g16: np.ndarray, clip_once: float | None = None) -> StepResult:
+        """clip_once: the coefficient of a clip_grad_norm_ call made before
+        this step (clip_once_coef); it replaces the configured clip for this
+        step only."""
         scale = self.scaler.scale
         inv = inv_scale_of(scale)
         ss = sumsq(g16, self.gdt, inv)
@@ -289,7 +340,8 @@ class ZeroStepOracle:
             self.overflow_count += 1
         else:
             self.t += 1
-            coef = clip_coef(norm, self.h.max_grad_norm, self.h.clip_eps)
+            coef = (clip_once if clip_once is not None
+                    else clip_coef(norm, self.h.max_grad_norm, self.h.clip_eps))
             adamw(self.p, self.m, self.v, self.p16, self.pdt, g16, self.gdt,
                   step_scalars(self.h, self.t, inv, coef))
         self.scaler.update(found_inf)

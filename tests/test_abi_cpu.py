@@ -143,6 +143,17 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.dsx_zero_step_flat_noalloc(al + 4, al, al, al, 2, al, 2, 16, al, scfg, hp, al, 1, 0, None,
                                           None) == EINVAL
     assert b"aligned" in lib.dsx_last_error()
+    # norms of other types and the one-shot clip: norm_type > 0 (or inf), max_norm >= 0
+    for bad in (0.0, -2.0, float("nan"), float("-inf")):
+        assert lib.dsx_norm_partials(al, 2, 16, al, bad, al, 1, None) == EINVAL
+        assert b"norm_type" in lib.dsx_last_error()
+        assert lib.dsx_norm_partials_multi(al, al, 1, 2, al, bad, al, 1, None) == EINVAL
+        assert lib.dsx_clip_prepare(al, 1, bad, 1.0, 1e-6, al, al, None) == EINVAL
+    assert lib.dsx_norm_partials(al + 2, 2, 16, al, 3.0, al, 1, None) == EINVAL
+    assert lib.dsx_norm_partials(al, 2, 16, al, 3.0, al, _lib.DSX_MAX_PARTIALS + 1, None) == EINVAL
+    assert lib.dsx_clip_prepare(al, 1, 2.0, -1.0, 1e-6, al, al, None) == EINVAL
+    assert b"max_norm" in lib.dsx_last_error()
+    assert lib.dsx_clip_prepare(al, 1, 2.0, 1.0, 1e-6, al, None, None) == EINVAL
     # tuning validation
     assert lib.dsx_set_tuning(8, 8, 3, 1) == EINVAL
     assert lib.dsx_set_tuning(0, 8, 4, 1) == EINVAL

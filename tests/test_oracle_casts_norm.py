@@ -142,3 +142,102 @@ def test_clip_coefficient_closed_form(oracle):
     g = np.array([3.0, 4.0], np.float32)
     c = np.float32(oracle.clip_coef(5.0, 1.0))
     assert float(np.linalg.norm((g * c).astype(np.float64))) == pytest.approx(5.0 / (5.0 + 1e-6), rel=1e-7)
+
+
+# ---- clip_grad_norm_'s norm types (Src/zero/utils.py:126-154) ----------------------------
+
+NORM_TYPES = [1.0, 2.0, 3.0, 0.5, 7.5, math.inf]
+
+
+def _grads(oracle, n, dt, seed, scale):
+    rng = np.random.default_rng(seed)
+    g = (rng.standard_normal(n) * 1e-3 * scale).astype(np.float32)
+    return g if dt == 0 else oracle.cast16(g, dt)
+
+
+@pytest.mark.parametrize("p", NORM_TYPES)
+@pytest.mark.parametrize("dt", [0, 1, 2])
+def test_norm_p_against_torch_fp64(oracle, dt, p):
+    """norm_p equals torch.linalg.vector_norm(ord=p) in fp64 over the same
+    unscaled fp32 values (inf exactly: a maximum has no rounding)."""
+    scale = 2.0 ** 10 if dt == 1 else 1.0
+    g = _grads(oracle, 100_003, dt, 11 + dt, scale)
+    inv = oracle.inv_scale_of(scale)
+    x = oracle.unscaled(g, dt, inv)
+    ref = float(torch.linalg.vector_norm(torch.from_numpy(x).double(), ord=p))
+    got = oracle.norm_p(g, dt, inv, p)
+    if math.isinf(p):
+        assert got == ref
+    else:
+        assert got == pytest.approx(ref, rel=1e-13)
+
+
+@pytest.mark.parametrize("p", NORM_TYPES)
+def test_norm_p_against_the_reference_formula(oracle, p):
+    """The reference's compute_norm restated with torch (Src/zero/utils.py:
+    141-152): per tensor t.norm(p, dtype=float32).item() ** p summed in
+    Python, then ** (1/p); for inf the max of t.abs().max(). torch
+    accumulates each tensor in fp32, so agreement is to fp32 accuracy."""
+    x = oracle.unscaled(_grads(oracle, 300_007, 2, 3, 1.0), 2, 1.0)
+    pieces = [torch.from_numpy(c.copy()) for c in np.array_split(x, 7)]
+    if math.isinf(p):
+        ref = max(t.abs().max().item() for t in pieces)
+        assert oracle.norm_p(oracle.cast16(x, 2), 2, 1.0, p) == ref
+        return
+    total = 0.0
+    for t in pieces:
+        total += (t.norm(dtype=torch.float32).item() ** 2 if p == 2.0
+                  else t.norm(p=p, dtype=torch.float32).item() ** p)
+    ref = total ** (1.0 / p)
+    # the fp32 sums' relative error is multiplied by 1/p in the root
+    assert oracle.norm_p(oracle.cast16(x, 2), 2, 1.0, p) == pytest.approx(ref, rel=2e-5 * max(1.0, 1.0 / p))
+
+
+@pytest.mark.parametrize("p", NORM_TYPES)
+def test_norm_p_closed_forms(oracle, p):
+    """n equal magnitudes c of mixed sign: n^(1/p) * c (c for inf); a single
+    nonzero element: its magnitude for every p; an inf anywhere: inf; a NaN
+    anywhere: NaN; no elements or all zeros: 0."""
+    n, c = 4096, np.float32(0.375)
+    x = np.full(n, c, np.float32)
+    x[::3] = -c
+    want = float(c) if math.isinf(p) else n ** (1.0 / p) * float(c)
+    assert oracle.norm_p(x, 0, 1.0, p) == pytest.approx(want, rel=1e-14)
+    one = np.zeros(1000, np.float32)
+    one[617] = -2.5
+    assert oracle.norm_p(one, 0, 1.0, p) == pytest.approx(2.5, rel=1e-15)
+    for bad, want_nan in ((np.inf, False), (-np.inf, False), (np.nan, True)):
+        y = x.copy()
+        y[100] = bad
+        r = oracle.norm_p(y, 0, 1.0, p)
+        assert math.isnan(r) if want_nan else r == math.inf
+    assert oracle.norm_p(np.zeros(0, np.float32), 0, 1.0, p) == 0.0
+    assert oracle.norm_p(np.zeros(77, np.float32), 0, 1.0, p) == 0.0
+
+
+def test_norm_p_planted_mistakes_fail_the_pins(oracle):
+    """Variants of norm_p with a plausible mistake -- no absolute value for an
+    odd p, the loss scale not removed, 1/p not applied -- miss torch's fp64
+    norm by far more than the 1e-13 the real one meets."""
+    scale = 2.0 ** 10
+    g = _grads(oracle, 50_001, 1, 4, scale)
+    inv = oracle.inv_scale_of(scale)
+    x = oracle.unscaled(g, 1, inv).astype(np.float64)
+    ref = float(torch.linalg.vector_norm(torch.from_numpy(x), ord=3.0))
+    assert oracle.norm_p(g, 1, inv, 3.0) == pytest.approx(ref, rel=1e-13)
+    no_abs = abs(math.fsum(x ** 3)) ** (1 / 3)
+    scaled = math.fsum(np.abs(oracle.widen16(g, 1).astype(np.float64)) ** 3) ** (1 / 3)
+    no_root = math.fsum(np.abs(x) ** 3)
+    for bad in (no_abs, scaled, no_root):
+        assert abs(bad - ref) > 1e-3 * ref
+
+
+def test_clip_once_coefficient_closed_form(oracle):
+    """The explicit call clips iff norm > max_norm, with no max_norm > 0
+    condition (Src/zero/utils.py:209-214): max_norm = 0 gives coefficient 0."""
+    assert oracle.clip_once_coef(0.5, 1.0) == 1.0
+    assert oracle.clip_once_coef(1.0, 1.0) == 1.0
+    assert oracle.clip_once_coef(4.0, 1.0) == float(np.float32(1.0 / (4.0 + 1e-6)))
+    assert oracle.clip_once_coef(4.0, 0.0) == 0.0
+    assert oracle.clip_once_coef(math.inf, 1.0) == 0.0
+    assert oracle.clip_once_coef(math.nan, 1.0) == 1.0  # NaN > max is false, as in Python
