@@ -69,8 +69,15 @@ class DsxGroupsDev(_c.Structure):
                 ("ngroups", _c.c_int32), ("bc_len", _c.c_int32), ("reserved", _c.c_int64 * 2)]
 
 
+class DsxFlatPlan(_c.Structure):
+    _fields_ = [("master", _P), ("exp_avg", _P), ("exp_avg_sq", _P), ("param16", _P), ("grad", _P),
+                ("n", _c.c_int64), ("param_dtype", _c.c_int32), ("grad_dtype", _c.c_int32), ("state", _P),
+                ("partials", _P), ("out", _P), ("nparts", _c.c_int32), ("ngroups", _c.c_int32),
+                ("scaler", DsxScalerConfig), ("group_end", _c.c_int64 * 16)]
+
+
 for _s, _n in ((DsxState, 64), (DsxScalerConfig, 32), (DsxAdamwHyper, 56), (DsxStepScalars, 64),
-               (DsxTensorRef, 56), (DsxChunk, 24), (DsxGroupsDev, 1112)):
+               (DsxTensorRef, 56), (DsxChunk, 24), (DsxGroupsDev, 1112), (DsxFlatPlan, 248)):
     assert _c.sizeof(_s) == _n, (_s.__name__, _c.sizeof(_s))
 
 # name -> (restype, argtypes); every symbol include/dsx.h declares.
@@ -100,6 +107,7 @@ SIGNATURES = {
     "dsx_traffic_probe_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int64, _P]),
     "dsx_zero_step_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, DsxScalerConfig,
                                       DsxAdamwHyper, _P, _c.c_int32, _P, _c.c_int32, _P, _P]),
+    "dsx_zero_step_plan": (_c.c_int, [_P, _P, _P]),
     "dsx_zero_step_flat_noalloc": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P,
                                               DsxScalerConfig, DsxAdamwHyper, _P, _c.c_int32, _c.c_int32, _P, _P]),
     "dsx_unscale_norm_multi": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _P, _P, _c.c_int32, _P]),

@@ -37,6 +37,7 @@ static_assert(sizeof(DsxStepScalars) == 64, "DsxStepScalars layout");
 static_assert(sizeof(DsxTensorRef) == 56, "DsxTensorRef layout");
 static_assert(sizeof(DsxChunk) == 24, "DsxChunk layout");
 static_assert(sizeof(DsxGroupsDev) == 1112, "DsxGroupsDev layout");
+static_assert(sizeof(DsxFlatPlan) == 248, "DsxFlatPlan layout");
 
 // Scratch of dsx_zero_step_flat_noalloc: K1's fp64 partials, then K0's step
 // scalars. One copy per GPU, held until the process ends. Host code never
@@ -1477,6 +1478,49 @@ int dsx_zero_step_flat(float* master, float* exp_avg, float* exp_avg_sq, void* p
   if (!out) return fail(DSX_EINVAL, "null scalars");
   return zero_step_flat(master, exp_avg, exp_avg_sq, param16, param_dtype, grad, grad_dtype, n, state, scaler, hyper,
                         bc_table, bc_len, partials, nparts, out, as_stream(stream));
+}
+
+int dsx_zero_step_plan(const DsxFlatPlan* plan, const DsxGroupsDev* groups, void* stream) {
+  if (!plan || !groups) return fail(DSX_EINVAL, "null plan or groups");
+  const DsxFlatPlan& P = *plan;
+  const DsxGroupsDev& G = *groups;
+  int rc = check_flat(P.master, P.exp_avg, P.exp_avg_sq, P.param16, P.param_dtype, P.grad, P.grad_dtype, P.n);
+  if (!rc) rc = check_parts(P.partials, P.nparts);
+  if (!rc) rc = check_scaler(P.scaler);
+  if (rc) return rc;
+  if (!P.state || !P.out) return fail(DSX_EINVAL, "null state or scalars");
+  if (P.ngroups < 1 || P.ngroups > DSX_MAX_GROUPS)
+    return fail(DSX_EINVAL, "ngroups must be in [1, %d] (got %d)", DSX_MAX_GROUPS, P.ngroups);
+  if (G.ngroups != P.ngroups)
+    return fail(DSX_EINVAL, "the group block holds %d groups, the plan %d", G.ngroups, P.ngroups);
+  if (G.bc_len < 0) return fail(DSX_EINVAL, "bad bias-correction table length");
+  int64_t prev = 0;
+  for (int k = 0; k < P.ngroups; ++k) {
+    rc = check_hyper(G.hyper[k]);
+    if (rc) return rc;
+    if (G.bc_len > 0 && !G.bc_table[k]) return fail(DSX_EINVAL, "null bias-correction table for group %d", k);
+    if (G.t_offset[k] < 0) return fail(DSX_EINVAL, "negative t_offset for group %d", k);
+    const int64_t end = P.group_end[k];
+    const bool last = k == P.ngroups - 1;
+    if (end < prev || end > P.n || (last ? end != P.n : (end & 7) != 0))
+      return fail(DSX_EINVAL, "group_end[%d] = %lld: boundaries must be nondecreasing multiples of 8 ending at n",
+                  k, (long long)end);
+    prev = end;
+  }
+  hipStream_t s = as_stream(stream);
+  rc = do_unscale_norm(P.grad, P.grad_dtype, P.n, P.state, P.partials, P.nparts, s);
+  if (!rc) rc = do_finalize(P.partials, P.nparts, P.state, P.scaler, G, P.out, s);
+  const int64_t gsz = P.grad_dtype == DSX_F32 ? 4 : 2;
+  prev = 0;
+  for (int k = 0; !rc && k < P.ngroups; ++k) {
+    const int64_t a = prev, b = P.group_end[k];
+    prev = b;
+    if (b == a) continue;
+    void* p16 = P.param16 ? static_cast<void*>(static_cast<uint16_t*>(P.param16) + a) : nullptr;
+    rc = do_adamw_flat(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype,
+                       static_cast<const char*>(P.grad) + a * gsz, P.grad_dtype, b - a, P.out + k, s);
+  }
+  return rc;
 }
 
 int dsx_zero_step_flat_noalloc(float* master, float* exp_avg, float* exp_avg_sq, void* param16, int param_dtype,

@@ -24,6 +24,7 @@ device memory; see graph.py).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from itertools import chain
 from typing import Iterable
@@ -392,6 +393,11 @@ class AdamWOptimizer(_FusedAdamWBase):
                     sc = self.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
                     self._k2.append(ops.plan_adamw_flat(master, m, v, p16, g, sc))
         self.capturable = bool(capturable)
+        # The eager step as one C call (dsx_zero_step_plan: K1, K0 and each
+        # group's K2), with its fixed arguments packed here once.
+        self._plan = None
+        if self.streamer is None and not self.use_graph and not self.capturable:
+            self._build_plan()
         # K1 folded into the hooks' copies (eager form only: a captured or
         # graph-replayed step keeps its K1).
         self._k0_hook = None
@@ -409,6 +415,54 @@ class AdamWOptimizer(_FusedAdamWBase):
 
     def _grads_may_move(self) -> bool:
         return not self.capturable
+
+    # ---- the eager step in one call ------------------------------------------------------
+
+    def _build_plan(self) -> None:
+        f = self.flat
+        P = _lib.DsxFlatPlan()
+        P.master, P.exp_avg, P.exp_avg_sq = f.master.data_ptr(), f.exp_avg.data_ptr(), f.exp_avg_sq.data_ptr()
+        P.param16 = f.param16.data_ptr() if f.param16 is not None else None
+        P.grad = f.grad.data_ptr()
+        P.n = f.numel
+        P.param_dtype = ops.dtype_code(f.param16.dtype) if f.param16 is not None else _lib.DSX_F16
+        P.grad_dtype = ops.grad_code(f.grad.dtype)
+        P.state, P.partials, P.out = self.dstate.data_ptr(), self.partials.data_ptr(), self.scalars.data_ptr()
+        P.nparts, P.ngroups = self.nparts, len(self.param_groups)
+        for k, (_, b) in enumerate(f.group_ranges):
+            P.group_end[k] = b
+        self._plan = P
+        self._gblock = _lib.DsxGroupsDev()
+        self._gkey = None  # what the group block was last filled from
+        self._skey = None  # the scaler settings packed into the plan
+        self._plan_fn = _lib.load().dsx_zero_step_plan
+        self._plan_args = (ctypes.byref(P), ctypes.byref(self._gblock))
+
+    def _step_plan(self) -> None:
+        """K1 -> K0 -> K2 through dsx_zero_step_plan. The group block (the
+        per-group hyper-parameters and bias tables) is refilled only when a
+        value in param_groups or max_grad_norm changed, or the bias tables
+        must grow; the scaler settings only when they changed."""
+        key = (tuple((float(g["lr"]), g["betas"], g["eps"], g["weight_decay"]) for g in self.param_groups),
+               self.max_grad_norm, self.clip_eps)
+        if key != self._gkey or self.steps_issued > self._gblock.bc_len:
+            hs, tables, bc_len = self._hypers()
+            blk = self._gblock
+            for k, h in enumerate(hs):
+                blk.hyper[k] = h
+                blk.bc_table[k] = tables[k].data_ptr()
+                blk.t_offset[k] = self._t_offsets[k]
+            blk.ngroups, blk.bc_len = len(hs), bc_len
+            self._gtables = tables  # the block holds their addresses
+            self._gkey = key
+        sc = self.scaler
+        skey = (sc.mode, sc.window, sc.hysteresis, sc.min_scale, sc.growth_factor, sc.backoff_factor)
+        if skey != self._skey:
+            self._plan.scaler = sc.to_c()
+            self._skey = skey
+        rc = self._plan_fn(*self._plan_args, ops.stream_of(self.device))
+        if rc:
+            raise _lib.DsxError("dsx_zero_step_plan", rc, _lib.last_error())
 
     # ---- capturable form ----------------------------------------------------------------
 
@@ -461,6 +515,13 @@ class AdamWOptimizer(_FusedAdamWBase):
             return
         self.flat.check_grads_bound()
         self.steps_issued += 1
+        if (self._plan is not None and self._skip_host is None
+                and not (self._k0_hook is not None and self.flat.hook_norm_ready())):
+            # one C call; with track_skips on, the three launches are issued
+            # one by one so that the skip flag's copy sits between K0 and K2
+            self._step_plan()
+            self.flat.disarm_hook_norm()
+            return
         hs, tables, bc_len = self._hypers()
         if self.use_graph:
             # Captured once (first step), replayed after uploading this step's

@@ -139,7 +139,14 @@ class RaggedParams:
         per_cu = self._table.nchunks / cus
         big = []
         if K3_SPLIT_RANGE[0] <= per_cu < K3_SPLIT_RANGE[1]:
-            big = [i for i, m in enumerate(self.master) if m.numel() >= K2_TENSOR_ELEMS]
+            # K2 needs every array 16-byte aligned. master / exp_avg / exp_avg_sq
+            # are allocated here and ensure_grads realigns a large tensor's grad
+            # before each step, but param.data may have been replaced by a
+            # misaligned view: such a tensor stays in K3's table, whose scalar
+            # loop takes any address.
+            big = [i for i, m in enumerate(self.master) if m.numel() >= K2_TENSOR_ELEMS
+                   and all(t.data_ptr() % 16 == 0 for t in (m, self.exp_avg[i], self.exp_avg_sq[i]))
+                   and (p16 is None or p16[i].data_ptr() % 16 == 0)]
         self.k2_tensors = big
         taken = set(big)
         self._small = [i for i in range(len(self.params)) if i not in taken]

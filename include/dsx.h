@@ -382,6 +382,37 @@ int dsx_zero_step_flat(float* master, float* exp_avg, float* exp_avg_sq,
                        double* partials, int32_t nparts, DsxStepScalars* out,
                        void* stream);
 
+/* What a flat partition's step needs that stays fixed from step to step
+ * (the drop-in optimizer builds it once). Parameter group g covers elements
+ * [group_end[g-1], group_end[g]) (group_end[-1] = 0): every boundary but the
+ * last a multiple of 8 elements, the last equal to n. */
+typedef struct DsxFlatPlan {
+  float*          master;
+  float*          exp_avg;
+  float*          exp_avg_sq;
+  void*           param16;      /* may be NULL                              */
+  const void*     grad;
+  int64_t         n;
+  int32_t         param_dtype;
+  int32_t         grad_dtype;
+  DsxState*       state;
+  double*         partials;     /* nparts doubles                           */
+  DsxStepScalars* out;          /* ngroups entries                          */
+  int32_t         nparts;
+  int32_t         ngroups;
+  DsxScalerConfig scaler;
+  int64_t         group_end[DSX_MAX_GROUPS];
+} DsxFlatPlan;
+
+/* K1 -> K0 -> K2 (one K2 call per non-empty group range) in one call: the
+ * whole step of the flat drop-in optimizer with parameter groups. plan and
+ * groups are HOST structs (groups holds this step's hyper-parameters, bias
+ * tables and t offsets, as dsx_finalize_groups takes them); both are checked
+ * at every call. Replaces ZeROOptimizer.step, Src/zero/optimizer.py:212-274,
+ * with torch AdamW's per-group loop behind Src/zero/stage2.py:609-612. */
+int dsx_zero_step_plan(const DsxFlatPlan* plan /* host */,
+                       const DsxGroupsDev* groups /* host */, void* stream);
+
 /* dsx_zero_step_flat that allocates nothing and takes no scratch buffer:
  * K1's partials and (when out is NULL) K0's step scalars live in a static
  * device array of the library, DSX_NOALLOC_SCRATCH_BYTES per GPU, held until

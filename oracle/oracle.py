@@ -180,8 +180,8 @@ def norm_p(g16: np.ndarray, dt: int, inv_scale: float, norm_type: float) -> floa
     up to the final rounding: p = inf is max |x| (NaN if any x is NaN, as
     tensor.abs().max()); p = 2 is sqrt of the exactly rounded sum of x^2;
     other p > 0 is (sum |x|^p)^(1/p) with each |x|^p in fp64 and the sum
-    exactly rounded (math.fsum). Parity unpinned by the reference itself
-    (its arithmetic is torch's fp32 per-tensor norm); pinned here against
+    exactly rounded (math.fsum). The reference holds no vectors for it (its
+    arithmetic is torch's fp32 per-tensor norm); it is pinned against
     torch.linalg.vector_norm in fp64, the reference's per-tensor formula in
     torch, and closed forms (tests/test_oracle_casts_norm.py)."""
     p = float(norm_type)
@@ -316,13 +316,22 @@ class StepResult:
 class ZeroStepOracle:
     """ZeROOptimizer.step (Src/zero/optimizer.py:212-274) over one flat
     partition, in the order: overflow check / skip -> unscale -> norm -> clip
-    -> AdamW -> cast -> scaler update. Arrays are updated in place."""
+    -> AdamW -> cast -> scaler update. Arrays are updated in place.
+
+    groups: optional [(start, end, Hyper)] ranges of the partition with their
+    own hyper-parameters (torch param_groups stepped by one optimizer): the
+    norm, skip decision and clip coefficient stay global, the clip threshold
+    is `hyper`'s. blocked_norm: take the norm as sumsq(..., blocks=1024) on
+    all cores (sumsq_parallel, the same bits) -- for partitions of billions
+    of elements."""
 
     def __init__(self, master: np.ndarray, exp_avg: np.ndarray, exp_avg_sq: np.ndarray,
                  p16: np.ndarray | None, pdt: int, gdt: int, hyper: Hyper,
-                 scaler: LossScalerSpec):
+                 scaler: LossScalerSpec, groups: list | None = None, blocked_norm: bool = False):
         self.p, self.m, self.v, self.p16 = master, exp_avg, exp_avg_sq, p16
         self.pdt, self.gdt, self.h, self.scaler = pdt, gdt, hyper, scaler
+        self.groups = list(groups) if groups else [(0, master.size, hyper)]
+        self.blocked_norm = blocked_norm
         self.t = 0
         self.overflow_count = 0
 
@@ -332,7 +341,7 @@ class ZeroStepOracle:
         step only."""
         scale = self.scaler.scale
         inv = inv_scale_of(scale)
-        ss = sumsq(g16, self.gdt, inv)
+        ss = sumsq_parallel(g16, self.gdt, inv, 1024) if self.blocked_norm else sumsq(g16, self.gdt, inv)
         norm = math.sqrt(ss) if math.isfinite(ss) else ss
         found_inf = not math.isfinite(ss)
         coef = 1.0
@@ -342,8 +351,9 @@ class ZeroStepOracle:
             self.t += 1
             coef = (clip_once if clip_once is not None
                     else clip_coef(norm, self.h.max_grad_norm, self.h.clip_eps))
-            adamw(self.p, self.m, self.v, self.p16, self.pdt, g16, self.gdt,
-                  step_scalars(self.h, self.t, inv, coef))
+            for a, b, h in self.groups:
+                adamw(self.p[a:b], self.m[a:b], self.v[a:b], None if self.p16 is None else self.p16[a:b],
+                      self.pdt, g16[a:b], self.gdt, step_scalars(h, self.t, inv, coef))
         self.scaler.update(found_inf)
         return StepResult(found_inf, self.t, ss, norm, coef, scale, self.scaler.scale)
 

@@ -39,7 +39,7 @@ def test_struct_layouts_match_header(lib):
     from distributedspeed_amd import _lib
     text = open(HEADER).read()
     for struct in ("DsxState", "DsxScalerConfig", "DsxAdamwHyper", "DsxStepScalars", "DsxTensorRef", "DsxChunk",
-                   "DsxGroupsDev"):
+                   "DsxGroupsDev", "DsxFlatPlan"):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
         fields = re.findall(r"([A-Za-z_][A-Za-z0-9_\s\*]*?)\s+\*?([a-z0-9_]+)(\[[A-Z0-9_]+\])?\s*;", body)
@@ -154,6 +154,33 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.dsx_clip_prepare(al, 1, 2.0, -1.0, 1e-6, al, al, None) == EINVAL
     assert b"max_norm" in lib.dsx_last_error()
     assert lib.dsx_clip_prepare(al, 1, 2.0, 1.0, 1e-6, al, None, None) == EINVAL
+    # the one-call step: its plan and group block are checked before anything is launched
+    plan = _lib.DsxFlatPlan(al, al, al, al, al, 64, 2, 2, al, al, al, 4, 2)
+    plan.scaler = scfg
+    plan.group_end[0], plan.group_end[1] = 32, 64
+    gb = _lib.DsxGroupsDev()
+    gb.ngroups, gb.bc_len = 2, 4
+    for k in range(2):
+        gb.hyper[k] = _lib.DsxAdamwHyper(1e-3, 0.9, 0.999, 1e-8, 0.0, 0.0, 1e-6)
+        gb.bc_table[k] = al
+    assert lib.dsx_zero_step_plan(None, ctypes.byref(gb), None) == EINVAL
+    plan.group_end[0] = 36  # not a multiple of 8
+    assert lib.dsx_zero_step_plan(ctypes.byref(plan), ctypes.byref(gb), None) == EINVAL
+    assert b"group_end" in lib.dsx_last_error()
+    plan.group_end[0], plan.group_end[1] = 32, 60  # the last must end at n
+    assert lib.dsx_zero_step_plan(ctypes.byref(plan), ctypes.byref(gb), None) == EINVAL
+    plan.group_end[1] = 64
+    gb.ngroups = 1
+    assert lib.dsx_zero_step_plan(ctypes.byref(plan), ctypes.byref(gb), None) == EINVAL
+    assert b"groups" in lib.dsx_last_error()
+    gb.ngroups = 2
+    gb.hyper[1].lr = -1.0
+    assert lib.dsx_zero_step_plan(ctypes.byref(plan), ctypes.byref(gb), None) == EINVAL
+    assert b"Invalid learning rate" in lib.dsx_last_error()
+    gb.hyper[1].lr = 1e-3
+    plan.master = al + 4
+    assert lib.dsx_zero_step_plan(ctypes.byref(plan), ctypes.byref(gb), None) == EINVAL
+    assert b"aligned" in lib.dsx_last_error()
     # tuning validation
     assert lib.dsx_set_tuning(8, 8, 3, 1) == EINVAL
     assert lib.dsx_set_tuning(0, 8, 4, 1) == EINVAL

@@ -603,3 +603,53 @@ def test_norm_taken_by_the_hand_over_copy(gpu):
         for k in s_fold:
             dt = torch.int16 if k == "param16" else torch.int32
             assert torch.equal(s_fold[k].view(dt), s_k1[k].view(dt)), (case, k)
+
+
+def test_one_call_step_matches_three_launches(gpu):
+    """The eager flat step issues K1 -> K0 -> K2 through one C call
+    (dsx_zero_step_plan) unless the skip flag is tracked, which keeps the
+    launches separate: both give the same bits over 1030 steps with two
+    groups, learning rates changed every 100 steps, betas changed once, an
+    overflow skip and the bias-correction tables growing past 1024 steps."""
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    shapes = [(130, 7), (9,), (64, 33)]
+    torch.manual_seed(3)
+    init = [torch.randn(s) * 0.05 for s in shapes]
+
+    def build(track):
+        ps = [torch.nn.Parameter(t.clone().to(gpu)) for t in init]
+        opt = AdamWOptimizer([{"params": ps[:2]}, {"params": ps[2:], "lr": 2e-3, "weight_decay": 0.0}],
+                             lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1, max_grad_norm=0.5,
+                             param_dtype=torch.float16, device=gpu,
+                             loss_scaler=ScalerConfig(mode="dynamic", init_scale=2.0 ** 8, window=50, hysteresis=1))
+        opt.track_skips(track)
+        return opt
+
+    a, b = build(False), build(True)
+    assert a._plan is not None
+    gen = torch.Generator(device=gpu).manual_seed(4)
+    _say("one-call step vs three launches, 1030 steps")
+    for step in range(1030):
+        g = (torch.randn(a.flat.numel, device=gpu, generator=gen) * 1e-2 * 256).half()
+        if step == 5:
+            g[100] = float("inf")
+        a.flat.grad.copy_(g)
+        b.flat.grad.copy_(g)
+        if step % 100 == 99:
+            for o in (a, b):
+                o.param_groups[0]["lr"] *= 0.9
+        if step == 500:
+            for o in (a, b):
+                o.param_groups[1]["betas"] = (0.8, 0.99)
+        a.step()
+        b.step()
+    torch.cuda.synchronize()
+    for name in ("master", "exp_avg", "exp_avg_sq", "param16"):
+        x, y = getattr(a.flat, name), getattr(b.flat, name)
+        assert torch.equal(x.view(torch.int16 if x.element_size() == 2 else torch.int32),
+                           y.view(torch.int16 if y.element_size() == 2 else torch.int32)), name
+    sa, sb = a.read_state(), b.read_state()
+    assert bytes(sa) == bytes(sb)
+    assert sa.t > 1024 and sa.overflow_count >= 1 and sa.error == 0

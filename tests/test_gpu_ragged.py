@@ -85,7 +85,8 @@ def test_ragged_large_tensors_through_k2_match_flat(gpu):
     through K3: bit-identical to the flat form over four steps with fp16
     grads, a dynamic loss scale with an overflow skip at step 2, two groups
     and clipping; a large tensor's grad given as a misaligned view is
-    realigned (copied) before K2 reads it."""
+    realigned (copied) before K2 reads it, and a large tensor whose param.data
+    becomes a misaligned view leaves K2 for K3's table."""
     import torch
     from distributedspeed_amd.flat_step import ScalerConfig
     from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
@@ -116,11 +117,21 @@ def test_ragged_large_tensors_through_k2_match_flat(gpu):
                 b.grad = view
             else:
                 b.grad = grads[step][i].clone()
+        if step == 3:
+            # param.data replaced by a misaligned view of the same values: the
+            # rebuilt table keeps the tensor in K3 (K2 needs 16-byte alignment)
+            pbuf = torch.empty(pr[0].numel() + 8, dtype=torch.float16, device=gpu)
+            pview = pbuf[1:1 + pr[0].numel()].view(shapes[0])
+            pview.copy_(pr[0].data)
+            assert pview.data_ptr() % 16
+            pr[0].data = pview
         flat.step()
         rag.step()
         if step == 0:
             assert rag.store.k2_tensors == [0] and K2_TENSOR_ELEMS <= shapes[0][0] * shapes[0][1]
             assert rag.store.small_table is not None and rag.store.small_table.nchunks > 0
+        if step == 3:
+            assert rag.store.k2_tensors == [] and rag.store.small_table is None
     torch.cuda.synchronize()
     assert flat.read_state().overflow_count == rag.read_state().overflow_count == 1
     for i in range(len(shapes)):
