@@ -28,7 +28,7 @@ def test_more_than_one_gpu_is_refused_with_a_message():
 @pytest.mark.gpu
 def test_bench_line_contract(gpu):
     r = _run(["--numel", str((1 << 22) + 3), "--steps", "3", "--warmup", "1", "--cpu-sample", str(1 << 20),
-              "--cpu-seconds", "0.2", "--torch-gpu", "1"], 300)
+              "--cpu-steps", "1", "--torch-gpu", "1", "--secondary", "0"], 300)
     assert r.returncode == 0, r.stderr[-2000:]
     lines = [x for x in r.stdout.splitlines() if x.startswith("{")]
     assert len(lines) == 1
@@ -42,7 +42,23 @@ def test_bench_line_contract(gpu):
     assert rf["bound"] == "hbm" and rf["unit"] == "GB/s" and rf["peak"] == 8000.0
     assert abs(rf["frac"] - rf["achieved"] / rf["peak"]) < 1e-3
     cb = d["cpu_baseline"]
-    assert cb["kind"] in ("port", "reference") and cb["cores"] >= 1 and cb["value"] > 0 and cb["sample"]
+    assert cb["kind"] == "reference" and cb["cores"] >= 1 and cb["value"] > 0 and cb["sample"]
+    assert cb["threads"]["used"] == cb["cores"] and cb["host"]["os_cpu_count"] >= 1
+    assert cb["port"]["value"] > 0 and cb["torch_adamw_cpu_fused"]["value"] > 0
+    assert cb["norm"]["rel_diff"] < 1e-5
+    assert d["secondary_configs"] is None
     assert d["torch_gpu_reference_path"]["foreach_ms_per_step"] > 0
     tp = d["k2_traffic_probe"]
     assert tp["ms"] > 0 and abs(tp["k2_over_probe"] - rf["achieved"] / tp["gbs"]) < 1e-3
+
+
+def test_cpu_baseline_host_facts():
+    """The CPU baseline states its thread count and why, and the host's core
+    counts and CPU model, without a GPU."""
+    sys.path.insert(0, ROOT)
+    import bench
+    info = bench.host_info()
+    assert info["os_cpu_count"] >= 1 and info["affinity_cpus"] >= 1
+    assert info["cpu_model"]
+    n, why = bench.cpu_threads()
+    assert n >= 1 and why
