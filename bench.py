@@ -71,6 +71,7 @@ def _args():
                     help="llama70b-offload: pinned host memory for the fp32 state (the shard shrinks to fit)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="for rocprofv3 --pmc runs: launch K1, K0, K2 and the traffic probe three times each "
+                         "(with --workload llama-ragged / gpt2-small: three steps of that list's ragged form) "
                          "and one 1 GiB fp32 copy (the byte-counter calibration), then exit without timing")
     return ap.parse_args()
 
@@ -82,12 +83,73 @@ def k2_parts(n: int, chunk) -> int:
     return -(-n // chunk) if chunk > 0 and n > chunk else 1
 
 
+def _calibration_copy(dev) -> None:
+    """A plain copy kernel of known size (2^28 fp32 = 1 GiB read and 1 GiB
+    written), three times, so that FETCH_SIZE / WRITE_SIZE per dispatch can
+    be scaled by what the counters report for it."""
+    import torch
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def profile_ragged(workload: str, dev) -> int:
+    """For rocprofv3 runs over the ragged form: three steps of configs[3]'s
+    list (K1 over the chunk table, K0, K3), or of configs[1]'s GPT-2-small
+    list through the drop-in MultiTensorAdamWOptimizer (K1 over the chunk
+    table, K0, K2 for wte and K3 over the other 147 tensors), then the copy
+    calibration."""
+    import math
+
+    import torch
+    from distributedspeed_amd import ops
+    from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
+    if workload == "llama-ragged":
+        ts, table = ragged_list(dev, [math.prod(s) for s in llama_ragged_shapes()])
+        hyper = AdamWHyper(lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, max_grad_norm=1.0)
+        scfg = ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, window=1000, hysteresis=2, min_scale=1.0)
+        bc = BiasCorrectionTable(dev, hyper.beta1, hyper.beta2)
+        st = ops.new_state(dev, scfg.init_scale, scfg.hysteresis)
+        nparts = ops.suggest_partials(table.numel)
+        parts = torch.zeros(nparts, dtype=torch.float64, device=dev)
+        out = ops.new_scalars(dev)
+        for _ in range(3):
+            ops.unscale_norm_multi(table, st, parts, nparts)
+            ops.finalize(parts, nparts, st, scfg.to_c(), hyper.to_c(), bc.table, bc.length, out)
+            ops.adamw_multi(table, out)
+        torch.cuda.synchronize()
+        del ts, table
+    else:
+        from distributedspeed_amd.optimizers import MultiTensorAdamWOptimizer
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1)
+        ps = [torch.nn.Parameter(torch.empty(s, device=dev).normal_(0.0, 0.02, generator=gen))
+              for s in gpt2_small_shapes()]
+        sc = ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, window=1000, hysteresis=1, min_scale=1.0)
+        opt = MultiTensorAdamWOptimizer(ps, lr=6e-4, weight_decay=0.01, max_grad_norm=1.0,
+                                        param_dtype=torch.float16, loss_scaler=sc, device=dev)
+        for p in opt.dsx_params:
+            p.grad = (torch.empty(p.shape, device=dev).normal_(0.0, 1e-3, generator=gen) * 2.0 ** 16).half()
+        for _ in range(3):
+            opt.step()
+        torch.cuda.synchronize()
+        st = opt.store
+        big = sum(st.master[i].numel() for i in st.k2_tensors)
+        _progress(f"gpt2-small ragged: K2 over {len(st.k2_tensors)} tensors / {big} elements, K3 over the other "
+                  f"{len(st.params) - len(st.k2_tensors)} / {st.numel - big} elements "
+                  f"({(st.small_table or st._table).nchunks} chunks)")
+        del opt, ps
+    torch.cuda.empty_cache()
+    _calibration_copy(dev)
+    _progress("profile-kernels done")
+    return 0
+
+
 def profile_kernels(n: int, dev) -> int:
     """Three dispatches of each kernel of the step and of the traffic probe,
-    plus a plain copy kernel of
-    known size (2^28 fp32 = 1 GiB read and 1 GiB written), so that
-    FETCH_SIZE / WRITE_SIZE per dispatch can be scaled by what the counters
-    report for the copy."""
+    plus the copy calibration (_calibration_copy)."""
     import torch
     from distributedspeed_amd import ops
     from distributedspeed_amd.flat_step import AdamWHyper, FlatStep, ScalerConfig
@@ -105,11 +167,7 @@ def profile_kernels(n: int, dev) -> int:
         ops.traffic_probe_flat(master, exp_avg, exp_avg_sq, p16, grad)
     torch.cuda.synchronize()
     del master, exp_avg, exp_avg_sq, p16, grad
-    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
+    _calibration_copy(dev)
     _progress("profile-kernels done")
     return 0
 
@@ -401,6 +459,22 @@ def bench_ffn_train(a, dev) -> int:
     return 0
 
 
+def ragged_list(dev, sizes):
+    """configs[3]'s tensors (seed 4): fp32 master N(0, 0.02^2), m = v = 0,
+    fp16 params, fp16 grads N(0, 1e-3^2) x 2^16; and their chunk table."""
+    import torch
+    from distributedspeed_amd import ops
+    _progress(f"configs[3]: allocating {len(sizes)} tensors / {sum(sizes)} elements")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    ts = []
+    for k in sizes:
+        p = torch.empty(k, device=dev).normal_(0.0, 0.02, generator=gen)
+        g = torch.empty(k, device=dev).normal_(0.0, 1e-3, generator=gen).mul_(2.0 ** 16).to(torch.float16)
+        ts.append((p, torch.zeros(k, device=dev), torch.zeros(k, device=dev), p.to(torch.float16), g))
+    return ts, ops.ChunkTable(*[[t[j] for t in ts] for j in range(5)])
+
+
 def measure_ragged(dev, steps: int, warmup: int) -> dict:
     """configs[3] through K3: fp16 grads N(0, 1e-3^2) x 2^16, dynamic scaler
     (init 2^16, window 1000, hysteresis 2, min 1), AdamW defaults, clip 1.0.
@@ -413,15 +487,7 @@ def measure_ragged(dev, steps: int, warmup: int) -> dict:
     from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
     sizes = [math.prod(s) for s in llama_ragged_shapes()]
     n = sum(sizes)
-    _progress(f"configs[3]: allocating {len(sizes)} tensors / {n} elements")
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(4)
-    ts = []
-    for k in sizes:
-        p = torch.empty(k, device=dev).normal_(0.0, 0.02, generator=gen)
-        g = torch.empty(k, device=dev).normal_(0.0, 1e-3, generator=gen).mul_(2.0 ** 16).to(torch.float16)
-        ts.append((p, torch.zeros(k, device=dev), torch.zeros(k, device=dev), p.to(torch.float16), g))
-    table = ops.ChunkTable(*[[t[j] for t in ts] for j in range(5)])
+    ts, table = ragged_list(dev, sizes)
     hyper = AdamWHyper(lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, max_grad_norm=1.0)
     scfg = ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, window=1000, hysteresis=2, min_scale=1.0)
     bc = BiasCorrectionTable(dev, hyper.beta1, hyper.beta2, capacity=warmup + 3 * steps + 8)
@@ -783,6 +849,8 @@ def main() -> int:
         _lib.call("dsx_set_tuning_k2_chunk", a.k2_chunk)
     n = int(a.numel)
     if a.profile_kernels:
+        if a.workload in ("llama-ragged", "gpt2-small"):
+            return profile_ragged(a.workload, dev)
         return profile_kernels(n, dev)
     if a.workload == "llama-ragged":
         return bench_ragged(a, dev)

@@ -45,6 +45,21 @@ def auto_chunk_elems(numel: int) -> int:
     return c
 
 
+def k3_chunk_elems(numel: int) -> int:
+    """Chunk size of K3's own table when a list's large tensors step through
+    K2: a power of two from 65536 down to 4096 that gives at least 16384
+    chunks where possible. What K3 then takes is many mid-size and small
+    tensors (configs[1]'s 147 GPT-2-small tensors besides wte: 85.8e6
+    elements), which it runs faster in small chunks: on two MI355X boxes, in
+    one process each, 4096-element chunks against the 16384 of
+    auto_chunk_elems took 407 against 414 us and 429 against 463 us (the
+    whole 148-tensor list: 613 against 641 us)."""
+    c = 65536
+    while c > 4096 and numel // c < 16384:
+        c //= 2
+    return c
+
+
 class RaggedParams:
     def __init__(self, groups: list[list[torch.nn.Parameter]], device: torch.device,
                  param_dtype: torch.dtype | None, names: dict | None = None, chunk_elems: int | None = None):
@@ -157,7 +172,7 @@ class RaggedParams:
             self.small_table = ops.ChunkTable(
                 [self.master[i] for i in sub], [self.exp_avg[i] for i in sub], [self.exp_avg_sq[i] for i in sub],
                 None if p16 is None else [p16[i] for i in sub], [self.params[i].grad for i in sub],
-                [self.group_of[i] for i in sub], auto_chunk_elems(n_small))
+                [self.group_of[i] for i in sub], k3_chunk_elems(n_small))
 
     def zero_grad(self, set_to_none: bool = False) -> None:
         """set_to_none: p.grad = None, so the next backward's grads are read

@@ -20,8 +20,16 @@ import glob
 import json
 import os
 
-KERNELS = {"k2_adamw_flat": 28, "k1_unscale_norm": 2, "k0_finalize": 0, "k2_adamw_multi": 28,
+KERNELS = {"k2_adamw_flat": 28, "k1_unscale_norm": 2, "k0_finalize": 0, "k0_finalize_dev": 0, "k2_adamw_multi": 28,
            "k1_unscale_norm_multi": 2, "k2_traffic_probe": 28}
+
+# The launches of one step, by form (the last kernel may repeat: K2 over a
+# partition above 2^26 elements is several consecutive dispatches).
+STEP_FORMS = {
+    "flat, eager (one dsx_zero_step_plan call)": ("k1_unscale_norm", "k0_finalize", "k2_adamw_flat"),
+    "flat, HIP graph replay": ("k1_unscale_norm", "k0_finalize_dev", "k2_adamw_flat"),
+    "ragged (chunk table)": ("k1_unscale_norm_multi", "k0_finalize", "k2_adamw_multi"),
+}
 COPY_NAME = "__amd_rocclr_copyBuffer"
 COPY_BYTES = 1 << 30
 
@@ -80,12 +88,19 @@ def parts_per_call(numel: int, part_elems: int) -> int:
     return -(-numel // part_elems) if part_elems > 0 and numel > part_elems else 1
 
 
-def summarise(trace_dir, fetch_dir, write_dir, numel, part_elems: int = 1 << 26) -> dict:
+def summarise(trace_dir, fetch_dir, write_dir, numel, part_elems: int = 1 << 26,
+              kernel_numel: dict | None = None) -> dict:
+    """kernel_numel: elements one call of a kernel covers where that is not
+    `numel` (a ragged list whose large tensors step through K2 and the rest
+    through K3)."""
+    kernel_numel = kernel_numel or {}
     stats = kernel_stats(trace_dir)
     fetch = counter_per_dispatch(fetch_dir)
     write = counter_per_dispatch(write_dir)
-    f_copy = sum(fetch["copy"]) / len(fetch["copy"])
-    w_copy = sum(write["copy"]) / len(write["copy"])
+    # the calibration copies are the last three copy dispatches of the run
+    # (earlier ones are the program's own copies, such as parameter clones)
+    f_copy = sum(fetch["copy"][-3:]) / len(fetch["copy"][-3:])
+    w_copy = sum(write["copy"][-3:]) / len(write["copy"][-3:])
     f_scale = COPY_BYTES / (f_copy * 1024)
     w_scale = COPY_BYTES / (w_copy * 1024)
     res = {"numel": int(numel), "fetch_scale": f_scale, "write_scale": w_scale,
@@ -93,8 +108,9 @@ def summarise(trace_dir, fetch_dir, write_dir, numel, part_elems: int = 1 << 26)
     for k, per_elt in KERNELS.items():
         if k not in fetch and k not in stats:
             continue
-        parts = parts_per_call(numel, part_elems) if k in PARTED else 1
-        d = {"dispatches_per_call": parts}
+        kn = int(kernel_numel.get(k, numel))
+        parts = parts_per_call(kn, part_elems) if k in PARTED else 1
+        d = {"dispatches_per_call": parts, "numel": kn}
         if k in stats:
             # per call: the dispatches' own durations, without the gaps between them
             d.update(avg_ms=stats[k]["avg_ns"] * parts / 1e6, avg_dispatch_ms=stats[k]["avg_ns"] / 1e6,
@@ -104,16 +120,69 @@ def summarise(trace_dir, fetch_dir, write_dir, numel, part_elems: int = 1 << 26)
             wb = sum(write[k]) / len(write[k]) * 1024 * w_scale * parts
             d.update(fetch_bytes=fb, write_bytes=wb, hbm_bytes=fb + wb)
             if per_elt:
-                d["algorithmic_bytes"] = per_elt * numel
-                d["traffic_over_algorithmic"] = (fb + wb) / (per_elt * numel)
+                d["algorithmic_bytes"] = per_elt * kn
+                d["traffic_over_algorithmic"] = (fb + wb) / (per_elt * kn)
         if "avg_ms" in d and per_elt:
-            d["achieved_gbs"] = per_elt * numel / (d["avg_ms"] * 1e-3) / 1e9
+            d["achieved_gbs"] = per_elt * kn / (d["avg_ms"] * 1e-3) / 1e9
             d["frac_of_8tbs"] = d["achieved_gbs"] / 8000.0
         res["kernels"][k] = d
     k2 = res["kernels"].get("k2_adamw_flat", {})
     res["k2_hbm_bytes_per_launch"] = k2.get("hbm_bytes")
     res["k1_hbm_bytes_per_launch"] = res["kernels"].get("k1_unscale_norm", {}).get("hbm_bytes")
     return res
+
+
+def step_chains(trace_dir: str) -> dict:
+    """Each step's launches found in the kernel trace (--kernel-trace CSV),
+    by form: per step the kernels' own durations, their sum (the time the
+    GPU spends in the step's kernels), the gaps between them, and the period
+    from one step's first kernel to the next step's (all in microseconds,
+    medians over the steps found)."""
+    rows = []
+    for r in csv.DictReader(open(_csv(trace_dir, "kernel_trace.csv"))):
+        rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), _short(r["Kernel_Name"])))
+    rows.sort()
+    med = lambda xs: sorted(xs)[len(xs) // 2] / 1e3 if xs else None  # noqa: E731  (ns -> us)
+    out = {}
+    for form, pat in STEP_FORMS.items():
+        steps, i = [], 0
+        while i < len(rows):
+            if rows[i][2] == pat[0] and i + 2 < len(rows) and rows[i + 1][2] == pat[1] and rows[i + 2][2] == pat[2]:
+                j = i + 3
+                while j < len(rows) and rows[j][2] == pat[2]:
+                    j += 1
+                steps.append(rows[i:j])
+                i = j
+            else:
+                i += 1
+        if not steps:
+            continue
+        per = {k: med([e - s for s, e, n in st if n == k]) for k in pat for st in steps[:1]}
+        for k in pat:
+            per[k] = med([sum(e - s for s, e, n in st if n == k) for st in steps])
+        busy = [sum(e - s for s, e, _ in st) for st in steps]
+        span = [st[-1][1] - st[0][0] for st in steps]
+        period = [steps[k + 1][0][0] - steps[k][0][0] for k in range(len(steps) - 1)]
+        out[form] = {"steps": len(steps), "kernels_us": per, "kernel_busy_us": med(busy), "span_us": med(span),
+                     "gaps_us": med([a - b for a, b in zip(span, busy)]), "period_us": med(period)}
+    return out
+
+
+def chains_markdown(res: dict, command: str, title: str, intro: str = "") -> str:
+    lines = [f"# {title}", ""] + ([intro.strip(), ""] if intro.strip() else []) + [
+             "Commands (run on one MI355X, from the repository root as $R):", "",
+             "```", command.strip(), "```", "",
+             "Per step, medians over the steps of each form in the trace, in microseconds: each kernel's "
+             "duration (for K2 the sum of its dispatches), their sum (kernel-busy), the time from the first "
+             "kernel's start to the last one's end (span), span minus kernel-busy (gaps), and the period from "
+             "one step's first kernel to the next step's. The period under the tracer includes the tracer's "
+             "own cost per dispatch.", "",
+             "| form | steps | K1 | K0 | K2 | kernel-busy | span | gaps | period |", "|---|---|---|---|---|---|---|---|---|"]
+    for form, d in res.items():
+        k = list(d["kernels_us"].values())
+        lines.append(f"| {form} | {d['steps']} | {k[0]:.2f} | {k[1]:.2f} | {k[2]:.2f} | {d['kernel_busy_us']:.2f} | "
+                     f"{d['span_us']:.2f} | {d['gaps_us']:.2f} | {d['period_us']:.2f} |")
+    return "\n".join(lines) + "\n"
 
 
 def markdown(res: dict, command: str, title: str, intro: str = "") -> str:
@@ -127,12 +196,13 @@ def markdown(res: dict, command: str, title: str, intro: str = "") -> str:
              "Figures are per call of the entry point; K2 and its probe issue `dispatches / call` consecutive "
              "dispatches over parts of the partition, and `avg ms` is the sum of their durations (without the gaps "
              "between them).", "",
-             "| kernel | calls | dispatches / call | avg ms | algorithmic GB | achieved GB/s | % of 8 TB/s | HBM read GB | HBM write GB | traffic / algorithmic |",
-             "|---|---|---|---|---|---|---|---|---|---|"]
+             "| kernel | elements / call | calls | dispatches / call | avg ms | algorithmic GB | achieved GB/s | % of 8 TB/s | HBM read GB | HBM write GB | traffic / algorithmic |",
+             "|---|---|---|---|---|---|---|---|---|---|---|"]
     for k, d in res["kernels"].items():
         alg = d.get("algorithmic_bytes")
-        lines.append("| {} | {} | {} | {} | {} | {} | {} | {} | {} | {} |".format(
-            k, d.get("calls", ""), d.get("dispatches_per_call", 1), f"{d['avg_ms']:.4f}" if "avg_ms" in d else "",
+        lines.append("| {} | {:,} | {} | {} | {} | {} | {} | {} | {} | {} | {} |".format(
+            k, d.get("numel", res["numel"]), d.get("calls", ""), d.get("dispatches_per_call", 1),
+            f"{d['avg_ms']:.4f}" if "avg_ms" in d else "",
             f"{alg / 1e9:.3f}" if alg else "", f"{d['achieved_gbs']:.0f}" if "achieved_gbs" in d else "",
             f"{100 * d['frac_of_8tbs']:.1f}" if "frac_of_8tbs" in d else "",
             f"{d['fetch_bytes'] / 1e9:.3f}" if "fetch_bytes" in d else "",
@@ -144,9 +214,11 @@ def markdown(res: dict, command: str, title: str, intro: str = "") -> str:
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--trace", required=True)
-    ap.add_argument("--fetch", required=True)
-    ap.add_argument("--write", required=True)
-    ap.add_argument("--numel", type=int, required=True)
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
+    ap.add_argument("--numel", type=int)
+    ap.add_argument("--chains", action="store_true",
+                    help="summarise the trace's step launches (K1, K0, K2 per step) instead of the counters")
     ap.add_argument("--part-elems", type=int, default=1 << 26,
                     help="the library's K2 part size (dsx_set_tuning_k2_chunk; 0: one dispatch per call)")
     ap.add_argument("--out-md", required=True)
@@ -154,8 +226,21 @@ def main() -> None:
     ap.add_argument("--command", default="")
     ap.add_argument("--title", default="rocprofv3 summary")
     ap.add_argument("--intro", default="", help="a paragraph placed under the title")
+    ap.add_argument("--kernel-numel", action="append", default=[],
+                    help="KERNEL=N: elements one call of KERNEL covers, where it is not --numel")
     a = ap.parse_args()
-    res = summarise(a.trace, a.fetch, a.write, a.numel, a.part_elems)
+    if a.chains:
+        res = step_chains(a.trace)
+        with open(a.out_json, "w") as f:
+            json.dump(res, f, indent=1)
+        with open(a.out_md, "w") as f:
+            f.write(chains_markdown(res, a.command, a.title, a.intro))
+        print(json.dumps(res))
+        return
+    if not (a.fetch and a.write and a.numel):
+        ap.error("--fetch, --write and --numel are required without --chains")
+    kn = {k: int(v) for k, v in (x.split("=", 1) for x in a.kernel_numel)}
+    res = summarise(a.trace, a.fetch, a.write, a.numel, a.part_elems, kn)
     with open(a.out_json, "w") as f:
         json.dump(res, f, indent=1)
     with open(a.out_md, "w") as f:
