@@ -13,8 +13,9 @@ Algorithmic bytes: K1 2 B/elt, K2 28 B/elt, step 30 B/elt.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--numel N]
 
-After the headline's timed steps the same run measures configs[1] (the flat
-drop-in step) and configs[3] (the ragged K1/K0/K3 step) as secondary keys, and
+After the headline's timed steps the same run measures configs[0] and
+configs[1] (the flat drop-in step), configs[3] (the ragged K1/K0/K3 step) and
+configs[4] (state in pinned host memory) as secondary keys, and
 times the reference's CPU route (torch.optim.AdamW on CPU fp32, on the same
 inputs) as cpu_baseline.
 
@@ -45,8 +46,9 @@ def _args():
     ap.add_argument("--cpu-steps", type=int, default=5,
                     help="timed CPU-baseline steps after one warm-up (median reported)")
     ap.add_argument("--secondary", type=int, default=1,
-                    help="after the headline, also measure configs[1] (flat drop-in step) and configs[3] "
-                         "(ragged K1/K0/K3 step) in the same run (0 disables)")
+                    help="after the headline, also measure configs[0] and configs[1] (the flat drop-in step), "
+                         "configs[3] (the ragged K1/K0/K3 step) and configs[4] (state offloaded to pinned host "
+                         "memory) in the same run (0 disables)")
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                       "k2_adamw_flat_llama8b_shard_traffic.json"))
     ap.add_argument("--torch-gpu", type=int, default=1,
@@ -557,7 +559,31 @@ def bench_ragged(a, dev) -> int:
     return 0
 
 
-def bench_offload(a, dev) -> int:
+def link_ceiling(dev) -> dict:
+    """Plain pinned-host <-> HBM copy bandwidth (offload.measure_link),
+    measured in a fresh child process: within a process that has already
+    allocated and freed large device buffers, the runtime can run the two
+    directions one at a time (the figure then halves), while a fresh
+    process gives the machine's ceiling. Falls back to this process."""
+    import subprocess
+    root = os.path.dirname(os.path.abspath(__file__))
+    code = ("import json, sys, torch; sys.path.insert(0, %r); from distributedspeed_amd.offload import measure_link; "
+            "print(json.dumps(measure_link(torch.device('cuda', %d))))" % (root, dev.index or 0))
+    try:
+        r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+        if r.returncode == 0:
+            out = json.loads(r.stdout.strip().splitlines()[-1])
+            out["measured_in"] = "a fresh process"
+            return out
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    from distributedspeed_amd.offload import measure_link
+    out = measure_link(dev)
+    out["measured_in"] = "this process"
+    return out
+
+
+def measure_offload(dev, full: int, budget_gib: float, steps: int) -> dict:
     """Llama-3-70B ZeRO-3 one-rank shard, 8,819,213,312 elements,
     fp32 master/m/v in pinned host memory (105.8 GB) streamed through HBM in
     64 Mi-element chunks, bf16 grads N(0, 3e-4^2) and params in HBM; AdamW lr
@@ -567,15 +593,14 @@ def bench_offload(a, dev) -> int:
     import torch
     from distributedspeed_amd import ops
     from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
-    from distributedspeed_amd.offload import HostStateStreamer, measure_link, pinned_zeros
-    full = int(a.numel) if a.numel != HEADLINE_NUMEL else 8_819_213_312
+    from distributedspeed_amd.offload import HostStateStreamer, pinned_zeros
     chunk = 64 << 20
     _progress("measuring the host link")
-    link = measure_link(dev)
+    link = link_ceiling(dev)
     # The machine caps GPU-visible pinned host memory (one hipHostMalloc above
     # 32 GiB fails, ~64 GiB in total, and the runtime needs part of it), so the
     # shard is sized to a pinned budget: 12 B of state per element.
-    budget = int(a.pinned_budget_gib * 2**30)
+    budget = int(budget_gib * 2**30)
     n = min(full, budget // 12 // chunk * chunk)
     _progress(f"link {link}; allocating {n} of {full} elements of pinned state ({12 * n / 2**30:.1f} GiB)")
     grad = torch.empty(n, dtype=torch.bfloat16, device=dev)
@@ -602,7 +627,6 @@ def bench_offload(a, dev) -> int:
     parts = torch.zeros(nparts, dtype=torch.float64, device=dev)
     out = ops.new_scalars(dev)
     streamer = HostStateStreamer(dev, chunk)
-    steps = max(1, min(a.steps, 3))
 
     def step():
         ops.unscale_norm(grad, st, parts, nparts)
@@ -622,22 +646,35 @@ def bench_offload(a, dev) -> int:
     s = ops.read_state(st)
     sec = sorted(times)[len(times) // 2]
     each_way = 12 * n / sec / 1e9
+    del grad, p16, master, m, v, streamer
+    torch.cuda.empty_cache()
+    return {"workload": "llama3-70b zero3 one-rank shard, state offloaded (BASELINE configs[4])",
+            "storage": "f32 state (pinned host) / bf16 grads+params", "numel": n, "chunk_elems": chunk,
+            "steps": steps, "warmup": 1, "ms_per_step": round(sec * 1e3, 1),
+            "gparam_per_s": round(n / sec / 1e9, 4), "link_gbs_each_way": round(each_way, 2),
+            "link_ceiling_gbs": {k: (round(x, 2) if isinstance(x, float) else x) for k, x in link.items()},
+            "frac_of_measured_bidirectional_link": round(each_way / link["both_each_way"], 4),
+            "frac_of_one_direction_link": round(each_way / min(link["h2d"], link["d2h"]), 4),
+            "reduced_from_numel": full if n != full else None,
+            "reduction_reason": (f"pinned budget {budget_gib} GiB: this machine caps GPU-visible pinned host "
+                                 "memory (no single hipHostMalloc above 32 GiB, ~64 GiB in total); the full shard "
+                                 "needs 105.8 GB; the step is host-link-bound, so Gparam/s does not depend on the size")
+            if n != full else None,
+            "state_t": s.t, "skipped": s.last_skip, "state_error": s.error}
+
+
+def bench_offload(a, dev) -> int:
+    """configs[4] as its own line (measure_offload)."""
+    full = int(a.numel) if a.numel != HEADLINE_NUMEL else 8_819_213_312
+    r = measure_offload(dev, full, a.pinned_budget_gib, max(1, min(a.steps, 3)))
     print(json.dumps({
         "metric": "offloaded ZeRO step (configs[4]): Gparam/s and host-link GB/s each way",
-        "value": round(n / sec / 1e9, 4), "unit": "Gparam/s", "n_gpus": 1, "steps": steps, "warmup": 1,
-        "ms_per_step": round(sec * 1e3, 1), "higher_is_better": True, "dtype": "f32",
-        "data": "synthetic", "config": {"workload": "llama3-70b zero3 one-rank shard, state offloaded "
-                                                    "(BASELINE configs[4])",
-                                        "storage": "f32 state (pinned host) / bf16 grads+params", "numel": n, "chunk_elems": chunk},
-        "link_gbs_each_way": round(each_way, 2), "link_ceiling_gbs": {k: round(x, 2) for k, x in link.items()},
-        "frac_of_measured_bidirectional_link": round(each_way / link["both_each_way"], 4),
-        "frac_of_one_direction_link": round(each_way / min(link["h2d"], link["d2h"]), 4),
-        "reduced_from_numel": full if n != full else None,
-        "reduction_reason": (f"pinned budget {a.pinned_budget_gib} GiB: this machine caps GPU-visible pinned host "
-                             "memory (no single hipHostMalloc above 32 GiB, ~64 GiB in total); the full shard needs "
-                             "105.8 GB; the step is host-link-bound, so Gparam/s does not depend on the size")
-        if n != full else None,
-        "state_t": s.t, "skipped": s.last_skip,
+        "value": r["gparam_per_s"], "unit": "Gparam/s", "n_gpus": 1, "steps": r["steps"], "warmup": 1,
+        "ms_per_step": r["ms_per_step"], "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+        "config": {k: r[k] for k in ("workload", "storage", "numel", "chunk_elems")},
+        **{k: r[k] for k in ("link_gbs_each_way", "link_ceiling_gbs", "frac_of_measured_bidirectional_link",
+                             "frac_of_one_direction_link", "reduced_from_numel", "reduction_reason", "state_t")},
+        "skipped": r["skipped"],
     }), flush=True)
     return 0
 
@@ -940,16 +977,34 @@ def main() -> int:
         except (OSError, ValueError):
             traffic = None
 
-    torch_gpu = torch_gpu_reference(master, grad, hyper, ms_step) if a.torch_gpu else None
+    # The other BASELINE configs in the same run, after the headline's timed
+    # region. configs[4] goes first, while nothing large has been returned to
+    # the HIP runtime: on these boxes, once a process has freed a large
+    # allocation (hipFree of 16 GB), its simultaneous host-to-device and
+    # device-to-host copies run one at a time (28.8 instead of 48.6 GB/s each
+    # way), which would halve that line.
+    secondary = {}
 
-    # configs[1] and configs[3] in the same run, after the headline's timed
-    # region and with its buffers freed
-    secondary = None
+    def run_secondary(key, fn):
+        try:
+            secondary[key] = fn()
+        except Exception as e:  # a secondary line must not cost the headline
+            secondary[key] = {"error": f"{type(e).__name__}: {e}"}
+            torch.cuda.empty_cache()
+
+    if a.secondary:
+        run_secondary("configs[4]", lambda: measure_offload(dev, 8_819_213_312, a.pinned_budget_gib, 3))
+    torch_gpu = torch_gpu_reference(master, grad, hyper, ms_step) if a.torch_gpu else None
     if a.secondary:
         del master, exp_avg, exp_avg_sq, p16, grad, fs
         torch.cuda.empty_cache()
-        secondary = {"configs[1]": measure_dropin(dev, True, a.steps, a.warmup, modes=("flat_eager",)),
-                     "configs[3]": measure_ragged(dev, max(3, min(a.steps, 10)), min(a.warmup, 3))}
+        run_secondary("configs[0]", lambda: measure_dropin(dev, False, max(a.steps, 200), max(a.warmup, 20),
+                                                           modes=("flat_eager",)))
+        run_secondary("configs[1]", lambda: measure_dropin(dev, True, a.steps, a.warmup, modes=("flat_eager",)))
+        run_secondary("configs[3]", lambda: measure_ragged(dev, max(3, min(a.steps, 10)), min(a.warmup, 3)))
+        secondary = {k: secondary[k] for k in sorted(secondary)}
+    else:
+        secondary = None
     cpu = cpu_baseline(*cpu_in, hyper, a.cpu_steps, shard=n)
 
     out = {

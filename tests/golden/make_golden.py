@@ -27,6 +27,11 @@ the library routines the reference calls, run on the CPU:
       hysteresis decision on top of it follows the ds_config key's meaning:
       an overflow while more than one is still tolerated resets the growth
       tracker without backing off (the op with backoff factor 1.0).
+
+  scaler_config4_llama_ragged_backoff.json
+      the same configuration from default_rng(1022), a seed whose sequence
+      reaches every branch: tolerated overflow, growth re-arming the
+      hysteresis, and back-offs.
 """
 from __future__ import annotations
 
@@ -124,6 +129,20 @@ def main() -> None:
                    "overflow": [int(x) for x in flags4], "scale_after": seq4,
                    "final_t": sum(1 for x in flags4 if not x)}, f)
     print("overflows in config4 sequence:", sum(flags4), "final scale", seq4[-1])
+
+    # a second seed for the same configuration, chosen so that the sequence
+    # holds every hysteresis-2 branch: a tolerated overflow (step 1), a growth
+    # that re-arms the hysteresis (1001), another tolerated overflow (1010),
+    # then two back-offs (1300, 1919)
+    rng = np.random.default_rng(1022)
+    flags4b = (rng.random(2000) < 1e-3).tolist()
+    seq4b = scaler_sequence(flags4b, 2.0 ** 16, 1000, 2, 1.0)
+    with open(os.path.join(HERE, "scaler_config4_llama_ragged_backoff.json"), "w") as f:
+        json.dump({"init_scale": 2.0 ** 16, "window": 1000, "hysteresis": 2, "min_scale": 1.0,
+                   "rng": "numpy default_rng(1022).random(2000) < 1e-3",
+                   "overflow": [int(x) for x in flags4b], "scale_after": seq4b,
+                   "final_t": sum(1 for x in flags4b if not x)}, f)
+    print("overflows in the second config4 sequence:", sum(flags4b), "final scale", seq4b[-1])
 
 
 if __name__ == "__main__":

@@ -110,65 +110,120 @@ def _checksums(tensors):
 
 
 def test_config4_ragged_k3_equals_flat_k2_full_size(gpu, oracle):
+    """configs[3] at full size, three steps (the second with an inf grad,
+    tolerated under hysteresis 2): K3 over the 289 tensors and K2 over the
+    same values laid out flat give bit-identical master / exp_avg / exp_avg_sq
+    / fp16 params and the same skip, clip and scaler decisions. Both forms are
+    resident at once (249 GB): the ragged tensors' grads are views of the
+    flat grad buffer, which both steps read."""
     import torch
     from distributedspeed_amd import ops
     from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
     shapes = llama_ragged_shapes()
     sizes = [math.prod(s) for s in shapes]
+    n = sum(sizes)
     hyper = AdamWHyper(lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, max_grad_norm=1.0)
     scfg = ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, window=1000, hysteresis=2, min_scale=1.0)
     bc = BiasCorrectionTable(gpu, hyper.beta1, hyper.beta2)
-
-    def fill(i, p, m, v, g):
+    _say("config4 full size: flat buffers")
+    flat = [torch.empty(n, device=gpu) for _ in range(3)]
+    p16f = torch.empty(n, dtype=torch.float16, device=gpu)
+    g = torch.empty(n, dtype=torch.float16, device=gpu)
+    off = 0
+    bounds = []
+    for i, k in enumerate(sizes):
         gen = torch.Generator(device=gpu)
         gen.manual_seed(10_000 + i)
-        p.normal_(0.0, 0.02, generator=gen)
-        m.normal_(0.0, 1e-4, generator=gen)
-        v.normal_(0.0, 1e-6, generator=gen).abs_()
-        g.copy_(torch.empty(g.numel(), device=gpu).normal_(0.0, 1e-3, generator=gen).mul_(2.0 ** 16))
+        flat[0][off:off + k].normal_(0.0, 0.02, generator=gen)
+        flat[1][off:off + k].normal_(0.0, 1e-4, generator=gen)
+        flat[2][off:off + k].normal_(0.0, 1e-6, generator=gen).abs_()
+        g[off:off + k].copy_(torch.empty(k, device=gpu).normal_(0.0, 1e-3, generator=gen).mul_(2.0 ** 16))
+        bounds.append((off, off + k))
+        off += k
+    _say("config4 full size: ragged tensors")
+    rag = [[flat[j][a:b].clone() for (a, b) in bounds] for j in range(3)]
+    rp16 = [torch.empty(b - a, dtype=torch.float16, device=gpu) for (a, b) in bounds]
+    rg = [g[a:b] for (a, b) in bounds]
+    table = ops.ChunkTable(rag[0], rag[1], rag[2], rp16, rg)
+    st_r, st_f = ops.new_state(gpu, scfg.init_scale, scfg.hysteresis), ops.new_state(gpu, scfg.init_scale,
+                                                                                     scfg.hysteresis)
+    nparts = ops.suggest_partials(n)
+    parts_r = torch.zeros(nparts, dtype=torch.float64, device=gpu)
+    parts_f = torch.zeros(nparts, dtype=torch.float64, device=gpu)
+    out_r, out_f = ops.new_scalars(gpu), ops.new_scalars(gpu)
+    bad = bounds[150][0] + 12_345
+    for step in range(3):
+        _say(f"config4 full size: step {step}")
+        if step == 1:
+            keep = g[bad].clone()
+            g[bad] = float("inf")
+        ops.unscale_norm_multi(table, st_r, parts_r, nparts)
+        ops.finalize(parts_r, nparts, st_r, scfg.to_c(), hyper.to_c(), bc.table, bc.length, out_r)
+        ops.adamw_multi(table, out_r)
+        ops.zero_step_flat(flat[0], flat[1], flat[2], p16f, g, st_f, scfg.to_c(), hyper.to_c(), bc.table,
+                           bc.length, parts_f, nparts, out_f)
+        if step == 1:
+            g[bad] = keep
+        sr, sf = ops.read_scalars(out_r), ops.read_scalars(out_f)
+        assert sr.skip == sf.skip == (1 if step == 1 else 0), step
+        if not sr.skip:
+            assert sr.norm == pytest.approx(sf.norm, rel=1e-12)
+            assert sr.clip_coef == sf.clip_coef and sr.clip_coef < 1.0
+        ar, af = ops.read_state(st_r), ops.read_state(st_f)
+        for k in ("scale", "good_steps", "hyst_left", "t", "overflow_count", "error"):
+            assert getattr(ar, k) == getattr(af, k), (step, k)
+    assert (ar.t, ar.overflow_count, ar.hyst_left, ar.scale) == (2, 1, 1, 2.0 ** 16)
+    _say("config4 full size: compare")
+    for i, (a, b) in enumerate(bounds):
+        for j, name in enumerate(("master", "exp_avg", "exp_avg_sq")):
+            assert torch.equal(rag[j][i].view(torch.int32), flat[j][a:b].view(torch.int32)), f"tensor {i}: {name}"
+        assert torch.equal(rp16[i].view(torch.int16), p16f[a:b].view(torch.int16)), f"tensor {i}: param16"
 
-    def run_ragged():
-        ts = []
-        for i, k in enumerate(sizes):
-            p, m, v = (torch.empty(k, device=gpu) for _ in range(3))
-            g = torch.empty(k, dtype=torch.float16, device=gpu)
-            fill(i, p, m, v, g)
-            ts.append((p, m, v, torch.empty(k, dtype=torch.float16, device=gpu), g))
-        table = ops.ChunkTable(*[[t[j] for t in ts] for j in range(5)])
-        st = ops.new_state(gpu, scfg.init_scale, scfg.hysteresis)
-        nparts = ops.suggest_partials(table.numel)
-        parts = torch.zeros(nparts, dtype=torch.float64, device=gpu)
-        out = ops.new_scalars(gpu)
+
+@pytest.mark.parametrize("name", ["scaler_config4_llama_ragged.json", "scaler_config4_llama_ragged_backoff.json"])
+def test_config4_golden_scaler_sequence_through_k3(gpu, name):
+    """configs[3]'s committed 2000-step loss-scale sequences (torch's
+    _amp_update_scale_ with the hysteresis of the ds_config key; the second
+    seed reaches a tolerated overflow, a growth that re-arms the hysteresis
+    and two back-offs) replayed through the ragged path (K1 over a chunk
+    table, K0, K3): the device scale after every step equals the golden one,
+    and the step count and overflow count match."""
+    import json
+    import os
+    import torch
+    from distributedspeed_amd import ops
+    from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)) as f:
+        gold = json.load(f)
+    sizes = [4096, 1000, 77]
+    gen = torch.Generator(device=gpu).manual_seed(6)
+    ts = [(torch.empty(k, device=gpu).normal_(0.0, 0.02, generator=gen), torch.zeros(k, device=gpu),
+           torch.zeros(k, device=gpu), torch.empty(k, dtype=torch.float16, device=gpu),
+           (torch.empty(k, device=gpu).normal_(0.0, 1e-3, generator=gen) * 64).half()) for k in sizes]
+    table = ops.ChunkTable(*[[t[j] for t in ts] for j in range(5)], chunk_elems=1024)
+    scfg = ScalerConfig(mode="dynamic", init_scale=gold["init_scale"], window=gold["window"],
+                        hysteresis=gold["hysteresis"], min_scale=gold["min_scale"])
+    hyper = AdamWHyper(lr=1e-5, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0)
+    bc = BiasCorrectionTable(gpu, hyper.beta1, hyper.beta2, capacity=len(gold["overflow"]) + 8)
+    st = ops.new_state(gpu, scfg.init_scale, scfg.hysteresis)
+    nparts = ops.suggest_partials(table.numel)
+    parts = torch.zeros(nparts, dtype=torch.float64, device=gpu)
+    out = ops.new_scalars(gpu)
+    scale_view = ops.scale_view(st)
+    got = torch.empty(len(gold["overflow"]), dtype=torch.float32, device=gpu)
+    g1 = ts[1][4]
+    _say(f"golden scaler sequence {name} through K3")
+    for i, f in enumerate(gold["overflow"]):
+        if f:
+            g1[500] = float("inf")
         ops.unscale_norm_multi(table, st, parts, nparts)
         ops.finalize(parts, nparts, st, scfg.to_c(), hyper.to_c(), bc.table, bc.length, out)
         ops.adamw_multi(table, out)
-        sums = [_checksums(t[:4]) for t in ts]
-        return sums, ops.read_scalars(out)
-
-    _say("config4 ragged K3 step")
-    sums3, sc3 = run_ragged()
-    torch.cuda.empty_cache()
-    _say("config4 flat K2 step")
-    n = sum(sizes)
-    flat = [torch.empty(n, device=gpu) for _ in range(3)]
-    g = torch.empty(n, dtype=torch.float16, device=gpu)
-    p16 = torch.empty(n, dtype=torch.float16, device=gpu)
-    off = 0
-    for i, k in enumerate(sizes):
-        fill(i, flat[0][off:off + k], flat[1][off:off + k], flat[2][off:off + k], g[off:off + k])
-        off += k
-    st = ops.new_state(gpu, scfg.init_scale, scfg.hysteresis)
-    nparts = ops.suggest_partials(n)
-    parts = torch.zeros(nparts, dtype=torch.float64, device=gpu)
-    out = ops.new_scalars(gpu)
-    ops.zero_step_flat(flat[0], flat[1], flat[2], p16, g, st, scfg.to_c(), hyper.to_c(), bc.table, bc.length,
-                       parts, nparts, out)
-    sc2 = ops.read_scalars(out)
-    assert sc3.skip == sc2.skip == 0
-    assert sc3.norm == pytest.approx(sc2.norm, rel=1e-12)
-    assert sc3.clip_coef == sc2.clip_coef and sc3.clip_coef < 1.0
-    off = 0
-    for i, k in enumerate(sizes):
-        got = _checksums([flat[0][off:off + k], flat[1][off:off + k], flat[2][off:off + k], p16[off:off + k]])
-        assert got == sums3[i], f"tensor {i} differs"
-        off += k
+        got[i] = scale_view[0]
+        if f:
+            g1[500] = 0.0
+    seq = got.cpu().tolist()
+    bad = [i + 1 for i, (a, b) in enumerate(zip(seq, gold["scale_after"])) if a != b]
+    assert not bad, f"scale differs from the golden sequence at steps {bad[:10]}"
+    s = ops.read_state(st)
+    assert s.t == gold["final_t"] and s.overflow_count == sum(gold["overflow"]) and s.error == 0

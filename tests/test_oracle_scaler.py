@@ -112,7 +112,8 @@ def test_skip_does_not_advance_step_counter(oracle):
     assert r2.scale_used == 4.0 and r2.scale_next == 2.0
 
 
-@pytest.mark.parametrize("name", ["scaler_config2_gpt2.json", "scaler_config4_llama_ragged.json"])
+@pytest.mark.parametrize("name", ["scaler_config2_gpt2.json", "scaler_config4_llama_ragged.json",
+                                  "scaler_config4_llama_ragged_backoff.json"])
 def test_golden_scaler_sequences(oracle, name):
     with open(os.path.join(GOLDEN, name)) as f:
         g = json.load(f)
