@@ -667,7 +667,8 @@ __global__ __launch_bounds__(kBlock) void k0_finalize_dev(const double* __restri
                                                           DsxStepScalars* __restrict__ out) {
   const double sumsq = reduce_partials(partials, nparts);
   if (threadIdx.x != 0) return;
-  const DsxGroupsDev grp = *gp;
+  // read in place: a copy of the 1112-byte block would live in scratch memory
+  const DsxGroupsDev& grp = *gp;
   bool bad = grp.ngroups < 1 || grp.ngroups > max_groups || grp.ngroups > DSX_MAX_GROUPS || grp.bc_len < 0;
   for (int k = 0; !bad && k < grp.ngroups; ++k)
     bad = !hyper_ok(grp.hyper[k]) || grp.t_offset[k] < 0 || (grp.bc_len > 0 && grp.bc_table[k] == nullptr);
