@@ -148,18 +148,26 @@ def _host(opt, grads):
             torch16_to_np(cat([p.data for p in st.params])), torch16_to_np(cat(grads)))
 
 
-@pytest.mark.parametrize("form", ["flat", "ragged"])
+# flat: the one-call eager step; graph: K1 + K0 (device-memory form) + K2
+# replayed from one HIP graph; capturable: the launches a caller may capture,
+# here issued eagerly; offload: state in pinned host memory, K2 streamed.
+FORMS = {"flat": {}, "graph": {"graph": True}, "capturable": {"capturable": True},
+         "offload": {"offload": True, "offload_chunk_elems": 8192}, "ragged": None}
+
+
+@pytest.mark.parametrize("form", list(FORMS))
 def test_clip_grad_norm_is_one_shot(gpu, oracle, form):
     import torch
     from distributedspeed_amd.flat_step import ScalerConfig
     from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
     from distributedspeed_amd.zero import ZeROOptimizer
     O = oracle
-    cls = AdamWOptimizer if form == "flat" else MultiTensorAdamWOptimizer
+    cls = MultiTensorAdamWOptimizer if form == "ragged" else AdamWOptimizer
+    kw = FORMS[form] or {}
     ps = _params(gpu, 3, torch.float32)
     sc = ScalerConfig(mode="dynamic", init_scale=2.0 ** 10, window=1000, hysteresis=1)
     opt = cls(ps, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0,
-              param_dtype=torch.float16, loss_scaler=sc, device=gpu)
+              param_dtype=torch.float16, loss_scaler=sc, device=gpu, **kw)
     zero = ZeROOptimizer(opt, {"stage": 2})
     gen = torch.Generator(device=gpu).manual_seed(8)
     # (explicit clip before the step: (max_norm, norm_type) or None, inject an inf)
@@ -172,7 +180,7 @@ def test_clip_grad_norm_is_one_shot(gpu, oracle, form):
             g = (torch.randn(p.shape, generator=gen, device=gpu) * 0.02 * scale).half()
             if inf and i == 2:
                 g.view(-1)[17] = float("inf")
-            if form == "flat":
+            if form != "ragged":
                 p.grad.copy_(g)
                 grads.append(p.grad)
             else:
@@ -194,6 +202,7 @@ def test_clip_grad_norm_is_one_shot(gpu, oracle, form):
             assert norm_t.dtype == torch.float32 and norm_t.device.type == "cuda" and norm_t.dim() == 0
             coef = O.clip_once_coef(ref, clip[0])
         zero.step()
+        torch.cuda.synchronize(gpu)  # the offloaded form writes host memory from its own streams
         r = orc.step(g16, clip_once=coef)
         st = opt.read_state()
         assert st.clip_once == 0, f"step {step}: the one-shot clip was not consumed"
