@@ -283,6 +283,63 @@ def test_checkpoint_round_trip_is_bit_exact(gpu, tmp_path, contiguous):
     assert (s1.scale, s1.t, s1.good_steps, s1.overflow_count) == (s2.scale, s2.t, s2.good_steps, s2.overflow_count)
 
 
+_FORM_CFG = {"flat": {}, "ragged": {"contiguous_gradients": False}, "offload": {"cpu_offload": True},
+             "graph": None}
+
+
+@pytest.mark.parametrize("src,dst", [("flat", "ragged"), ("flat", "offload"), ("flat", "graph"),
+                                     ("ragged", "flat"), ("offload", "ragged")])
+def test_checkpoint_moves_between_storage_forms(gpu, tmp_path, src, dst):
+    """The checkpoint is keyed by parameter name and offset, not by the
+    storage it came from: one saved by one step form (flat HBM partition,
+    ragged list, state offloaded to pinned host memory, graph-replayed step)
+    loads into another, and training continues bit for bit as it would have
+    in the saving engine. No clipping here: the flat form's norm comes from
+    the hooks' copies, the ragged form's from K1 over the list, equal to
+    1e-12 but not bit for bit, and the clip coefficient is rounded from it."""
+    import torch
+    import distributedspeed_amd as ds
+    _say(f"checkpoint from {src} into {dst}")
+
+    def cfg(form):
+        zo = {"stage": 2, "contiguous_gradients": True}
+        zo.update(_FORM_CFG[form] or {})
+        c = {"fp16": {"enabled": True, "hysteresis": 1, "initial_scale_power": 12}, "max_grad_norm": 0.0,
+             "zero_optimization": zo}
+        if form == "graph":
+            c["hip_graph"] = True
+        return c
+
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(21)
+    data = [(torch.randn(16, 784, device=gpu, generator=gen), torch.randint(0, 10, (16,), device=gpu, generator=gen))
+            for _ in range(6)]
+
+    def train(engine, batches):
+        for x, y in batches:
+            engine.backward(torch.nn.functional.cross_entropy(engine(x).float(), y))
+            engine.step()
+
+    e1, _, _, _ = ds.initialize(_mlp(5), cfg(src))
+    train(e1, data[:3])
+    e1.save_checkpoint(str(tmp_path))
+    train(e1, data[3:])
+    e2, _, _, _ = ds.initialize(_mlp(6), cfg(dst))
+    e2.load_checkpoint(str(tmp_path))
+    assert e2.global_steps == 3
+    train(e2, data[3:])
+    torch.cuda.synchronize(gpu)
+    b1, b2 = e1.optimizer.base_optimizer, e2.optimizer.base_optimizer
+    for i in range(len(b1.dsx_params)):
+        v1, v2 = b1.store.views_of(i), b2.store.views_of(i)
+        for name in ("master", "exp_avg", "exp_avg_sq"):
+            assert torch.equal(v1[name].cpu(), v2[name].cpu()), (i, name)
+        assert torch.equal(b1.dsx_params[i].detach(), b2.dsx_params[i].detach()), (i, "param16")
+    s1, s2 = b1.read_state(), b2.read_state()
+    assert (s1.scale, s1.t, s1.good_steps, s1.overflow_count) == (s2.scale, s2.t, s2.good_steps, s2.overflow_count)
+    assert s1.t == 6
+
+
 @pytest.mark.parametrize("contiguous", [True, False])
 def test_model_state_loaded_after_initialize_is_kept(gpu, contiguous):
     """A model state dict loaded into the module after initialize() writes
