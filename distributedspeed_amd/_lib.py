@@ -34,7 +34,8 @@ class DsxState(_c.Structure):
     _fields_ = [("scale", _c.c_float), ("good_steps", _c.c_int32), ("hyst_left", _c.c_int32),
                 ("t", _c.c_int32), ("iter", _c.c_int64), ("overflow_count", _c.c_int64),
                 ("error", _c.c_int32), ("last_skip", _c.c_int32), ("last_norm", _c.c_double),
-                ("clip_once_coef", _c.c_float), ("clip_once", _c.c_int32), ("reserved", _c.c_int64)]
+                ("clip_once_coef", _c.c_float), ("clip_once", _c.c_int32), ("step_scale", _c.c_float),
+                ("step_t2", _c.c_int32)]
 
 
 class DsxScalerConfig(_c.Structure):
@@ -88,6 +89,7 @@ SIGNATURES = {
     "dsx_set_tuning": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int]),
     "dsx_set_tuning_k2": (_c.c_int, [_c.c_int, _c.c_int]),
     "dsx_set_tuning_k2_chunk": (_c.c_int, [_c.c_int64]),
+    "dsx_set_tuning_fold": (_c.c_int, [_c.c_int64]),
     "dsx_copy_unscale_norm": (_c.c_int, [_P, _P, _c.c_int, _c.c_int64, _P, _P, _c.c_int32, _P]),
     "dsx_reduce_segments": (_c.c_int, [_P, _P, _c.c_int32, _P, _P]),
     "dsx_suggest_partials": (_c.c_int32, [_c.c_int64]),

@@ -121,6 +121,11 @@ struct Tuning {
   // TB/s from 64 Mi to 4 Gi elements (16 Mi parts lose to launch gaps, 256 Mi
   // parts lose the gain; splitting below 64 Mi gains nothing).
   int64_t k2_chunk_elems = int64_t(1) << 26;
+  // Steps over at most this many elements (with at most kFoldMaxParts
+  // partials) run as two launches, K1 and K2 with the finalize folded in
+  // (k2_adamw_fold), instead of K1, K0, K2; 0: always three launches. 2^24
+  // elements is the end of K2's one-trip grid on 256 CUs.
+  int64_t fold_max_elems = int64_t(1) << 24;
 };
 Tuning g_tune;
 
@@ -359,13 +364,25 @@ __device__ __forceinline__ float inv_of(float scale) {
 // Each element contributes (double)(f32(g) * inv)^2. The square of a finite
 // fp32 value is exact in fp64 and the sum of 2^31 of them cannot overflow,
 // so the sum is non-finite exactly when some unscaled grad is inf or NaN.
+//
+// fold != NULL (the same state) starts a two-launch step whose finalize runs
+// inside K2 (k2_adamw_fold): block 0 records the entry scale and t with the
+// one-shot clip flag, which it consumes, in step_scale / step_t2. The K2
+// blocks read those two fields, which nothing else writes during the step,
+// while one of them writes the state's updated fields.
 
 template <int GD, int U, bool NT>
 __global__ __launch_bounds__(kBlock) void k1_unscale_norm(const void* __restrict__ gv, int64_t n,
-                                                          const DsxState* __restrict__ state,
-                                                          double* __restrict__ partials) {
+                                                          const DsxState* state, double* __restrict__ partials,
+                                                          DsxState* fold) {
   using G = Grad<GD>;
   const float inv = inv_of(state->scale);
+  if (fold != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    const int32_t armed = fold->clip_once != 0 ? 1 : 0;
+    fold->step_scale = fold->scale;
+    fold->step_t2 = 2 * fold->t + armed;
+    fold->clip_once = 0;
+  }
   const u4* g16 = static_cast<const u4*>(gv);
   const typename G::elem* g = static_cast<const typename G::elem*>(gv);
   const int64_t nvec = n / G::per16;
@@ -554,70 +571,108 @@ __device__ __forceinline__ bool hyper_ok(const DsxAdamwHyper& h) {
          h.weight_decay >= 0.0 && h.clip_eps >= 0.0 && h.max_grad_norm == h.max_grad_norm;
 }
 
-// Thread 0 only. Global part of a step (norm, skip, clip, t, scaler) once;
-// per-group fp32 scalars into out[0..nout). Slots at or past grp.ngroups (and
-// every slot when groups_bad) get skip = 1, so a K2 launched for them leaves
-// its group unchanged rather than reusing an older step's scalars.
-__device__ void finalize_body(double sumsq, DsxState* __restrict__ state, const DsxScalerConfig& scfg,
-                              const DsxGroupsDev& grp, bool groups_bad, int nout,
-                              DsxStepScalars* __restrict__ out) {
-  DsxState s = *state;
-  const double norm = sqrt(sumsq);
-  const float inv = inv_of(s.scale);
-  const bool found_inf = !__builtin_isfinite(sumsq);
-  const bool dynamic = scfg.mode == DSX_SCALE_DYNAMIC;
-  const int32_t t = s.t + 1;
-  bool skip = found_inf || groups_bad;
+// The step's decision from the squared norm and the state as the step began
+// (scale, t, clip_once, clip_once_coef): norm, skip, clip coefficient, t.
+// Error bits found on the way are set in s.error.
+struct Decision {
+  double norm;
+  float inv, coef;
+  int32_t t;  // t of a step that is not skipped
+  int ng;     // live groups (0 when the group inputs are bad)
+  bool found_inf, skip;
+};
+
+__device__ Decision decide(double sumsq, DsxState& s, const DsxGroupsDev& grp, bool groups_bad) {
+  Decision d;
+  d.norm = sqrt(sumsq);
+  d.inv = inv_of(s.scale);
+  d.found_inf = !__builtin_isfinite(sumsq);
+  d.t = s.t + 1;
+  d.skip = d.found_inf || groups_bad;
   if (groups_bad) s.error |= DSX_STATE_ERR_GROUPS;
-  const int ng = groups_bad ? 0 : grp.ngroups;
-  if (!skip) {
-    for (int k = 0; k < ng; ++k) {
-      const int32_t tk = t - grp.t_offset[k];
+  d.ng = groups_bad ? 0 : grp.ngroups;
+  if (!d.skip) {
+    for (int k = 0; k < d.ng; ++k) {
+      const int32_t tk = d.t - grp.t_offset[k];
       if (tk < 1 || tk > grp.bc_len) {
-        skip = true;
+        d.skip = true;
         s.error |= DSX_STATE_ERR_BC_TABLE;
       }
     }
   }
   // A coefficient armed by clip_grad_norm_ (dsx_clip_prepare) replaces the
   // configured clip for this one step, applied or skipped, and is consumed.
-  float coef = 1.0f;
-  if (ng > 0 && !skip) {
+  d.coef = 1.0f;
+  if (d.ng > 0 && !d.skip) {
     const DsxAdamwHyper& h0 = grp.hyper[0];
     if (s.clip_once)
-      coef = s.clip_once_coef;
-    else if (h0.max_grad_norm > 0.0 && norm > h0.max_grad_norm)
-      coef = (float)(h0.max_grad_norm / (norm + h0.clip_eps));
+      d.coef = s.clip_once_coef;
+    else if (h0.max_grad_norm > 0.0 && d.norm > h0.max_grad_norm)
+      d.coef = (float)(h0.max_grad_norm / (d.norm + h0.clip_eps));
   }
-  s.clip_once = 0;
-  for (int k = 0; k < nout; ++k) {
-    const bool live = k < ng;
-    DsxStepScalars o = {};
-    o.sumsq = sumsq;
-    o.norm = norm;
-    o.inv_scale = inv;
-    o.clip_coef = coef;
-    o.decay = 1.0f;
-    o.skip = (skip || !live) ? 1 : 0;
-    o.t = (skip ? s.t : t) - (live ? grp.t_offset[k] : 0);
-    if (!skip && live) {
-      const DsxAdamwHyper& hp = grp.hyper[k];
-      const int32_t tk = t - grp.t_offset[k];
-      const double bc1 = grp.bc_table[k][2 * (int64_t)(tk - 1)];
-      const double bc2s = grp.bc_table[k][2 * (int64_t)(tk - 1) + 1];
-      if (hp.weight_decay != 0.0) o.decay = (float)(1.0 - hp.lr * hp.weight_decay);
-      o.w1 = (float)(1.0 - hp.beta1);
-      o.w1c = 1.0f - o.w1;
-      o.b2 = (float)hp.beta2;
-      o.val2 = (float)(1.0 - hp.beta2);
-      o.eps = (float)hp.eps;
-      o.bc2s = (float)bc2s;
-      o.nss = (float)(-(hp.lr / bc1));
-    }
-    out[k] = o;
-  }
+  return d;
+}
 
-  if (found_inf) {
+// Group k's fp32 step scalars. Slots at or past the live groups get skip = 1,
+// so a K2 launched for them leaves its group unchanged rather than reusing an
+// older step's scalars.
+__device__ __forceinline__ DsxStepScalars record_bc(const Decision& d, const DsxState& s, const DsxGroupsDev& grp,
+                                                    int k, double sumsq, double bc1, double bc2s) {
+  const bool live = k < d.ng;
+  DsxStepScalars o = {};
+  o.sumsq = sumsq;
+  o.norm = d.norm;
+  o.inv_scale = d.inv;
+  o.clip_coef = d.coef;
+  o.decay = 1.0f;
+  o.skip = (d.skip || !live) ? 1 : 0;
+  o.t = (d.skip ? s.t : d.t) - (live ? grp.t_offset[k] : 0);
+  if (!d.skip && live) {
+    const DsxAdamwHyper& hp = grp.hyper[k];
+    if (hp.weight_decay != 0.0) o.decay = (float)(1.0 - hp.lr * hp.weight_decay);
+    o.w1 = (float)(1.0 - hp.beta1);
+    o.w1c = 1.0f - o.w1;
+    o.b2 = (float)hp.beta2;
+    o.val2 = (float)(1.0 - hp.beta2);
+    o.eps = (float)hp.eps;
+    o.bc2s = (float)bc2s;
+    o.nss = (float)(-(hp.lr / bc1));
+  }
+  return o;
+}
+
+// Group k's bias corrections for step t (1-based), or (1, 1) when t is out
+// of the table's range (decide() then skips the step). The table is read
+// through the constant address space, i.e. with scalar loads (t and k are
+// uniform; no kernel writes a bias-correction table).
+typedef const double __attribute__((address_space(4)))* ConstDoubles;
+
+__device__ __forceinline__ void bc_of(const DsxGroupsDev& grp, int k, int32_t t, double& bc1, double& bc2s) {
+  const int32_t tk = t - grp.t_offset[k];
+  bc1 = 1.0;
+  bc2s = 1.0;
+  if (tk >= 1 && tk <= grp.bc_len) {
+    const ConstDoubles row = (ConstDoubles)(uintptr_t)(grp.bc_table[k] + 2 * (int64_t)(tk - 1));
+    bc1 = row[0];
+    bc2s = row[1];
+  }
+}
+
+__device__ DsxStepScalars record(const Decision& d, const DsxState& s, const DsxGroupsDev& grp, int k,
+                                 double sumsq) {
+  double bc1 = 1.0, bc2s = 1.0;
+  if (!d.skip && k < d.ng) bc_of(grp, k, d.t, bc1, bc2s);
+  return record_bc(d, s, grp, k, sumsq, bc1, bc2s);
+}
+
+// The state after the step: counters, t, the loss scaler, the step's record
+// fields, and the entry values step_scale / step_t2.
+__device__ void advance(const Decision& d, DsxState& s, const DsxScalerConfig& scfg) {
+  const bool dynamic = scfg.mode == DSX_SCALE_DYNAMIC;
+  s.step_scale = s.scale;
+  s.step_t2 = 2 * s.t + (s.clip_once != 0 ? 1 : 0);
+  s.clip_once = 0;
+  if (d.found_inf) {
     s.overflow_count += 1;
     if (dynamic) {
       if (scfg.hysteresis <= 1 || s.hyst_left <= 1) {
@@ -628,8 +683,8 @@ __device__ void finalize_body(double sumsq, DsxState* __restrict__ state, const 
       }
       s.good_steps = 0;
     }
-  } else if (!skip) {
-    s.t = t;
+  } else if (!d.skip) {
+    s.t = d.t;
     if (dynamic) {
       s.good_steps += 1;
       if (s.good_steps >= scfg.window) {
@@ -641,8 +696,19 @@ __device__ void finalize_body(double sumsq, DsxState* __restrict__ state, const 
     }
   }
   s.iter += 1;
-  s.last_skip = skip ? 1 : 0;
-  s.last_norm = norm;
+  s.last_skip = d.skip ? 1 : 0;
+  s.last_norm = d.norm;
+}
+
+// Thread 0 only. Global part of a step (norm, skip, clip, t, scaler) once;
+// per-group fp32 scalars into out[0..nout).
+__device__ void finalize_body(double sumsq, DsxState* __restrict__ state, const DsxScalerConfig& scfg,
+                              const DsxGroupsDev& grp, bool groups_bad, int nout,
+                              DsxStepScalars* __restrict__ out) {
+  DsxState s = *state;
+  const Decision d = decide(sumsq, s, grp, groups_bad);
+  for (int k = 0; k < nout; ++k) out[k] = record(d, s, grp, k, sumsq);
+  advance(d, s, scfg);
   *state = s;
 }
 
@@ -787,6 +853,187 @@ __global__ __launch_bounds__(kBlock) void k2_traffic_probe(float* __restrict__ p
   k2_flat_body<GD, PD, U, NT, DRAIN, false>(p, m, v, p16, gv, n, scp);
 }
 
+// ---- K2 with the finalize folded in (two-launch step) ---------------------------
+// After a K1 launched with fold (block 0 recorded the entry scale, t and the
+// one-shot clip flag in step_scale / step_t2), every thread of this kernel
+// runs K0's decision itself: the same reduction of K1's partials
+// (reduce_partials' per-thread order and block_sum's tree, so the same bits)
+// and the same decide / record code on the entry values, giving the scalars
+// K0 would give. The launch with `writer` set (the step's first K2 launch)
+// has one more block, its last, which does no slot work: it reduces the
+// partials and decides the same way, then writes every group's record to
+// out[] and the state's updated fields, leaving step_scale / step_t2 and
+// clip_once_coef, the fields the other blocks read, untouched. (A block of
+// its own keeps that code's registers out of the slot blocks' path.) No block waits for another and nothing is counted
+// across blocks. Each thread issues its partials' loads first and its first
+// trip's slot loads next, so that waiting for the partials does not wait for
+// the slot loads, which stay in flight while the block reduces and decides;
+// the entry values and the bias corrections come through scalar loads, which
+// wait on neither. 1 <= nparts <= kFoldMaxParts (two partials per thread),
+// n >= 4.
+constexpr int kFoldParts = 2;
+constexpr int kFoldMaxParts = kFoldParts * kBlock;
+
+// block_sum's tree with its result in every thread (each adds the wave sums
+// in the order thread 0 does).
+__device__ __forceinline__ double block_sum_all(double x) {
+  __shared__ double lds[kWaves];
+  x = wave_sum(x);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = x;
+  __syncthreads();
+  double s = 0.0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) s += lds[w];
+  return s;
+}
+
+// The step scalars, equal in every lane, moved to scalar registers (so that
+// the slot loop holds them as K2 does, where they come from scalar loads).
+__device__ __forceinline__ float sgpr(float x) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+}
+
+__device__ __forceinline__ Sc uniform_sc(const Sc& a) {
+  Sc r;
+  r.inv = sgpr(a.inv); r.coef = sgpr(a.coef); r.decay = sgpr(a.decay);
+  r.w1 = sgpr(a.w1); r.w1c = sgpr(a.w1c); r.b2 = sgpr(a.b2); r.val2 = sgpr(a.val2);
+  r.eps = sgpr(a.eps); r.bc2s = sgpr(a.bc2s); r.nss = sgpr(a.nss);
+  r.small = __builtin_amdgcn_readfirstlane(a.small ? 1 : 0) != 0;
+  return r;
+}
+
+template <int GD, int PD, int U, bool NT>
+__global__ __launch_bounds__(kBlock) void k2_adamw_fold(float* __restrict__ p, float* __restrict__ m,
+                                                        float* __restrict__ v, uint16_t* __restrict__ p16,
+                                                        const void* __restrict__ gv, int64_t n,
+                                                        const double* __restrict__ partials, int32_t nparts,
+                                                        DsxState* state, DsxScalerConfig scfg, DsxGroupsDev grp, int32_t group,
+                                                        int32_t writer, DsxStepScalars* __restrict__ out) {
+  using G = Grad<GD>;
+  using GS = typename G::slot4;
+  if (writer && blockIdx.x == gridDim.x - 1) {
+    // The extra block of the writing launch: the step's records and state.
+    double x = 0.0;
+    for (int i = threadIdx.x; i < nparts; i += kBlock) x += partials[i];
+    const double sumsq = block_sum_all(x);
+    if (threadIdx.x == 0) {
+      DsxState f = *state;
+      const int32_t t2 = f.step_t2;
+      f.clip_once = t2 & 1;  // K1 consumed the live flag into step_t2
+      const Decision d = decide(sumsq, f, grp, false);
+      for (int k = 0; k < grp.ngroups; ++k) out[k] = record(d, f, grp, k, sumsq);
+      advance(d, f, scfg);
+      state->scale = f.scale;
+      state->good_steps = f.good_steps;
+      state->hyst_left = f.hyst_left;
+      state->t = f.t;
+      state->iter = f.iter;
+      state->overflow_count = f.overflow_count;
+      state->error = f.error;
+      state->last_skip = f.last_skip;
+      state->last_norm = f.last_norm;
+      state->clip_once = 0;
+    }
+    return;
+  }
+  // The entry values, read first (vector loads: `state` is written below).
+  int32_t t2 = state->step_t2;
+  float scale0 = state->step_scale, coef1 = state->clip_once_coef;
+  // Every vector load below is issued unconditionally (an index past the end
+  // reads the last element again, and the value is not used), so the number
+  // of loads in flight is the same on every path and waiting for the
+  // partials waits for them alone.
+  double pv[kFoldParts];
+#pragma unroll
+  for (int j = 0; j < kFoldParts; ++j) {
+    const int i = threadIdx.x + j * kBlock;
+    const double x = partials[i < nparts ? i : nparts - 1];
+    pv[j] = i < nparts ? x : 0.0;
+  }
+  f4* p4 = reinterpret_cast<f4*>(p);
+  f4* m4 = reinterpret_cast<f4*>(m);
+  f4* v4 = reinterpret_cast<f4*>(v);
+  u2* o2 = reinterpret_cast<u2*>(p16);
+  const GS* g4 = static_cast<const GS*>(gv);
+  const typename G::elem* g = static_cast<const typename G::elem*>(gv);
+  const bool cast = p16 != nullptr;
+  const int64_t nvec = n >> 2;
+  const int64_t stride = (int64_t)(gridDim.x - (writer ? 1 : 0)) * kBlock * U;  // the slot blocks
+  int64_t i0 = (int64_t)blockIdx.x * kBlock * U + threadIdx.x;
+  GS Gs[U];
+  f4 P[U], M[U], V[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int64_t i = i0 + (int64_t)u * kBlock;
+    i = i < nvec ? i : nvec - 1;  // nvec >= 1 (n >= 4 on this path)
+    Gs[u] = ld<NT>(g4 + i);
+    P[u] = ld<NT>(p4 + i);
+    M[u] = ld<NT>(m4 + i);
+    V[u] = ld<NT>(v4 + i);
+  }
+  // After the slot loads are issued: the entry values (the oldest loads, so
+  // waiting for them waits for nothing else), then this group's bias
+  // corrections for t + 1 through scalar loads.
+  asm volatile("" : "+v"(t2), "+v"(scale0), "+v"(coef1));
+  DsxState s = {};
+  s.scale = scale0;
+  t2 = __builtin_amdgcn_readfirstlane(t2);
+  s.t = t2 >> 1;
+  s.clip_once = t2 & 1;
+  s.clip_once_coef = coef1;
+  double bc1, bc2s;
+  bc_of(grp, group, s.t + 1, bc1, bc2s);
+  // The slot loads issue before the first use of a partial.
+  asm volatile("" : "+v"(pv[0]), "+v"(pv[1]));
+  // reduce_partials' order: each thread adds its partials in index order
+  // (the zeros past nparts add nothing to a sum of squares), then the tree.
+  double x = 0.0;
+#pragma unroll
+  for (int j = 0; j < kFoldParts; ++j) x += pv[j];
+  const double sumsq = block_sum_all(x);
+  const Decision d = decide(sumsq, s, grp, false);
+  if (!d.skip) {
+    const Sc sc = uniform_sc(load_sc(record_bc(d, s, grp, group, sumsq, bc1, bc2s)));
+    for (;;) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = i0 + (int64_t)u * kBlock;
+        if (i < nvec) {
+          float gf[4];
+          G::four(Gs[u], gf);
+          f4 pp = P[u], mm = M[u], vv = V[u];
+          adamw4(gf, pp, mm, vv, sc);
+          st<NT>(p4 + i, pp);
+          st<NT>(m4 + i, mm);
+          st<NT>(v4 + i, vv);
+          if (cast) st<NT>(o2 + i, pack4<PD>(pp));
+        }
+      }
+      i0 += stride;
+      if (i0 >= nvec) break;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        int64_t i = i0 + (int64_t)u * kBlock;
+        i = i < nvec ? i : nvec - 1;
+        Gs[u] = ld<NT>(g4 + i);
+        P[u] = ld<NT>(p4 + i);
+        M[u] = ld<NT>(m4 + i);
+        V[u] = ld<NT>(v4 + i);
+      }
+    }
+    const int64_t tail0 = nvec << 2;
+    const int64_t gt = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (gt < n - tail0) {
+      const int64_t e = tail0 + gt;
+      float pe = p[e], me = m[e], ve = v[e];
+      adamw_elt(G::one(g[e]), pe, me, ve, sc);
+      p[e] = pe; m[e] = me; v[e] = ve;
+      if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
+    }
+  }
+}
+
 // ---- K3: ragged lists ----------------------------------------------------------
 
 template <int GD>
@@ -907,11 +1154,12 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __r
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 template <int GD>
-void launch_k1(const void* g, int64_t n, const DsxState* st, double* partials, int nparts, hipStream_t s) {
+void launch_k1(const void* g, int64_t n, const DsxState* st, double* partials, int nparts, DsxState* fold,
+               hipStream_t s) {
   if (g_tune.nontemporal)
-    hipLaunchKernelGGL((k1_unscale_norm<GD, 4, true>), dim3(nparts), dim3(kBlock), 0, s, g, n, st, partials);
+    hipLaunchKernelGGL((k1_unscale_norm<GD, 4, true>), dim3(nparts), dim3(kBlock), 0, s, g, n, st, partials, fold);
   else
-    hipLaunchKernelGGL((k1_unscale_norm<GD, 4, false>), dim3(nparts), dim3(kBlock), 0, s, g, n, st, partials);
+    hipLaunchKernelGGL((k1_unscale_norm<GD, 4, false>), dim3(nparts), dim3(kBlock), 0, s, g, n, st, partials, fold);
 }
 
 template <int GD, int PD, int U, bool NT, bool DRAIN>
@@ -1016,11 +1264,11 @@ int check_parts(const double* partials, int32_t nparts) {
 }
 
 int do_unscale_norm(const void* g, int gdt, int64_t n, const DsxState* st, double* partials, int32_t nparts,
-                    hipStream_t s) {
+                    hipStream_t s, DsxState* fold = nullptr) {
   switch (gdt) {
-    case DSX_BF16: launch_k1<DSX_BF16>(g, n, st, partials, nparts, s); break;
-    case DSX_F16: launch_k1<DSX_F16>(g, n, st, partials, nparts, s); break;
-    default: launch_k1<DSX_F32>(g, n, st, partials, nparts, s); break;
+    case DSX_BF16: launch_k1<DSX_BF16>(g, n, st, partials, nparts, fold, s); break;
+    case DSX_F16: launch_k1<DSX_F16>(g, n, st, partials, nparts, fold, s); break;
+    default: launch_k1<DSX_F32>(g, n, st, partials, nparts, fold, s); break;
   }
   return launch_status("dsx_unscale_norm");
 }
@@ -1079,6 +1327,61 @@ int do_adamw_flat(float* p, float* m, float* v, void* p16, int pdt, const void* 
   if (n == 0) return DSX_OK;
   k2_dispatch(p, m, v, p16, pdt, g, gdt, n, sc, s, false);
   return launch_status("dsx_adamw_flat");
+}
+
+// The folded K2 over one group's range: the one-trip grid of K2 (2 slots per
+// thread, at most kK2OneTripPerCu blocks per CU; the kernel strides over what
+// one trip does not cover).
+template <int GD, int PD>
+void launch_k2_fold(float* p, float* m, float* v, void* p16, const void* g, int64_t n, const double* partials,
+                    int32_t nparts, DsxState* state, const DsxScalerConfig& scfg, const DsxGroupsDev& grp,
+                    int group, bool writer, DsxStepScalars* out, hipStream_t s) {
+  constexpr int U = 2;
+  const int64_t slots = n >> 2;
+  int64_t blocks = ceil_div(slots > 0 ? slots : 1, (int64_t)kBlock * U);
+  const int64_t cap = (int64_t)cu_count() * kK2OneTripPerCu;
+  if (blocks > cap) blocks = cap;
+  if (writer) blocks += 1;  // the block that writes the records and the state
+  uint16_t* o = static_cast<uint16_t*>(p16);
+  const int32_t w = writer ? 1 : 0;
+  if (g_tune.nontemporal)
+    hipLaunchKernelGGL((k2_adamw_fold<GD, PD, U, true>), dim3((unsigned)blocks), dim3(kBlock), 0, s, p, m, v, o, g,
+                       n, partials, nparts, state, scfg, grp, group, w, out);
+  else
+    hipLaunchKernelGGL((k2_adamw_fold<GD, PD, U, false>), dim3((unsigned)blocks), dim3(kBlock), 0, s, p, m, v, o, g,
+                       n, partials, nparts, state, scfg, grp, group, w, out);
+}
+
+template <int GD>
+void k2_fold_by_param(int pd, float* p, float* m, float* v, void* p16, const void* g, int64_t n,
+                      const double* partials, int32_t nparts, DsxState* state, const DsxScalerConfig& scfg,
+                      const DsxGroupsDev& grp, int group, bool writer, DsxStepScalars* out, hipStream_t s) {
+  if (pd == DSX_BF16)
+    launch_k2_fold<GD, DSX_BF16>(p, m, v, p16, g, n, partials, nparts, state, scfg, grp, group, writer, out, s);
+  else
+    launch_k2_fold<GD, DSX_F16>(p, m, v, p16, g, n, partials, nparts, state, scfg, grp, group, writer, out, s);
+}
+
+bool fold_applies(int64_t n, int32_t nparts) {
+  return g_tune.fold_max_elems > 0 && n >= 4 && n <= g_tune.fold_max_elems && nparts <= kFoldMaxParts;
+}
+
+int do_adamw_fold(float* p, float* m, float* v, void* p16, int pdt, const void* g, int gdt, int64_t n,
+                  const double* partials, int32_t nparts, DsxState* state, const DsxScalerConfig& scfg,
+                  const DsxGroupsDev& grp, int group, bool writer, DsxStepScalars* out, hipStream_t s) {
+  const int pd = p16 ? pdt : DSX_F16;
+  switch (gdt) {
+    case DSX_BF16:
+      k2_fold_by_param<DSX_BF16>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, grp, group, writer, out, s);
+      break;
+    case DSX_F16:
+      k2_fold_by_param<DSX_F16>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, grp, group, writer, out, s);
+      break;
+    default:
+      k2_fold_by_param<DSX_F32>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, grp, group, writer, out, s);
+      break;
+  }
+  return launch_status("dsx_adamw_flat (finalize folded in)");
 }
 
 template <int GD, int PD, int U>
@@ -1169,8 +1472,15 @@ int zero_step_flat(float* master, float* m, float* v, void* p16, int pdt, const 
                    DsxState* state, const DsxScalerConfig& scaler, const DsxAdamwHyper& hyper,
                    const double* bc_table, int32_t bc_len, double* partials, int32_t nparts, DsxStepScalars* out,
                    hipStream_t s) {
+  const DsxGroupsDev grp = one_group(hyper, bc_table, bc_len);
+  if (fold_applies(n, nparts)) {
+    int rc = do_unscale_norm(g, gdt, n, state, partials, nparts, s, state);
+    if (!rc) rc = do_adamw_fold(master, m, v, p16, pdt, g, gdt, n, partials, nparts, state, scaler, grp, 0, true,
+                                out, s);
+    return rc;
+  }
   int rc = do_unscale_norm(g, gdt, n, state, partials, nparts, s);
-  if (!rc) rc = do_finalize(partials, nparts, state, scaler, one_group(hyper, bc_table, bc_len), out, s);
+  if (!rc) rc = do_finalize(partials, nparts, state, scaler, grp, out, s);
   if (!rc) rc = do_adamw_flat(master, m, v, p16, pdt, g, gdt, n, out, s);
   return rc;
 }
@@ -1240,6 +1550,12 @@ int dsx_set_tuning_k2_chunk(int64_t chunk_elems) {
   if (chunk_elems > 0 && chunk_elems < (int64_t(1) << 20))
     return fail(DSX_EINVAL, "chunk_elems must be 0 or at least 2^20");
   g_tune.k2_chunk_elems = chunk_elems;
+  return DSX_OK;
+}
+
+int dsx_set_tuning_fold(int64_t max_elems) {
+  if (max_elems < 0) return fail(DSX_EINVAL, "max_elems must be >= 0 (0: three launches always)");
+  g_tune.fold_max_elems = max_elems;
   return DSX_OK;
 }
 
@@ -1509,17 +1825,33 @@ int dsx_zero_step_plan(const DsxFlatPlan* plan, const DsxGroupsDev* groups, void
     prev = end;
   }
   hipStream_t s = as_stream(stream);
-  rc = do_unscale_norm(P.grad, P.grad_dtype, P.n, P.state, P.partials, P.nparts, s);
-  if (!rc) rc = do_finalize(P.partials, P.nparts, P.state, P.scaler, G, P.out, s);
+  // Two launches (K1, then each group's K2 with the finalize folded in, the
+  // first of them writing the state) or three (K1, K0, each group's K2).
+  bool fold = fold_applies(P.n, P.nparts);
+  prev = 0;
+  for (int k = 0; fold && k < P.ngroups; ++k) {
+    const int64_t len = P.group_end[k] - prev;
+    prev = P.group_end[k];
+    if (len > 0 && len < 4) fold = false;  // the folded K2 takes at least one 4-element slot
+  }
+  rc = do_unscale_norm(P.grad, P.grad_dtype, P.n, P.state, P.partials, P.nparts, s, fold ? P.state : nullptr);
+  if (!rc && !fold) rc = do_finalize(P.partials, P.nparts, P.state, P.scaler, G, P.out, s);
   const int64_t gsz = P.grad_dtype == DSX_F32 ? 4 : 2;
+  bool writer = true;
   prev = 0;
   for (int k = 0; !rc && k < P.ngroups; ++k) {
     const int64_t a = prev, b = P.group_end[k];
     prev = b;
     if (b == a) continue;
     void* p16 = P.param16 ? static_cast<void*>(static_cast<uint16_t*>(P.param16) + a) : nullptr;
-    rc = do_adamw_flat(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype,
-                       static_cast<const char*>(P.grad) + a * gsz, P.grad_dtype, b - a, P.out + k, s);
+    const void* ga = static_cast<const char*>(P.grad) + a * gsz;
+    if (fold)
+      rc = do_adamw_fold(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype, ga, P.grad_dtype, b - a,
+                         P.partials, P.nparts, P.state, P.scaler, G, k, writer, P.out, s);
+    else
+      rc = do_adamw_flat(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype, ga, P.grad_dtype, b - a,
+                         P.out + k, s);
+    writer = false;
   }
   return rc;
 }

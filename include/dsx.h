@@ -94,7 +94,8 @@ typedef struct DsxState {
   double  last_norm;      /* global grad norm seen by the last finalize      */
   float   clip_once_coef; /* clip coefficient armed by dsx_clip_prepare      */
   int32_t clip_once;      /* 1: the next finalize applies clip_once_coef     */
-  int64_t reserved;
+  float   step_scale;     /* scale as the last step began                    */
+  int32_t step_t2;        /* 2 t + clip_once as the last step began          */
 } DsxState;
 
 /* Loss-scaler configuration (by value). */
@@ -191,6 +192,17 @@ int dsx_set_tuning_k2(int k2_cu_eighths, int drain);
  * dsx_traffic_probe_flat. chunk_elems must be 0 or >= 2^20. No counterpart
  * in the reference. */
 int dsx_set_tuning_k2_chunk(int64_t chunk_elems);
+
+/* One-call steps (dsx_zero_step_flat, dsx_zero_step_plan and the no-
+ * allocation variant) over at most max_elems elements, with at most 512
+ * partials and every nonempty group at least 4 elements, run as two
+ * launches: K1, which also records the entry scale, t and one-shot clip flag
+ * in the state's step_scale / step_t2, and K2 with K0's finalize folded in
+ * (every K2 block reduces the partials and decides the step itself, with
+ * K0's code and order, so the bits are K0's; one extra block writes the
+ * state and the step records). 0 always runs K1, K0, K2. Default 2^24 (the
+ * end of K2's one-trip grid on 256 CUs). No counterpart in the reference. */
+int dsx_set_tuning_fold(int64_t max_elems);
 
 /* The same for K3 (dsx_adamw_multi): blocks per CU (the grid is also capped
  * at the chunk count; 0, the default, picks the shape from the chunk count,

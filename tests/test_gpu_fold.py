@@ -1,0 +1,279 @@
+"""The two-launch step against the three-launch step, through the C ABI.
+
+One-call steps (dsx_zero_step_flat, dsx_zero_step_plan) of at most 2^24
+elements with at most 512 partials run as K1 followed by K2 with K0's
+finalize folded in (every K2 block reduces the partials and decides the step
+with K0's code; one block writes the state and the step records). With
+dsx_set_tuning_fold(0) the same calls run K1, K0, K2. On the same inputs the
+two must agree bit for bit, step after step: master, exp_avg, exp_avg_sq,
+param16, the whole 64-byte device state and the step record. The steps cover
+an overflow skip with a scale back-off, scale growth (window 2), a one-shot
+clip armed by dsx_norm_partials + dsx_clip_prepare, partition tails (n = 4,
+5, 1001, odd sizes), the largest partial count the fold takes (512) and the
+first it does not, a grid that strides (the fold widened past K2's one-trip
+grid), fp32 grads with bf16 params, and bf16 without a scaler. The mlp case
+is also checked against the oracle (ZeroStepOracle) at every step."""
+from __future__ import annotations
+
+import ctypes
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import BF16, F16, torch16_to_np
+
+pytestmark = pytest.mark.gpu
+
+F32 = 0
+FOLD_DEFAULT = 1 << 24
+
+# (id, n, grad dtype, param dtype, scaler mode, nparts (None: the library's), fold bound)
+CASES = [
+    ("mlp-f16-dynamic", 1_863_690, F16, F16, "dynamic", None, FOLD_DEFAULT),
+    ("tail-bf16", 1001, BF16, BF16, "none", None, FOLD_DEFAULT),
+    ("n4", 4, F16, F16, "dynamic", 1, FOLD_DEFAULT),
+    ("n5", 5, BF16, BF16, "none", 3, FOLD_DEFAULT),
+    ("parts-512", 300_001, F16, F16, "dynamic", 512, FOLD_DEFAULT),
+    ("parts-513", 300_001, F16, F16, "dynamic", 513, FOLD_DEFAULT),
+    ("strided", 40_000_003, BF16, BF16, "none", None, 1 << 26),
+    ("f32-grads", 123_457, F32, BF16, "none", None, FOLD_DEFAULT),
+]
+
+
+def _say(msg):
+    print(f"[gpu-test] {msg}", file=sys.stderr, flush=True)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _tdt(dt):
+    import torch
+    return {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}[dt]
+
+
+class _Side:
+    def __init__(self, gpu, master, pdt, gdt, n, scaler):
+        import torch
+        from distributedspeed_amd import ops
+        self.p = master.clone()
+        self.m = torch.zeros_like(master)
+        self.v = torch.zeros_like(master)
+        self.p16 = master.to(_tdt(pdt))
+        self.g = torch.zeros(n, dtype=_tdt(gdt), device=gpu)
+        self.state = ops.new_state(gpu, scaler.init_scale if scaler.mode != "none" else 1.0,
+                                   scaler.hysteresis if scaler.mode == "dynamic" else 1)
+        self.out = torch.zeros(ops.SCALARS_BYTES, dtype=torch.uint8, device=gpu)
+
+    def bits(self):
+        import torch
+        return {"master": self.p.view(torch.int32).cpu(), "exp_avg": self.m.view(torch.int32).cpu(),
+                "exp_avg_sq": self.v.view(torch.int32).cpu(), "param16": self.p16.view(torch.int16).cpu(),
+                "state": self.state.cpu(), "record": self.out.cpu()}
+
+
+def _arm_clip(side, n, gdt, max_norm, partials, stream):
+    """clip_grad_norm_(max_norm, 2) through the C ABI: norm partials, then
+    the one-shot coefficient armed in the state."""
+    import torch
+    from distributedspeed_amd import _lib
+    nparts = partials.numel()
+    norm = torch.zeros(1, dtype=torch.float64, device=side.state.device)
+    _lib.call("dsx_norm_partials", _ptr(side.g), gdt, ctypes.c_int64(n), _ptr(side.state), ctypes.c_double(2.0),
+              _ptr(partials), nparts, stream)
+    _lib.call("dsx_clip_prepare", _ptr(partials), nparts, ctypes.c_double(2.0), ctypes.c_double(max_norm),
+              ctypes.c_double(1e-6), _ptr(side.state), _ptr(norm), stream)
+    return norm
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_two_launch_step_matches_three_launches(gpu, case):
+    import torch
+    from distributedspeed_amd import _lib, ops
+    from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
+    cid, n, gdt, pdt, mode, nparts, fold_max = case
+    scale0 = 2.0 ** 12 if mode == "dynamic" else 1.0
+    scaler = (ScalerConfig(mode="dynamic", init_scale=scale0, window=2, hysteresis=1) if mode == "dynamic"
+              else ScalerConfig(mode="none"))
+    hyper = AdamWHyper(lr=1e-3, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    gen = torch.Generator(device=gpu).manual_seed(1000 + n % 997)
+    master = (torch.randn(n, generator=gen, device=gpu) * 0.02).float()
+    a = _Side(gpu, master, pdt, gdt, n, scaler)  # the library's choice (two launches where the fold applies)
+    b = _Side(gpu, master, pdt, gdt, n, scaler)  # three launches
+    bc = BiasCorrectionTable(gpu, hyper.beta1, hyper.beta2)
+    stream = ops.stream_of(gpu)
+    nparts = nparts or ops.suggest_partials(n)
+    parts_a = torch.zeros(nparts, dtype=torch.float64, device=gpu)
+    parts_b = torch.zeros(nparts, dtype=torch.float64, device=gpu)
+    oracle_run = cid == "mlp-f16-dynamic"
+    if oracle_run:
+        from oracle import oracle as O
+        orc = O.ZeroStepOracle(master.cpu().numpy().copy(), np.zeros(n, np.float32), np.zeros(n, np.float32),
+                               torch16_to_np(a.p16).copy(), pdt, gdt,
+                               O.Hyper(lr=1e-3, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1,
+                                       max_grad_norm=1.0),
+                               O.LossScalerSpec(scale=scale0, window=2, hysteresis=1))
+    try:
+        for step in range(6):
+            scale = float(ops.read_state(a.state).scale)
+            g = (torch.randn(n, generator=gen, device=gpu) * 1e-3 * scale).to(_tdt(gdt))
+            if step == 1:
+                g[n // 2] = float("inf")
+            a.g.copy_(g)
+            b.g.copy_(g)
+            clip = None
+            if step == 3:  # a one-shot clip far below the norm
+                na = _arm_clip(a, n, gdt, 1e-4, parts_a, stream)
+                _arm_clip(b, n, gdt, 1e-4, parts_b, stream)
+                clip = float(na.item())
+            _say(f"fold case={cid} n={n} nparts={nparts} step={step}")
+            _lib.call("dsx_set_tuning_fold", ctypes.c_int64(fold_max))
+            _lib.call("dsx_zero_step_flat", _ptr(a.p), _ptr(a.m), _ptr(a.v), _ptr(a.p16), pdt, _ptr(a.g), gdt,
+                      ctypes.c_int64(n), _ptr(a.state), scaler.to_c(), hyper.to_c(), _ptr(bc.table), bc.length,
+                      _ptr(parts_a), nparts, _ptr(a.out), stream)
+            _lib.call("dsx_set_tuning_fold", ctypes.c_int64(0))
+            _lib.call("dsx_zero_step_flat", _ptr(b.p), _ptr(b.m), _ptr(b.v), _ptr(b.p16), pdt, _ptr(b.g), gdt,
+                      ctypes.c_int64(n), _ptr(b.state), scaler.to_c(), hyper.to_c(), _ptr(bc.table), bc.length,
+                      _ptr(parts_b), nparts, _ptr(b.out), stream)
+            torch.cuda.synchronize()
+            xa, xb = a.bits(), b.bits()
+            for name in xa:
+                assert torch.equal(xa[name], xb[name]), \
+                    f"step {step}: {name} differs ({int((xa[name] != xb[name]).sum())} elements)"
+            st = ops.read_state(a.state)
+            assert st.error == 0 and st.clip_once == 0
+            assert st.last_skip == (1 if step == 1 else 0), step
+            if oracle_run:
+                g16 = torch16_to_np(g)
+                coef = None if clip is None else O.clip_once_coef(clip, 1e-4)
+                r = orc.step(g16, clip_once=coef)
+                assert r.skipped == (step == 1) and st.scale == r.scale_next
+                assert np.array_equal(a.p.cpu().numpy().view(np.uint32), orc.p.view(np.uint32)), step
+                assert np.array_equal(a.m.cpu().numpy().view(np.uint32), orc.m.view(np.uint32)), step
+                assert np.array_equal(a.v.cpu().numpy().view(np.uint32), orc.v.view(np.uint32)), step
+                assert np.array_equal(torch16_to_np(a.p16), orc.p16), step
+        st = ops.read_state(a.state)
+        assert st.t == 5 and st.overflow_count == 1
+        if mode == "dynamic":  # back-off at step 1, growth after two clean steps, twice
+            assert st.scale == scale0 / 2 * 4
+    finally:
+        _lib.call("dsx_set_tuning_fold", ctypes.c_int64(FOLD_DEFAULT))
+
+
+def _plan_step(side, n, gdt, pdt, scaler, hypers, tables, ends, parts, stream):
+    """dsx_zero_step_plan over `side` with groups ending at `ends`."""
+    from distributedspeed_amd import _lib
+    P = _lib.DsxFlatPlan()
+    P.master, P.exp_avg, P.exp_avg_sq = side.p.data_ptr(), side.m.data_ptr(), side.v.data_ptr()
+    P.param16, P.grad, P.n = side.p16.data_ptr(), side.g.data_ptr(), n
+    P.param_dtype, P.grad_dtype = pdt, gdt
+    P.state, P.partials, P.out = side.state.data_ptr(), parts.data_ptr(), side.out.data_ptr()
+    P.nparts, P.ngroups, P.scaler = parts.numel(), len(ends), scaler.to_c()
+    G = _lib.DsxGroupsDev()
+    for k, (h, bc, e) in enumerate(zip(hypers, tables, ends)):
+        P.group_end[k] = e
+        G.hyper[k] = h.to_c()
+        G.bc_table[k] = bc.table.data_ptr()
+        G.t_offset[k] = 0
+    G.ngroups, G.bc_len = len(ends), min(bc.length for bc in tables)
+    _lib.call("dsx_zero_step_plan", ctypes.byref(P), ctypes.byref(G), stream)
+
+
+# group ends: the last group of 3 elements is one the fold does not take
+# (three launches on both sides); the others fold, with an empty group
+# between two nonempty ones (the first nonempty group's K2 writes the state).
+PLAN_CASES = [("fold", [1000, 1000, 2005]), ("tiny-last-group", [1000, 1000, 1003]), ("empty-first", [0, 2000])]
+
+
+@pytest.mark.parametrize("pcase", PLAN_CASES, ids=[c[0] for c in PLAN_CASES])
+def test_plan_two_launch_step_matches_three_launches(gpu, pcase):
+    import torch
+    from distributedspeed_amd import _lib, ops
+    from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
+    cid, ends = pcase
+    n, gdt, pdt = ends[-1], F16, F16
+    scaler = ScalerConfig(mode="dynamic", init_scale=2.0 ** 10, window=3, hysteresis=2)
+    hypers = [AdamWHyper(lr=1e-3, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=0.5),
+              AdamWHyper(lr=5e-3, beta1=0.8, beta2=0.99, eps=1e-6, weight_decay=0.0, max_grad_norm=0.5),
+              AdamWHyper(lr=2e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, max_grad_norm=0.5)][:len(ends)]
+    tables = [BiasCorrectionTable(gpu, h.beta1, h.beta2) for h in hypers]
+    gen = torch.Generator(device=gpu).manual_seed(31)
+    master = (torch.randn(n, generator=gen, device=gpu) * 0.05).float()
+    a, b = _Side(gpu, master, pdt, gdt, n, scaler), _Side(gpu, master, pdt, gdt, n, scaler)
+    a.out = torch.zeros(ops.SCALARS_BYTES * len(ends), dtype=torch.uint8, device=gpu)
+    b.out = torch.zeros(ops.SCALARS_BYTES * len(ends), dtype=torch.uint8, device=gpu)
+    stream = ops.stream_of(gpu)
+    nparts = ops.suggest_partials(n)
+    parts_a = torch.zeros(nparts, dtype=torch.float64, device=gpu)
+    parts_b = torch.zeros(nparts, dtype=torch.float64, device=gpu)
+    try:
+        for step in range(10):
+            scale = float(ops.read_state(a.state).scale)
+            g = (torch.randn(n, generator=gen, device=gpu) * 1e-2 * scale).half()
+            if step in (2, 3):  # two overflows: hysteresis 2 tolerates the first
+                g[n - 1] = float("nan")
+            a.g.copy_(g)
+            b.g.copy_(g)
+            if step == 6:
+                _arm_clip(a, n, gdt, 0.01, parts_a, stream)
+                _arm_clip(b, n, gdt, 0.01, parts_b, stream)
+            _say(f"fold plan case={cid} ends={ends} step={step}")
+            _lib.call("dsx_set_tuning_fold", ctypes.c_int64(FOLD_DEFAULT))
+            _plan_step(a, n, gdt, pdt, scaler, hypers, tables, ends, parts_a, stream)
+            _lib.call("dsx_set_tuning_fold", ctypes.c_int64(0))
+            _plan_step(b, n, gdt, pdt, scaler, hypers, tables, ends, parts_b, stream)
+            torch.cuda.synchronize()
+            xa, xb = a.bits(), b.bits()
+            for name in xa:
+                assert torch.equal(xa[name], xb[name]), f"step {step}: {name} differs"
+        st = ops.read_state(a.state)
+        assert st.t == 8 and st.overflow_count == 2 and st.error == 0
+    finally:
+        _lib.call("dsx_set_tuning_fold", ctypes.c_int64(FOLD_DEFAULT))
+
+
+def test_optimizer_with_empty_group_matches_three_launches(gpu):
+    """The drop-in optimizer's one-call step with an empty parameter group
+    between two others, against three launches (track_skips keeps them
+    separate) over 12 steps with a NaN overflow and a one-shot clip."""
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    shapes = [(130, 7), (64, 33), (40, 9)]
+    torch.manual_seed(5)
+    init = [torch.randn(s) * 0.05 for s in shapes]
+
+    def build(track):
+        ps = [torch.nn.Parameter(t.clone().to(gpu)) for t in init]
+        groups = [{"params": ps[:1]}, {"params": [], "lr": 5e-3}, {"params": ps[1:], "lr": 2e-3}]
+        opt = AdamWOptimizer(groups, lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1, max_grad_norm=0.5,
+                             param_dtype=torch.float16, device=gpu,
+                             loss_scaler=ScalerConfig(mode="dynamic", init_scale=2.0 ** 8, window=3, hysteresis=1))
+        opt.track_skips(track)
+        return opt
+
+    a, b = build(False), build(True)
+    assert a._plan is not None
+    gen = torch.Generator(device=gpu).manual_seed(6)
+    _say("fold: optimizer with an empty group")
+    for step in range(12):
+        g = (torch.randn(a.flat.numel, device=gpu, generator=gen) * 1e-2 * 256).half()
+        if step == 4:
+            g[7] = float("nan")
+        a.flat.grad.copy_(g)
+        b.flat.grad.copy_(g)
+        if step == 8:
+            assert torch.equal(a.clip_grad_norm_(0.01), b.clip_grad_norm_(0.01))
+        a.step()
+        b.step()
+    torch.cuda.synchronize()
+    for name in ("master", "exp_avg", "exp_avg_sq", "param16"):
+        x, y = getattr(a.flat, name), getattr(b.flat, name)
+        assert torch.equal(x.view(torch.int16 if x.element_size() == 2 else torch.int32),
+                           y.view(torch.int16 if y.element_size() == 2 else torch.int32)), name
+    sa, sb = a.read_state(), b.read_state()
+    assert bytes(sa) == bytes(sb)
+    assert sa.t == 11 and sa.overflow_count == 1 and sa.error == 0 and not math.isnan(sa.last_norm)
