@@ -110,6 +110,7 @@ SIGNATURES = {
     "dsx_zero_step_flat": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P, DsxScalerConfig,
                                       DsxAdamwHyper, _P, _c.c_int32, _P, _c.c_int32, _P, _P]),
     "dsx_zero_step_plan": (_c.c_int, [_P, _P, _P]),
+    "dsx_zero_step_dev": (_c.c_int, [_P, _P, _P]),
     "dsx_zero_step_flat_noalloc": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _P, _c.c_int, _c.c_int64, _P,
                                               DsxScalerConfig, DsxAdamwHyper, _P, _c.c_int32, _c.c_int32, _P, _P]),
     "dsx_unscale_norm_multi": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _P, _P, _c.c_int32, _P]),

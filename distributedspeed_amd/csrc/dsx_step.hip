@@ -27,6 +27,7 @@
 #include <math.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "dsx.h"
 
@@ -700,6 +701,16 @@ __device__ void advance(const Decision& d, DsxState& s, const DsxScalerConfig& s
   s.last_norm = d.norm;
 }
 
+// A group block read from device memory fails these checks when its group
+// count is out of range or a group's inputs are (the host cannot check it at
+// launch in the graph form).
+__device__ __forceinline__ bool groups_bad_dev(const DsxGroupsDev& grp, int32_t max_groups) {
+  bool bad = grp.ngroups < 1 || grp.ngroups > max_groups || grp.ngroups > DSX_MAX_GROUPS || grp.bc_len < 0;
+  for (int k = 0; !bad && k < grp.ngroups; ++k)
+    bad = !hyper_ok(grp.hyper[k]) || grp.t_offset[k] < 0 || (grp.bc_len > 0 && grp.bc_table[k] == nullptr);
+  return bad;
+}
+
 // Thread 0 only. Global part of a step (norm, skip, clip, t, scaler) once;
 // per-group fp32 scalars into out[0..nout).
 __device__ void finalize_body(double sumsq, DsxState* __restrict__ state, const DsxScalerConfig& scfg,
@@ -735,10 +746,7 @@ __global__ __launch_bounds__(kBlock) void k0_finalize_dev(const double* __restri
   if (threadIdx.x != 0) return;
   // read in place: a copy of the 1112-byte block would live in scratch memory
   const DsxGroupsDev& grp = *gp;
-  bool bad = grp.ngroups < 1 || grp.ngroups > max_groups || grp.ngroups > DSX_MAX_GROUPS || grp.bc_len < 0;
-  for (int k = 0; !bad && k < grp.ngroups; ++k)
-    bad = !hyper_ok(grp.hyper[k]) || grp.t_offset[k] < 0 || (grp.bc_len > 0 && grp.bc_table[k] == nullptr);
-  finalize_body(sumsq, state, scfg, grp, bad, max_groups, out);
+  finalize_body(sumsq, state, scfg, grp, groups_bad_dev(grp, max_groups), max_groups, out);
 }
 
 // Writes a group block passed by value (through the kernel-argument
@@ -903,13 +911,28 @@ __device__ __forceinline__ Sc uniform_sc(const Sc& a) {
   return r;
 }
 
-template <int GD, int PD, int U, bool NT>
+// The group block gb: a DsxGroupsDev kernel argument checked on the host
+// (the eager form; the writer writes its ngroups records), or a pointer to
+// the block in device memory (the graph form), checked here as
+// k0_finalize_dev checks it -- a bad block skips the step with
+// DSX_STATE_ERR_GROUPS set -- with records for max_groups slots. (One kernel
+// template for both, with the body inline: as a shared function the compiler
+// gave it more registers than K2's occupancy allows.)
+__device__ __forceinline__ const DsxGroupsDev& group_block(const DsxGroupsDev& g) { return g; }
+__device__ __forceinline__ const DsxGroupsDev& group_block(const DsxGroupsDev* g) { return *g; }
+
+template <int GD, int PD, int U, bool NT, typename GB>
 __global__ __launch_bounds__(kBlock) void k2_adamw_fold(float* __restrict__ p, float* __restrict__ m,
                                                         float* __restrict__ v, uint16_t* __restrict__ p16,
                                                         const void* __restrict__ gv, int64_t n,
                                                         const double* __restrict__ partials, int32_t nparts,
-                                                        DsxState* state, DsxScalerConfig scfg, DsxGroupsDev grp, int32_t group,
-                                                        int32_t writer, DsxStepScalars* __restrict__ out) {
+                                                        DsxState* state, DsxScalerConfig scfg, GB gb,
+                                                        int32_t max_groups, int32_t group, int32_t writer,
+                                                        DsxStepScalars* __restrict__ out) {
+  constexpr bool DEV = std::is_pointer<GB>::value;
+  const DsxGroupsDev& grp = group_block(gb);
+  const bool groups_bad = DEV ? groups_bad_dev(grp, max_groups) : false;
+  const int nout = DEV ? max_groups : grp.ngroups;
   using G = Grad<GD>;
   using GS = typename G::slot4;
   if (writer && blockIdx.x == gridDim.x - 1) {
@@ -921,8 +944,8 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_fold(float* __restrict__ p, f
       DsxState f = *state;
       const int32_t t2 = f.step_t2;
       f.clip_once = t2 & 1;  // K1 consumed the live flag into step_t2
-      const Decision d = decide(sumsq, f, grp, false);
-      for (int k = 0; k < grp.ngroups; ++k) out[k] = record(d, f, grp, k, sumsq);
+      const Decision d = decide(sumsq, f, grp, groups_bad);
+      for (int k = 0; k < nout; ++k) out[k] = record(d, f, grp, k, sumsq);
       advance(d, f, scfg);
       state->scale = f.scale;
       state->good_steps = f.good_steps;
@@ -982,8 +1005,8 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_fold(float* __restrict__ p, f
   s.t = t2 >> 1;
   s.clip_once = t2 & 1;
   s.clip_once_coef = coef1;
-  double bc1, bc2s;
-  bc_of(grp, group, s.t + 1, bc1, bc2s);
+  double bc1 = 1.0, bc2s = 1.0;
+  if (!groups_bad && group < grp.ngroups) bc_of(grp, group, s.t + 1, bc1, bc2s);
   // The slot loads issue before the first use of a partial.
   asm volatile("" : "+v"(pv[0]), "+v"(pv[1]));
   // reduce_partials' order: each thread adds its partials in index order
@@ -992,8 +1015,10 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_fold(float* __restrict__ p, f
 #pragma unroll
   for (int j = 0; j < kFoldParts; ++j) x += pv[j];
   const double sumsq = block_sum_all(x);
-  const Decision d = decide(sumsq, s, grp, false);
-  if (!d.skip) {
+  const Decision d = decide(sumsq, s, grp, groups_bad);
+  // This group is skipped with the step, or when it is past the block's live
+  // groups (a device block may hold fewer than the plan): record()'s skip.
+  if (!d.skip && group < d.ng) {
     const Sc sc = uniform_sc(load_sc(record_bc(d, s, grp, group, sumsq, bc1, bc2s)));
     for (;;) {
 #pragma unroll
@@ -1329,37 +1354,57 @@ int do_adamw_flat(float* p, float* m, float* v, void* p16, int pdt, const void* 
   return launch_status("dsx_adamw_flat");
 }
 
+// Where the folded K2 takes the group block from: a host block passed as a
+// kernel argument (checked on the host), or a block in device memory with
+// max_groups record slots (checked in the kernel; the graph form).
+struct FoldGroups {
+  const DsxGroupsDev* host;
+  const DsxGroupsDev* dev;
+  int32_t max_groups;
+};
+
 // The folded K2 over one group's range: the one-trip grid of K2 (2 slots per
 // thread, at most kK2OneTripPerCu blocks per CU; the kernel strides over what
-// one trip does not cover).
+// one trip does not cover), plus the writer's block.
+template <int GD, int PD, bool NT>
+void launch_k2_fold_nt(dim3 grid, float* p, float* m, float* v, uint16_t* o, const void* g, int64_t n,
+                       const double* partials, int32_t nparts, DsxState* state, const DsxScalerConfig& scfg,
+                       const FoldGroups& fg, int group, int32_t w, DsxStepScalars* out, hipStream_t s) {
+  constexpr int U = 2;
+  if (fg.dev)
+    hipLaunchKernelGGL((k2_adamw_fold<GD, PD, U, NT, const DsxGroupsDev*>), grid, dim3(kBlock), 0, s, p, m, v, o, g,
+                       n, partials, nparts, state, scfg, fg.dev, fg.max_groups, group, w, out);
+  else
+    hipLaunchKernelGGL((k2_adamw_fold<GD, PD, U, NT, DsxGroupsDev>), grid, dim3(kBlock), 0, s, p, m, v, o, g, n,
+                       partials, nparts, state, scfg, *fg.host, fg.max_groups, group, w, out);
+}
+
 template <int GD, int PD>
 void launch_k2_fold(float* p, float* m, float* v, void* p16, const void* g, int64_t n, const double* partials,
-                    int32_t nparts, DsxState* state, const DsxScalerConfig& scfg, const DsxGroupsDev& grp,
+                    int32_t nparts, DsxState* state, const DsxScalerConfig& scfg, const FoldGroups& fg,
                     int group, bool writer, DsxStepScalars* out, hipStream_t s) {
-  constexpr int U = 2;
   const int64_t slots = n >> 2;
-  int64_t blocks = ceil_div(slots > 0 ? slots : 1, (int64_t)kBlock * U);
+  int64_t blocks = ceil_div(slots > 0 ? slots : 1, (int64_t)kBlock * 2);
   const int64_t cap = (int64_t)cu_count() * kK2OneTripPerCu;
   if (blocks > cap) blocks = cap;
   if (writer) blocks += 1;  // the block that writes the records and the state
   uint16_t* o = static_cast<uint16_t*>(p16);
+  const dim3 grid((unsigned)blocks);
   const int32_t w = writer ? 1 : 0;
   if (g_tune.nontemporal)
-    hipLaunchKernelGGL((k2_adamw_fold<GD, PD, U, true>), dim3((unsigned)blocks), dim3(kBlock), 0, s, p, m, v, o, g,
-                       n, partials, nparts, state, scfg, grp, group, w, out);
+    launch_k2_fold_nt<GD, PD, true>(grid, p, m, v, o, g, n, partials, nparts, state, scfg, fg, group, w, out, s);
   else
-    hipLaunchKernelGGL((k2_adamw_fold<GD, PD, U, false>), dim3((unsigned)blocks), dim3(kBlock), 0, s, p, m, v, o, g,
-                       n, partials, nparts, state, scfg, grp, group, w, out);
+    launch_k2_fold_nt<GD, PD, false>(grid, p, m, v, o, g, n, partials, nparts, state, scfg, fg, group, w, out, s);
 }
 
 template <int GD>
 void k2_fold_by_param(int pd, float* p, float* m, float* v, void* p16, const void* g, int64_t n,
                       const double* partials, int32_t nparts, DsxState* state, const DsxScalerConfig& scfg,
-                      const DsxGroupsDev& grp, int group, bool writer, DsxStepScalars* out, hipStream_t s) {
+                      const FoldGroups& fg, int group, bool writer, DsxStepScalars* out, hipStream_t s) {
   if (pd == DSX_BF16)
-    launch_k2_fold<GD, DSX_BF16>(p, m, v, p16, g, n, partials, nparts, state, scfg, grp, group, writer, out, s);
+    launch_k2_fold<GD, DSX_BF16>(p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s);
   else
-    launch_k2_fold<GD, DSX_F16>(p, m, v, p16, g, n, partials, nparts, state, scfg, grp, group, writer, out, s);
+    launch_k2_fold<GD, DSX_F16>(p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s);
 }
 
 bool fold_applies(int64_t n, int32_t nparts) {
@@ -1368,17 +1413,17 @@ bool fold_applies(int64_t n, int32_t nparts) {
 
 int do_adamw_fold(float* p, float* m, float* v, void* p16, int pdt, const void* g, int gdt, int64_t n,
                   const double* partials, int32_t nparts, DsxState* state, const DsxScalerConfig& scfg,
-                  const DsxGroupsDev& grp, int group, bool writer, DsxStepScalars* out, hipStream_t s) {
+                  const FoldGroups& fg, int group, bool writer, DsxStepScalars* out, hipStream_t s) {
   const int pd = p16 ? pdt : DSX_F16;
   switch (gdt) {
     case DSX_BF16:
-      k2_fold_by_param<DSX_BF16>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, grp, group, writer, out, s);
+      k2_fold_by_param<DSX_BF16>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s);
       break;
     case DSX_F16:
-      k2_fold_by_param<DSX_F16>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, grp, group, writer, out, s);
+      k2_fold_by_param<DSX_F16>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s);
       break;
     default:
-      k2_fold_by_param<DSX_F32>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, grp, group, writer, out, s);
+      k2_fold_by_param<DSX_F32>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s);
       break;
   }
   return launch_status("dsx_adamw_flat (finalize folded in)");
@@ -1475,8 +1520,8 @@ int zero_step_flat(float* master, float* m, float* v, void* p16, int pdt, const 
   const DsxGroupsDev grp = one_group(hyper, bc_table, bc_len);
   if (fold_applies(n, nparts)) {
     int rc = do_unscale_norm(g, gdt, n, state, partials, nparts, s, state);
-    if (!rc) rc = do_adamw_fold(master, m, v, p16, pdt, g, gdt, n, partials, nparts, state, scaler, grp, 0, true,
-                                out, s);
+    if (!rc) rc = do_adamw_fold(master, m, v, p16, pdt, g, gdt, n, partials, nparts, state, scaler,
+                                FoldGroups{&grp, nullptr, 1}, 0, true, out, s);
     return rc;
   }
   int rc = do_unscale_norm(g, gdt, n, state, partials, nparts, s);
@@ -1513,6 +1558,71 @@ int noalloc_scratch(hipStream_t s, unsigned char** out) {
   }
   *out = g_scratch_ptr[dev];
   return DSX_OK;
+}
+
+// The flat plan's own checks (everything but the group block).
+int check_plan(const DsxFlatPlan& P) {
+  int rc = check_flat(P.master, P.exp_avg, P.exp_avg_sq, P.param16, P.param_dtype, P.grad, P.grad_dtype, P.n);
+  if (!rc) rc = check_parts(P.partials, P.nparts);
+  if (!rc) rc = check_scaler(P.scaler);
+  if (rc) return rc;
+  if (!P.state || !P.out) return fail(DSX_EINVAL, "null state or scalars");
+  if (P.ngroups < 1 || P.ngroups > DSX_MAX_GROUPS)
+    return fail(DSX_EINVAL, "ngroups must be in [1, %d] (got %d)", DSX_MAX_GROUPS, P.ngroups);
+  int64_t prev = 0;
+  for (int k = 0; k < P.ngroups; ++k) {
+    const int64_t end = P.group_end[k];
+    const bool last = k == P.ngroups - 1;
+    if (end < prev || end > P.n || (last ? end != P.n : (end & 7) != 0))
+      return fail(DSX_EINVAL, "group_end[%d] = %lld: boundaries must be nondecreasing multiples of 8 ending at n",
+                  k, (long long)end);
+    prev = end;
+  }
+  return DSX_OK;
+}
+
+// The step of a checked plan: two launches (K1, then each nonempty group's K2
+// with the finalize folded in, the first of them writing the state) where
+// the fold applies, else three (K1, K0, each nonempty group's K2). The group
+// block is the host's G (a kernel argument) or, when G is NULL, the block at
+// the device address Gdev (read by the kernels: the graph form).
+int plan_launches(const DsxFlatPlan& P, const DsxGroupsDev* G, const DsxGroupsDev* Gdev, hipStream_t s) {
+  bool fold = fold_applies(P.n, P.nparts);
+  int64_t prev = 0;
+  for (int k = 0; fold && k < P.ngroups; ++k) {
+    const int64_t len = P.group_end[k] - prev;
+    prev = P.group_end[k];
+    if (len > 0 && len < 4) fold = false;  // the folded K2 takes at least one 4-element slot
+  }
+  int rc = do_unscale_norm(P.grad, P.grad_dtype, P.n, P.state, P.partials, P.nparts, s, fold ? P.state : nullptr);
+  if (!rc && !fold) {
+    if (G) {
+      rc = do_finalize(P.partials, P.nparts, P.state, P.scaler, *G, P.out, s);
+    } else {
+      hipLaunchKernelGGL(k0_finalize_dev, dim3(1), dim3(kBlock), 0, s, P.partials, P.nparts, P.state, P.scaler, Gdev,
+                         P.ngroups, P.out);
+      rc = launch_status("dsx_finalize_dev");
+    }
+  }
+  const FoldGroups fg{G, Gdev, P.ngroups};
+  const int64_t gsz = P.grad_dtype == DSX_F32 ? 4 : 2;
+  bool writer = true;
+  prev = 0;
+  for (int k = 0; !rc && k < P.ngroups; ++k) {
+    const int64_t a = prev, b = P.group_end[k];
+    prev = b;
+    if (b == a) continue;
+    void* p16 = P.param16 ? static_cast<void*>(static_cast<uint16_t*>(P.param16) + a) : nullptr;
+    const void* ga = static_cast<const char*>(P.grad) + a * gsz;
+    if (fold)
+      rc = do_adamw_fold(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype, ga, P.grad_dtype, b - a,
+                         P.partials, P.nparts, P.state, P.scaler, fg, k, writer, P.out, s);
+    else
+      rc = do_adamw_flat(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype, ga, P.grad_dtype, b - a,
+                         P.out + k, s);
+    writer = false;
+  }
+  return rc;
 }
 
 }  // namespace
@@ -1801,59 +1911,26 @@ int dsx_zero_step_plan(const DsxFlatPlan* plan, const DsxGroupsDev* groups, void
   if (!plan || !groups) return fail(DSX_EINVAL, "null plan or groups");
   const DsxFlatPlan& P = *plan;
   const DsxGroupsDev& G = *groups;
-  int rc = check_flat(P.master, P.exp_avg, P.exp_avg_sq, P.param16, P.param_dtype, P.grad, P.grad_dtype, P.n);
-  if (!rc) rc = check_parts(P.partials, P.nparts);
-  if (!rc) rc = check_scaler(P.scaler);
+  int rc = check_plan(P);
   if (rc) return rc;
-  if (!P.state || !P.out) return fail(DSX_EINVAL, "null state or scalars");
-  if (P.ngroups < 1 || P.ngroups > DSX_MAX_GROUPS)
-    return fail(DSX_EINVAL, "ngroups must be in [1, %d] (got %d)", DSX_MAX_GROUPS, P.ngroups);
   if (G.ngroups != P.ngroups)
     return fail(DSX_EINVAL, "the group block holds %d groups, the plan %d", G.ngroups, P.ngroups);
   if (G.bc_len < 0) return fail(DSX_EINVAL, "bad bias-correction table length");
-  int64_t prev = 0;
   for (int k = 0; k < P.ngroups; ++k) {
     rc = check_hyper(G.hyper[k]);
     if (rc) return rc;
     if (G.bc_len > 0 && !G.bc_table[k]) return fail(DSX_EINVAL, "null bias-correction table for group %d", k);
     if (G.t_offset[k] < 0) return fail(DSX_EINVAL, "negative t_offset for group %d", k);
-    const int64_t end = P.group_end[k];
-    const bool last = k == P.ngroups - 1;
-    if (end < prev || end > P.n || (last ? end != P.n : (end & 7) != 0))
-      return fail(DSX_EINVAL, "group_end[%d] = %lld: boundaries must be nondecreasing multiples of 8 ending at n",
-                  k, (long long)end);
-    prev = end;
   }
-  hipStream_t s = as_stream(stream);
-  // Two launches (K1, then each group's K2 with the finalize folded in, the
-  // first of them writing the state) or three (K1, K0, each group's K2).
-  bool fold = fold_applies(P.n, P.nparts);
-  prev = 0;
-  for (int k = 0; fold && k < P.ngroups; ++k) {
-    const int64_t len = P.group_end[k] - prev;
-    prev = P.group_end[k];
-    if (len > 0 && len < 4) fold = false;  // the folded K2 takes at least one 4-element slot
-  }
-  rc = do_unscale_norm(P.grad, P.grad_dtype, P.n, P.state, P.partials, P.nparts, s, fold ? P.state : nullptr);
-  if (!rc && !fold) rc = do_finalize(P.partials, P.nparts, P.state, P.scaler, G, P.out, s);
-  const int64_t gsz = P.grad_dtype == DSX_F32 ? 4 : 2;
-  bool writer = true;
-  prev = 0;
-  for (int k = 0; !rc && k < P.ngroups; ++k) {
-    const int64_t a = prev, b = P.group_end[k];
-    prev = b;
-    if (b == a) continue;
-    void* p16 = P.param16 ? static_cast<void*>(static_cast<uint16_t*>(P.param16) + a) : nullptr;
-    const void* ga = static_cast<const char*>(P.grad) + a * gsz;
-    if (fold)
-      rc = do_adamw_fold(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype, ga, P.grad_dtype, b - a,
-                         P.partials, P.nparts, P.state, P.scaler, G, k, writer, P.out, s);
-    else
-      rc = do_adamw_flat(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype, ga, P.grad_dtype, b - a,
-                         P.out + k, s);
-    writer = false;
-  }
-  return rc;
+  return plan_launches(P, &G, nullptr, as_stream(stream));
+}
+
+int dsx_zero_step_dev(const DsxFlatPlan* plan, const DsxGroupsDev* groups_dev, void* stream) {
+  if (!plan || !groups_dev) return fail(DSX_EINVAL, "null plan or groups");
+  if (reinterpret_cast<uintptr_t>(groups_dev) & 7u) return fail(DSX_EINVAL, "groups must be 8-byte aligned");
+  const int rc = check_plan(*plan);
+  if (rc) return rc;
+  return plan_launches(*plan, nullptr, groups_dev, as_stream(stream));
 }
 
 int dsx_zero_step_flat_noalloc(float* master, float* exp_avg, float* exp_avg_sq, void* param16, int param_dtype,

@@ -1,13 +1,15 @@
 """The fused optimizer step captured once as a HIP graph and replayed.
 
-K1 (unscale + norm partials) -> K0 (dsx_finalize_dev) -> K2 per parameter
-group are recorded into one torch.cuda.CUDAGraph on the first step. Every
-buffer the kernels touch (flat partition, DsxState, partials, scalars) keeps
-its address for the optimizer's life, so the recorded launches stay valid.
-What changes from step to step -- learning rate and the other per-group
+The launches of one dsx_zero_step_dev call -- K1 (unscale + norm partials)
+then K2 per parameter group with the finalize folded in, or on partitions
+above the fold's bound K1 -> K0 (dsx_finalize_dev) -> K2 per group -- are
+recorded into one torch.cuda.CUDAGraph on the first step. Every buffer the
+kernels touch (flat partition, DsxState, partials, scalars) keeps its
+address for the optimizer's life, so the recorded launches stay valid. What
+changes from step to step -- learning rate and the other per-group
 hyper-parameters a scheduler may set, the bias-correction tables as they
-grow -- lives in a DsxGroupsDev block in device memory, which K0 reads at
-replay time. When those values changed since the last replay, the host
+grow -- lives in a DsxGroupsDev block in device memory, which the kernels
+read at replay time. When those values changed since the last replay, the host
 enqueues dsx_groups_upload before the replay (a one-wave kernel that takes
 the block as its argument: no staging buffer, no DMA copy, no host wait);
 the upload is not part of the graph, and nothing in the graph is a memset
@@ -28,7 +30,7 @@ import gc
 
 import torch
 
-from . import ops
+from . import _lib, ops
 
 
 class GraphedStep:
@@ -62,16 +64,12 @@ class GraphedStep:
                 gc.enable()
 
     def _plans(self, opt) -> list:
-        """Every launch of the step, checked and bound before the capture."""
-        plans = [ops.plan_unscale_norm(opt.flat.grad, opt.dstate, opt.partials, opt.nparts),
-                 ops.plan_finalize_dev(opt.partials, opt.nparts, opt.dstate, opt.scaler.to_c(), self.groups_dev,
-                                       self.ngroups, opt.scalars)]
-        for gi in range(self.ngroups):
-            master, m, v, p16, g = opt.flat.group_views(gi)
-            if master.numel():
-                sc = opt.scalars[gi * ops.SCALARS_BYTES:(gi + 1) * ops.SCALARS_BYTES]
-                plans.append(ops.plan_adamw_flat(master, m, v, p16, g, sc))
-        return plans
+        """The step's launches, checked and bound before the capture: one
+        dsx_zero_step_dev call (K1, then each group's K2 with the finalize
+        folded in, or K1, K0, K2 on larger partitions), its group block read
+        from self.groups_dev when the graph replays."""
+        return [ops.plan_zero_step_dev(opt.pack_plan(), self.groups_dev,
+                                       keep=(opt.flat, opt.partials, opt.dstate, opt.scalars))]
 
     @staticmethod
     def _warm(opt, dev: torch.device) -> None:
@@ -91,6 +89,17 @@ class GraphedStep:
         ops.unscale_norm(g, st, parts, 1)
         ops.finalize_dev(parts, 1, st, opt.scaler.to_c(), groups, 1, sc)
         ops.adamw_flat(f[0], f[1], f[2], p16, g, sc)
+        # the two-launch form's kernels (the empty group block makes it a skip)
+        P = _lib.DsxFlatPlan()
+        P.master, P.exp_avg, P.exp_avg_sq = f[0].data_ptr(), f[1].data_ptr(), f[2].data_ptr()
+        P.param16 = p16.data_ptr() if p16 is not None else None
+        P.grad, P.n = g.data_ptr(), g.numel()
+        P.param_dtype = ops.dtype_code(pd) if pd is not None else _lib.DSX_F16
+        P.grad_dtype = ops.grad_code(gd)
+        P.state, P.partials, P.out = st.data_ptr(), parts.data_ptr(), sc.data_ptr()
+        P.nparts, P.ngroups, P.scaler = 1, 1, opt.scaler.to_c()
+        P.group_end[0] = g.numel()
+        ops.plan_zero_step_dev(P, groups)(ops.stream_of(dev))
         torch.cuda.synchronize(dev)
 
     def replay(self, hypers, tables, t_offsets, bc_len: int) -> None:

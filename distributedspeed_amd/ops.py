@@ -393,6 +393,18 @@ def plan_finalize_dev(partials: torch.Tensor, nparts: int, state: torch.Tensor, 
                   int(max_groups), _ptr(out), keep=(partials, state, groups_dev, out))
 
 
+def plan_zero_step_dev(plan: _lib.DsxFlatPlan, groups_dev: torch.Tensor, keep=()) -> Launch:
+    """dsx_zero_step_dev bound to a packed flat plan and a device group
+    block (uint8[GROUPS_BYTES]): the flat step whose per-group inputs the
+    kernels read from device memory, so that it can be captured into a graph.
+    `keep` holds the tensors the plan points into."""
+    if groups_dev.dtype != torch.uint8 or groups_dev.numel() < GROUPS_BYTES or not groups_dev.is_cuda:
+        raise ValueError("groups_dev must be a uint8 device tensor of GROUPS_BYTES bytes")
+    if groups_dev.data_ptr() % 8:
+        raise ValueError("groups_dev must be 8-byte aligned")
+    return Launch("dsx_zero_step_dev", ctypes.byref(plan), _ptr(groups_dev), keep=(plan, groups_dev) + tuple(keep))
+
+
 # ---- ragged lists (K3) --------------------------------------------------------------
 
 class ChunkTable:

@@ -405,11 +405,11 @@ class AdamWOptimizer(_FusedAdamWBase):
             self._k0_hook = ops.FinalizeGroups(self.flat.hook_norm_partials, len(self.flat.params), self.dstate,
                                                self.scalars, len(self.param_groups))
         if self.capturable:
-            # K0 reads the per-group values from device memory, so the launches
-            # can be recorded into a caller's graph and replayed.
+            # The kernels read the per-group values from device memory, so the
+            # launches can be recorded into a caller's graph and replayed.
             self.groups_dev = torch.zeros(ops.GROUPS_BYTES, dtype=torch.uint8, device=self.device)
-            self._k0dev = ops.plan_finalize_dev(self.partials, self.nparts, self.dstate, self.scaler.to_c(),
-                                                self.groups_dev, len(self.param_groups), self.scalars)
+            self._dev_step = ops.plan_zero_step_dev(self.pack_plan(), self.groups_dev,
+                                                    keep=(self.flat, self.partials, self.dstate, self.scalars))
             self._uploaded = None
             self._prepared = False
 
@@ -418,7 +418,9 @@ class AdamWOptimizer(_FusedAdamWBase):
 
     # ---- the eager step in one call ------------------------------------------------------
 
-    def _build_plan(self) -> None:
+    def pack_plan(self) -> _lib.DsxFlatPlan:
+        """The flat step's fixed arguments as a DsxFlatPlan (host struct):
+        buffers, dtypes, partials, step records, group boundaries, scaler."""
         f = self.flat
         P = _lib.DsxFlatPlan()
         P.master, P.exp_avg, P.exp_avg_sq = f.master.data_ptr(), f.exp_avg.data_ptr(), f.exp_avg_sq.data_ptr()
@@ -429,8 +431,13 @@ class AdamWOptimizer(_FusedAdamWBase):
         P.grad_dtype = ops.grad_code(f.grad.dtype)
         P.state, P.partials, P.out = self.dstate.data_ptr(), self.partials.data_ptr(), self.scalars.data_ptr()
         P.nparts, P.ngroups = self.nparts, len(self.param_groups)
+        P.scaler = self.scaler.to_c()
         for k, (_, b) in enumerate(f.group_ranges):
             P.group_end[k] = b
+        return P
+
+    def _build_plan(self) -> None:
+        P = self.pack_plan()
         self._plan = P
         self._gblock = _lib.DsxGroupsDev()
         self._gkey = None  # what the group block was last filled from
@@ -490,13 +497,9 @@ class AdamWOptimizer(_FusedAdamWBase):
             self.prepare_step()
         self._prepared = False
         self.flat.check_grads_bound()
-        s = ops.stream_of(self.device)
-        self._k1(s)
-        self._k0dev(s)
+        self._dev_step(ops.stream_of(self.device))
         if not capturing:
             self._after_finalize()
-        for k2 in self._k2:
-            k2(s)
 
     def launch_norm(self) -> None:
         """K1 alone over the current grads (partials <- squared norms)."""

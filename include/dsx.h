@@ -425,6 +425,18 @@ typedef struct DsxFlatPlan {
 int dsx_zero_step_plan(const DsxFlatPlan* plan /* host */,
                        const DsxGroupsDev* groups /* host */, void* stream);
 
+/* dsx_zero_step_plan with the group block in DEVICE memory (written, e.g.,
+ * by dsx_groups_upload), read by the kernels when they run: the launches
+ * can be recorded into a HIP graph once and replayed, with a new block
+ * uploaded between replays. The block is checked on the device (as
+ * dsx_finalize_dev checks it: a bad block skips the step and sets
+ * DSX_STATE_ERR_GROUPS); records are written for plan->ngroups slots. The
+ * same kernels and bits as dsx_zero_step_plan (two launches where
+ * dsx_set_tuning_fold's bound allows, else three). No counterpart in the
+ * reference (it has no graph path). */
+int dsx_zero_step_dev(const DsxFlatPlan* plan /* host */,
+                      const DsxGroupsDev* groups_dev, void* stream);
+
 /* dsx_zero_step_flat that allocates nothing and takes no scratch buffer:
  * K1's partials and (when out is NULL) K0's step scalars live in a static
  * device array of the library, DSX_NOALLOC_SCRATCH_BYTES per GPU, held until

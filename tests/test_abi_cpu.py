@@ -181,6 +181,17 @@ def test_argument_checks_reject_before_launch(lib):
     plan.master = al + 4
     assert lib.dsx_zero_step_plan(ctypes.byref(plan), ctypes.byref(gb), None) == EINVAL
     assert b"aligned" in lib.dsx_last_error()
+    # the same plan checks with the group block in device memory
+    assert lib.dsx_zero_step_dev(ctypes.byref(plan), al, None) == EINVAL
+    assert b"aligned" in lib.dsx_last_error()
+    plan.master = al
+    assert lib.dsx_zero_step_dev(None, al, None) == EINVAL
+    assert lib.dsx_zero_step_dev(ctypes.byref(plan), None, None) == EINVAL
+    assert lib.dsx_zero_step_dev(ctypes.byref(plan), al + 4, None) == EINVAL
+    plan.group_end[0] = 36
+    assert lib.dsx_zero_step_dev(ctypes.byref(plan), al, None) == EINVAL
+    assert b"group_end" in lib.dsx_last_error()
+    plan.group_end[0] = 32
     # tuning validation
     assert lib.dsx_set_tuning(8, 8, 3, 1) == EINVAL
     assert lib.dsx_set_tuning(0, 8, 4, 1) == EINVAL
@@ -188,6 +199,7 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.dsx_set_tuning_k2(-1, 1) == EINVAL and lib.dsx_set_tuning_k2(9, 0) == EINVAL
     assert lib.dsx_set_tuning_k2(0, 2) == EINVAL and lib.dsx_set_tuning_k2(0, -2) == EINVAL
     assert lib.dsx_set_tuning_k2_chunk(-1) == EINVAL and lib.dsx_set_tuning_k2_chunk(1000) == EINVAL
+    assert lib.dsx_set_tuning_fold(-1) == EINVAL
     assert lib.dsx_set_tuning_multi(8, 3, 0, 0) == EINVAL
     assert lib.dsx_set_tuning_multi(-1, 1, 0, 0) == EINVAL
     assert lib.dsx_set_tuning_multi(0, 1, 1, 2) == EINVAL

@@ -277,3 +277,73 @@ def test_optimizer_with_empty_group_matches_three_launches(gpu):
     sa, sb = a.read_state(), b.read_state()
     assert bytes(sa) == bytes(sb)
     assert sa.t == 11 and sa.overflow_count == 1 and sa.error == 0 and not math.isnan(sa.last_norm)
+
+
+@pytest.mark.parametrize("case", ["ok", "ngroups", "lr", "ok_fewer"])
+def test_dev_block_step_two_and_three_launches(gpu, case):
+    """dsx_zero_step_dev (the group block in device memory, the graph form)
+    with a block the device-side checks accept or reject: two launches and
+    three give the same bits; a rejected block (ngroups above the plan's
+    slots, a negative lr) skips the step in every slot and sets
+    DSX_STATE_ERR_GROUPS; a block with fewer groups than the plan steps those
+    and writes the other slots as skipped."""
+    import torch
+    from distributedspeed_amd import _lib, ops
+    from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
+    n, ends = 48, [16, 32, 48]
+    scaler = ScalerConfig(mode="dynamic", init_scale=2.0 ** 6, window=2, hysteresis=1)
+    tab = BiasCorrectionTable(gpu, 0.9, 0.999)
+    h = [AdamWHyper(lr=1e-3 * (k + 1), weight_decay=0.01, max_grad_norm=1.0).to_c() for k in range(3)]
+    g = _lib.DsxGroupsDev.from_buffer_copy(ops.pack_groups(h, [tab.table] * 3, [0, 0, 0], tab.length))
+    if case == "ngroups":
+        g.ngroups = 5
+    elif case == "lr":
+        g.hyper[1].lr = -1.0
+    elif case == "ok_fewer":
+        g.ngroups = 1
+    gen = torch.Generator(device=gpu).manual_seed(3)
+    master = (torch.randn(n, generator=gen, device=gpu) * 0.05).float()
+    sides = []
+    for fold in (FOLD_DEFAULT, 0):
+        sd = _Side(gpu, master, F16, F16, n, scaler)
+        sd.out = torch.full((ops.SCALARS_BYTES * 3,), 0x7F, dtype=torch.uint8, device=gpu)
+        sd.groups = torch.frombuffer(bytearray(bytes(g)), dtype=torch.uint8).to(gpu)
+        sd.parts = torch.zeros(4, dtype=torch.float64, device=gpu)
+        sd.fold = fold
+        sides.append(sd)
+    stream = ops.stream_of(gpu)
+    _say(f"dev block step case={case}")
+    try:
+        for step in range(3):
+            gg = (torch.randn(n, generator=gen, device=gpu) * 1e-2 * 64).half()
+            for sd in sides:
+                sd.g.copy_(gg)
+                P = _lib.DsxFlatPlan()
+                P.master, P.exp_avg, P.exp_avg_sq = sd.p.data_ptr(), sd.m.data_ptr(), sd.v.data_ptr()
+                P.param16, P.grad, P.n, P.param_dtype, P.grad_dtype = sd.p16.data_ptr(), sd.g.data_ptr(), n, F16, F16
+                P.state, P.partials, P.out = sd.state.data_ptr(), sd.parts.data_ptr(), sd.out.data_ptr()
+                P.nparts, P.ngroups, P.scaler = 4, 3, scaler.to_c()
+                for k, e in enumerate(ends):
+                    P.group_end[k] = e
+                _lib.call("dsx_set_tuning_fold", ctypes.c_int64(sd.fold))
+                _lib.call("dsx_zero_step_dev", ctypes.byref(P), _ptr(sd.groups), stream)
+            torch.cuda.synchronize()
+            xa, xb = sides[0].bits(), sides[1].bits()
+            for name in xa:
+                assert torch.equal(xa[name], xb[name]), f"{case} step {step}: {name} differs"
+    finally:
+        _lib.call("dsx_set_tuning_fold", ctypes.c_int64(FOLD_DEFAULT))
+    a = sides[0]
+    s = ops.read_state(a.state)
+    sc = [ops.read_scalars(a.out[k * ops.SCALARS_BYTES:(k + 1) * ops.SCALARS_BYTES]) for k in range(3)]
+    p = a.p.cpu()
+    moved = [not torch.equal(p[b - 16:b], master[b - 16:b].cpu()) for b in ends]
+    if case in ("ngroups", "lr"):
+        assert s.error & _lib.DSX_STATE_ERR_GROUPS and s.t == 0 and s.last_skip == 1
+        assert all(x.skip == 1 for x in sc) and not any(moved)
+    elif case == "ok_fewer":
+        assert s.error == 0 and s.t == 3
+        assert sc[0].skip == 0 and sc[1].skip == 1 and sc[2].skip == 1
+        assert moved == [True, False, False]
+    else:
+        assert s.error == 0 and s.t == 3 and all(x.skip == 0 for x in sc) and all(moved)
