@@ -25,6 +25,7 @@ measures one GPU; the multi-GPU layout is described in the design notes.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -58,6 +59,9 @@ def _args():
                          "the default is 2,0,0,1,0,-1: 0 and -1 pick by size)")
     ap.add_argument("--k2-chunk", type=int, default=None,
                     help="K2 part size in elements (dsx_set_tuning_k2_chunk; 0: one launch; default: the library's 2^26)")
+    ap.add_argument("--fold", type=int, default=None,
+                    help="largest partition whose one-call step runs as two launches, K0 folded into K2 "
+                         "(dsx_set_tuning_fold; 0: always three launches; default: the library's 2^24)")
     ap.add_argument("--tuning-multi", default="",
                     help="k3_bpc,k3_unroll,nt,drain (K3 launch-shape override; k3_bpc 0 picks by chunk count)")
     ap.add_argument("--workload", default="llama8b-shard",
@@ -884,6 +888,8 @@ def main() -> int:
         _lib.call("dsx_set_tuning_multi", *[int(x) for x in a.tuning_multi.split(",")])
     if a.k2_chunk is not None:
         _lib.call("dsx_set_tuning_k2_chunk", a.k2_chunk)
+    if a.fold is not None:
+        _lib.call("dsx_set_tuning_fold", ctypes.c_int64(a.fold))
     n = int(a.numel)
     if a.profile_kernels:
         if a.workload in ("llama-ragged", "gpt2-small"):

@@ -20,14 +20,19 @@ import glob
 import json
 import os
 
-KERNELS = {"k2_adamw_flat": 28, "k1_unscale_norm": 2, "k0_finalize": 0, "k0_finalize_dev": 0, "k2_adamw_multi": 28,
-           "k1_unscale_norm_multi": 2, "k2_traffic_probe": 28}
+KERNELS = {"k2_adamw_flat": 28, "k2_adamw_fold": 28, "k2_adamw_fold_dev": 28, "k1_unscale_norm": 2, "k0_finalize": 0,
+           "k0_finalize_dev": 0, "k2_adamw_multi": 28, "k1_unscale_norm_multi": 2, "k2_traffic_probe": 28}
 
-# The launches of one step, by form (the last kernel may repeat: K2 over a
-# partition above 2^26 elements is several consecutive dispatches).
+# The launches of one step, by form: K1, K0 (None where the finalize is
+# folded into K2) and K2 (which may repeat: K2 over a partition above 2^26
+# elements is several consecutive dispatches, and the folded form has one
+# per parameter group). The folded K2 reading its group block from device
+# memory (the graph form) is told apart by its template argument.
 STEP_FORMS = {
-    "flat, eager (one dsx_zero_step_plan call)": ("k1_unscale_norm", "k0_finalize", "k2_adamw_flat"),
-    "flat, HIP graph replay": ("k1_unscale_norm", "k0_finalize_dev", "k2_adamw_flat"),
+    "flat, eager, two launches (K0 folded into K2)": ("k1_unscale_norm", None, "k2_adamw_fold"),
+    "flat, HIP graph replay, two launches (K0 folded into K2)": ("k1_unscale_norm", None, "k2_adamw_fold_dev"),
+    "flat, eager, three launches": ("k1_unscale_norm", "k0_finalize", "k2_adamw_flat"),
+    "flat, HIP graph replay, three launches": ("k1_unscale_norm", "k0_finalize_dev", "k2_adamw_flat"),
     "ragged (chunk table)": ("k1_unscale_norm_multi", "k0_finalize", "k2_adamw_multi"),
 }
 COPY_NAME = "__amd_rocclr_copyBuffer"
@@ -35,6 +40,8 @@ COPY_BYTES = 1 << 30
 
 
 def _short(name: str) -> str | None:
+    if "k2_adamw_fold<" in name and "DsxGroupsDev const*>" in name:
+        return "k2_adamw_fold_dev"
     for k in sorted(KERNELS, key=len, reverse=True):
         if k in name:
             return k
@@ -144,22 +151,24 @@ def step_chains(trace_dir: str) -> dict:
     rows.sort()
     med = lambda xs: sorted(xs)[len(xs) // 2] / 1e3 if xs else None  # noqa: E731  (ns -> us)
     out = {}
-    for form, pat in STEP_FORMS.items():
+    for form, full in STEP_FORMS.items():
+        pat = [k for k in full if k is not None]
         steps, i = [], 0
         while i < len(rows):
-            if rows[i][2] == pat[0] and i + 2 < len(rows) and rows[i + 1][2] == pat[1] and rows[i + 2][2] == pat[2]:
-                j = i + 3
-                while j < len(rows) and rows[j][2] == pat[2]:
+            if all(i + q < len(rows) and rows[i + q][2] == k for q, k in enumerate(pat)):
+                j = i + len(pat)
+                while j < len(rows) and rows[j][2] == pat[-1]:
                     j += 1
                 steps.append(rows[i:j])
                 i = j
             else:
                 i += 1
-        if not steps:
+        if len(steps) < 3:  # a warm-up's launches, not a timed run of this form
             continue
-        per = {k: med([e - s for s, e, n in st if n == k]) for k in pat for st in steps[:1]}
-        for k in pat:
-            per[k] = med([sum(e - s for s, e, n in st if n == k) for st in steps])
+        per = {}
+        for k in full:
+            per[k or "k0 (folded)"] = (None if k is None else
+                                       med([sum(e - s for s, e, n in st if n == k) for st in steps]))
         busy = [sum(e - s for s, e, _ in st) for st in steps]
         span = [st[-1][1] - st[0][0] for st in steps]
         period = [steps[k + 1][0][0] - steps[k][0][0] for k in range(len(steps) - 1)]
@@ -178,10 +187,11 @@ def chains_markdown(res: dict, command: str, title: str, intro: str = "") -> str
              "one step's first kernel to the next step's. The period under the tracer includes the tracer's "
              "own cost per dispatch.", "",
              "| form | steps | K1 | K0 | K2 | kernel-busy | span | gaps | period |", "|---|---|---|---|---|---|---|---|---|"]
+    fmt = lambda x: "–" if x is None else f"{x:.2f}"  # noqa: E731
     for form, d in res.items():
         k = list(d["kernels_us"].values())
-        lines.append(f"| {form} | {d['steps']} | {k[0]:.2f} | {k[1]:.2f} | {k[2]:.2f} | {d['kernel_busy_us']:.2f} | "
-                     f"{d['span_us']:.2f} | {d['gaps_us']:.2f} | {d['period_us']:.2f} |")
+        lines.append(f"| {form} | {d['steps']} | {fmt(k[0])} | {fmt(k[1])} | {fmt(k[2])} | "
+                     f"{d['kernel_busy_us']:.2f} | {d['span_us']:.2f} | {d['gaps_us']:.2f} | {fmt(d['period_us'])} |")
     return "\n".join(lines) + "\n"
 
 

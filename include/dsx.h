@@ -16,6 +16,10 @@
  *   K3 dsx_*_multi        K1/K2 over a ragged list of tensors, driven by a
  *                         chunk table (one launch per pass for any count).
  *
+ * The one-call steps (dsx_zero_step_flat, dsx_zero_step_plan,
+ * dsx_zero_step_dev) run small partitions (dsx_set_tuning_fold) as two
+ * launches with the same results: K1, and K2 with K0's finalize folded in.
+ *
  * Conventions
  *   - Every pointer argument is a DEVICE pointer owned by the caller, except
  *     where a comment says "host". The library allocates no device memory;
