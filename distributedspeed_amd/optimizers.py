@@ -281,6 +281,34 @@ class _FusedAdamWBase(torch.optim.Optimizer):
         """DsxState on the host (synchronises)."""
         return ops.read_state(self.dstate)
 
+    def init_warm_step(self) -> None:
+        """The reference's construction-time warm step, on request
+        (Src/zero/stage1.py:330-374, Src/zero/stage2.py:386-430: its ZeRO
+        stages 1 and 2 give every owned parameter a zero grad and call step()
+        on a throwaway copy of the optimizer, then keep that copy's state).
+        One AdamW step over zero grads: each parameter decays once by
+        (1 - lr * weight_decay), exp_avg and exp_avg_sq stay zero, and the
+        AdamW step count becomes 1, so later steps take the bias corrections
+        of t = 2, 3, ... The loss scaler takes no part (the reference calls
+        the torch optimizer's step directly). Only before the first step;
+        the grads are set to None afterwards, as the reference leaves them."""
+        if self.steps_issued:
+            raise RuntimeError("init_warm_step() is the construction-time step: call it before any other step")
+        self._zero_grads_in_place()
+        saved = self.scaler
+        self.scaler = ScalerConfig(mode="none")
+        try:
+            self._warm_launch()
+        finally:
+            self.scaler = saved
+        self.zero_grad(set_to_none=True)
+
+    def _zero_grads_in_place(self) -> None:
+        raise NotImplementedError
+
+    def _warm_launch(self) -> None:
+        self.step_fused()
+
     def last_scalars(self, group: int = 0):
         return ops.read_scalars(self.scalars[group * ops.SCALARS_BYTES:(group + 1) * ops.SCALARS_BYTES])
 
@@ -415,6 +443,21 @@ class AdamWOptimizer(_FusedAdamWBase):
 
     def _grads_may_move(self) -> bool:
         return not self.capturable
+
+    def _zero_grads_in_place(self) -> None:
+        self.flat.zero_grad(set_to_none=False)
+
+    def _warm_launch(self) -> None:
+        if not (self.use_graph or self.capturable):
+            self.step_fused()
+            return
+        # Not through the graph or the device group block: a one-off eager
+        # dsx_zero_step_plan call with this step's (scaler-free) plan.
+        self.steps_issued += 1
+        hs, tables, bc_len = self._hypers()
+        G = _lib.DsxGroupsDev.from_buffer_copy(ops.pack_groups(hs, tables, self._t_offsets, bc_len))
+        P = self.pack_plan()
+        _lib.call("dsx_zero_step_plan", ctypes.byref(P), ctypes.byref(G), ops.stream_of(self.device))
 
     # ---- the eager step in one call ------------------------------------------------------
 
@@ -586,6 +629,14 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
         self._bind_state()
         self._k0 = ops.FinalizeGroups(self.partials, self.nparts, self.dstate, self.scalars, len(self.param_groups))
         self._plans_for = None  # the chunk table the bound K1 / K3 launches point at
+
+    def _zero_grads_in_place(self) -> None:
+        with torch.no_grad():
+            for p in self.store.params:
+                if p.grad is None:
+                    p.grad = torch.zeros_like(p)
+                else:
+                    p.grad.zero_()
 
     def _plans(self):
         table = self.store.table()

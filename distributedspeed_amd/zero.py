@@ -118,6 +118,15 @@ class ZeROOptimizer:
         after. See AdamWOptimizer.clip_grad_norm_."""
         return self.base_optimizer.clip_grad_norm_(max_norm, norm_type)
 
+    def init_warm_step(self) -> None:
+        """The reference stages' construction-time warm step (one AdamW step
+        over zero grads: Src/zero/stage1.py:330-374, stage2.py:386-430), on
+        request, for runs that must follow the reference's trajectory; see
+        AdamWOptimizer.init_warm_step. current_step stays 0, as the
+        reference's counter does not see that step."""
+        self.base_optimizer.init_warm_step()
+        self._step_base -= 1
+
     def grad_norm(self) -> torch.Tensor:
         """sqrt(sum of squared unscaled grads) of the current grads, computed
         by K1 into a device tensor (no host sync)."""

@@ -313,3 +313,74 @@ def test_sixteen_groups_with_empty_and_single_element_groups(gpu):
             for name, a, b in (("master", v["master"], p.detach()), ("exp_avg", v["exp_avg"], s["exp_avg"]),
                                ("exp_avg_sq", v["exp_avg_sq"], s["exp_avg_sq"])):
                 assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"step {step} param {i}: {name}"
+
+
+WARM_FORMS = {"flat": ("AdamWOptimizer", {}), "graph": ("AdamWOptimizer", {"graph": True}),
+              "capturable": ("AdamWOptimizer", {"capturable": True}),
+              "offload": ("AdamWOptimizer", {"offload": True, "offload_chunk_elems": 4096}),
+              "ragged": ("MultiTensorAdamWOptimizer", {})}
+
+
+@pytest.mark.parametrize("form", list(WARM_FORMS))
+def test_init_warm_step_follows_the_reference_trajectory(gpu, form):
+    """ZeROOptimizer.init_warm_step() reproduces the reference stages'
+    construction-time warm step (Src/zero/stage1.py:330-374: zero grads, one
+    step of the torch optimizer, its state kept): against torch.optim.AdamW
+    (default dispatch) on this GPU taking a zero-grad step and then the same
+    four steps, every master value, exp_avg and exp_avg_sq bit for bit, in
+    every storage form; the step count is 1 after the warm step while
+    current_step stays 0; the loss scaler is untouched."""
+    import torch
+    from distributedspeed_amd import optimizers as O
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.zero import ZeROOptimizer
+    _say(f"init warm step vs torch, {form}")
+    cls_name, kw = WARM_FORMS[form]
+    gen = torch.Generator(device=gpu).manual_seed(44)
+    shapes = [(96, 33), (33,), (50, 17)]
+    p0 = [torch.randn(s, device=gpu, generator=gen) * 0.05 for s in shapes]
+    lr, betas, eps = 2e-3, (0.9, 0.98), 1e-8
+    sc = ScalerConfig(mode="dynamic", init_scale=2.0 ** 10, window=2, hysteresis=1)
+    ps = [torch.nn.Parameter(t.clone()) for t in p0]
+    opt = getattr(O, cls_name)([{"params": ps[:2], "weight_decay": 0.1}, {"params": ps[2:], "weight_decay": 0.0}],
+                               lr=lr, betas=betas, eps=eps, param_dtype=torch.bfloat16, loss_scaler=sc, device=gpu,
+                               **kw)
+    zero = ZeROOptimizer(opt, {"stage": 2})
+    ref_ps = [torch.nn.Parameter(t.clone()) for t in p0]
+    ref = torch.optim.AdamW([{"params": ref_ps[:2], "weight_decay": 0.1},
+                             {"params": ref_ps[2:], "weight_decay": 0.0}], lr=lr, betas=betas, eps=eps)
+    for p in ref_ps:
+        p.grad = torch.zeros_like(p)
+    ref.step()
+    zero.init_warm_step()
+    st = opt.read_state()
+    assert st.t == 1 and zero.current_step == 0 and st.scale == 2.0 ** 10 and st.good_steps == 0
+    assert all(p.grad is None for p in opt.dsx_params) or form == "capturable"
+    with pytest.raises(RuntimeError, match="before any other step"):
+        zero.init_warm_step()
+
+    def check(tag):
+        torch.cuda.synchronize()
+        for i, rp in enumerate(ref_ps):
+            v = opt.store.views_of(i)
+            rs = ref.state[rp]
+            for name, a, b in (("master", v["master"], rp.detach()), ("exp_avg", v["exp_avg"], rs["exp_avg"]),
+                               ("exp_avg_sq", v["exp_avg_sq"], rs["exp_avg_sq"])):
+                a = a.reshape(b.shape).to(b.device)
+                assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"{tag}: tensor {i} {name}"
+
+    check("after the warm step")
+    for step in range(4):
+        scale = float(opt.read_state().scale)
+        for p, rp in zip(opt.dsx_params, ref_ps):
+            g = (torch.randn(p.shape, device=gpu, generator=gen) * 1e-2).to(torch.bfloat16)
+            if p.grad is None:
+                p.grad = (g.float() * scale).to(torch.bfloat16)
+            else:
+                p.grad.copy_((g.float() * scale).to(torch.bfloat16))
+            rp.grad = p.grad.float() * (1.0 / scale)
+        zero.step()
+        ref.step()
+        check(f"step {step}")
+    st = opt.read_state()
+    assert st.t == 5 and zero.current_step == 4
