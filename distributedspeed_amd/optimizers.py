@@ -322,6 +322,10 @@ class _FusedAdamWBase(torch.optim.Optimizer):
         """torch-compatible layout (state keyed by parameter index with
         exp_avg / exp_avg_sq / step) plus the fp32 master and the device
         scaler state; tensors are host copies."""
+        if getattr(self, "streamer", None) is not None:
+            # offloaded state: pinned host memory written by asynchronous
+            # copies, whichever stream the caller is on now
+            torch.cuda.synchronize(self.device)
         s = self.read_state()
         groups = []
         idx = 0
@@ -342,6 +346,8 @@ class _FusedAdamWBase(torch.optim.Optimizer):
                         "layout": self.store.layout(), "scaler": dict(vars(self.scaler))}}
 
     def load_state_dict(self, state_dict: dict) -> None:
+        if getattr(self, "streamer", None) is not None:
+            torch.cuda.synchronize(self.device)  # no copy of an earlier step may still write the host state
         groups = state_dict["param_groups"]
         if len(groups) != len(self.param_groups):
             raise ValueError("loaded state dict has a different number of parameter groups")
