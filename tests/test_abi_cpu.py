@@ -215,3 +215,16 @@ def test_python_layer_mirrors_torch_errors():
         AdamWHyper(eps=-1e-8).validate()
     with pytest.raises(ValueError, match="hysteresis"):
         ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, hysteresis=0).validate()
+
+
+def test_c_caller_builds_and_checks_its_arguments():
+    """The plain C caller of the ABI (tests/c_abi, built by build()) links
+    against libdsx.so and the HIP runtime and refuses bad arguments before
+    touching a device (its GPU run: tests/test_gpu_c_caller.py)."""
+    import subprocess
+    exe = os.path.join(ROOT, "tests", "c_abi", "dsx_c_caller")
+    assert os.path.exists(exe), "run build(): make -C tests/c_abi"
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1 and "usage" in r.stderr
+    r = subprocess.run([exe, "0", "1", "4", "/tmp"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1 and "bad arguments" in r.stderr
