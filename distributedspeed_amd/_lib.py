@@ -115,6 +115,8 @@ SIGNATURES = {
                                               DsxScalerConfig, DsxAdamwHyper, _P, _c.c_int32, _c.c_int32, _P, _P]),
     "dsx_unscale_norm_multi": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _P, _P, _c.c_int32, _P]),
     "dsx_adamw_multi": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _c.c_int, _P, _P]),
+    "dsx_zero_step_multi": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int64, _c.c_int, _c.c_int, _P, DsxScalerConfig, _P,
+                                       _P, _c.c_int32, _P, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -1064,11 +1064,16 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_fold(float* __restrict__ p, f
 template <int GD>
 __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorRef* __restrict__ tensors,
                                                                 const DsxChunk* __restrict__ chunks,
-                                                                int64_t nchunks,
-                                                                const DsxState* __restrict__ state,
-                                                                double* __restrict__ partials) {
+                                                                int64_t nchunks, const DsxState* state,
+                                                                double* __restrict__ partials, DsxState* fold) {
   using G = Grad<GD>;
   const float inv = inv_of(state->scale);
+  if (fold != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {  // as k1_unscale_norm
+    const int32_t armed = fold->clip_once != 0 ? 1 : 0;
+    fold->step_scale = fold->scale;
+    fold->step_t2 = 2 * fold->t + armed;
+    fold->clip_once = 0;
+  }
   double acc = 0.0;
   for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
     const DsxChunk ch = chunks[c];
@@ -1101,76 +1106,132 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorR
   if (threadIdx.x == 0) partials[blockIdx.x] = s;
 }
 
+// One chunk of K3: the K2 slot loop (U slots per thread, all of a trip's
+// loads before any use) where every array is aligned for its 4-element
+// slot, element by element otherwise.
+template <int GD, int PD, int U, bool NT, bool DRAIN>
+__device__ __forceinline__ void k3_chunk(const DsxTensorRef& tr, const DsxChunk& ch, const Sc& s) {
+  using G = Grad<GD>;
+  using GS = typename G::slot4;
+  float* p = tr.master + ch.start;
+  float* m = tr.exp_avg + ch.start;
+  float* v = tr.exp_avg_sq + ch.start;
+  uint16_t* p16 = tr.param16 ? static_cast<uint16_t*>(tr.param16) + ch.start : nullptr;
+  const typename G::elem* g = static_cast<const typename G::elem*>(tr.grad) + ch.start;
+  const bool cast = p16 != nullptr;
+  const int64_t len = ch.len;
+  const uintptr_t mis = (reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(m) |
+                         reinterpret_cast<uintptr_t>(v)) & 15u;
+  const uintptr_t gmis = reinterpret_cast<uintptr_t>(g) & (sizeof(GS) - 1);
+  const uintptr_t omis = cast ? (reinterpret_cast<uintptr_t>(p16) & 7u) : 0;
+  int64_t done = 0;
+  if (!mis && !gmis && !omis) {
+    f4* p4 = reinterpret_cast<f4*>(p);
+    f4* m4 = reinterpret_cast<f4*>(m);
+    f4* v4 = reinterpret_cast<f4*>(v);
+    u2* o2 = reinterpret_cast<u2*>(p16);
+    const GS* g4 = reinterpret_cast<const GS*>(g);
+    const int64_t nvec = len >> 2;
+    for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += (int64_t)kBlock * U) {
+      GS Gs[U];
+      f4 P[U], M[U], V[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = i0 + (int64_t)u * kBlock;
+        if (i < nvec) {
+          Gs[u] = ld<NT>(g4 + i);
+          P[u] = ld<NT>(p4 + i);
+          M[u] = ld<NT>(m4 + i);
+          V[u] = ld<NT>(v4 + i);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = i0 + (int64_t)u * kBlock;
+        if (i < nvec) {
+          float gf[4];
+          G::four(Gs[u], gf);
+          f4 pp = P[u], mm = M[u], vv = V[u];
+          adamw4(gf, pp, mm, vv, s);
+          st<NT>(p4 + i, pp);
+          st<NT>(m4 + i, mm);
+          st<NT>(v4 + i, vv);
+          if (cast) st<NT>(o2 + i, pack4<PD>(pp));
+        }
+      }
+      if constexpr (DRAIN) __builtin_amdgcn_s_waitcnt(0);  // as in k2_adamw_flat
+    }
+    done = nvec << 2;
+  }
+  for (int64_t e = done + threadIdx.x; e < len; e += kBlock) {
+    float pe = p[e], me = m[e], ve = v[e];
+    adamw_elt(G::one(g[e]), pe, me, ve, s);
+    p[e] = pe; m[e] = me; v[e] = ve;
+    if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
+  }
+}
+
 template <int GD, int PD, int U, bool NT, bool DRAIN>
 __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __restrict__ tensors,
                                                          const DsxChunk* __restrict__ chunks, int64_t nchunks,
                                                          const DsxStepScalars* __restrict__ scalars) {
-  using G = Grad<GD>;
-  using GS = typename G::slot4;
   if (scalars[0].skip) return;  // the skip decision is global
   for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
     const DsxChunk ch = chunks[c];
     const DsxTensorRef tr = tensors[ch.tensor];
-    const Sc s = load_sc(scalars[tr.group]);
-    float* p = tr.master + ch.start;
-    float* m = tr.exp_avg + ch.start;
-    float* v = tr.exp_avg_sq + ch.start;
-    uint16_t* p16 = tr.param16 ? static_cast<uint16_t*>(tr.param16) + ch.start : nullptr;
-    const typename G::elem* g = static_cast<const typename G::elem*>(tr.grad) + ch.start;
-    const bool cast = p16 != nullptr;
-    const int64_t len = ch.len;
-    // Vector path when every array is aligned for its 4-element slot.
-    const uintptr_t mis = (reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(m) |
-                           reinterpret_cast<uintptr_t>(v)) & 15u;
-    const uintptr_t gmis = reinterpret_cast<uintptr_t>(g) & (sizeof(GS) - 1);
-    const uintptr_t omis = cast ? (reinterpret_cast<uintptr_t>(p16) & 7u) : 0;
-    int64_t done = 0;
-    if (!mis && !gmis && !omis) {
-      f4* p4 = reinterpret_cast<f4*>(p);
-      f4* m4 = reinterpret_cast<f4*>(m);
-      f4* v4 = reinterpret_cast<f4*>(v);
-      u2* o2 = reinterpret_cast<u2*>(p16);
-      const GS* g4 = reinterpret_cast<const GS*>(g);
-      const int64_t nvec = len >> 2;
-      // U slots per thread: all loads of a trip are issued before any use,
-      // as in k2_adamw_flat.
-      for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += (int64_t)kBlock * U) {
-        GS Gs[U];
-        f4 P[U], M[U], V[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int64_t i = i0 + (int64_t)u * kBlock;
-          if (i < nvec) {
-            Gs[u] = ld<NT>(g4 + i);
-            P[u] = ld<NT>(p4 + i);
-            M[u] = ld<NT>(m4 + i);
-            V[u] = ld<NT>(v4 + i);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int64_t i = i0 + (int64_t)u * kBlock;
-          if (i < nvec) {
-            float gf[4];
-            G::four(Gs[u], gf);
-            f4 pp = P[u], mm = M[u], vv = V[u];
-            adamw4(gf, pp, mm, vv, s);
-            st<NT>(p4 + i, pp);
-            st<NT>(m4 + i, mm);
-            st<NT>(v4 + i, vv);
-            if (cast) st<NT>(o2 + i, pack4<PD>(pp));
-          }
-        }
-        if constexpr (DRAIN) __builtin_amdgcn_s_waitcnt(0);  // as in k2_adamw_flat
-      }
-      done = nvec << 2;
+    k3_chunk<GD, PD, U, NT, DRAIN>(tr, ch, load_sc(scalars[tr.group]));
+  }
+}
+
+// K3 with K0's finalize folded in (the ragged form of k2_adamw_fold, after a
+// K1 over the list launched with fold): every block reduces the partials in
+// K0's order and decides the step with K0's code on the entry values, then
+// steps its chunks with its group's scalars; the last block does no chunk
+// work and writes the step records and the state's updated fields. Chunks
+// go one per block (the small-list shape), grid-stride over the rest.
+template <int GD, int PD, bool NT>
+__global__ __launch_bounds__(kBlock) void k3_adamw_fold(const DsxTensorRef* __restrict__ tensors,
+                                                        const DsxChunk* __restrict__ chunks, int64_t nchunks,
+                                                        const double* __restrict__ partials, int32_t nparts,
+                                                        DsxState* state, DsxScalerConfig scfg, DsxGroupsDev grp,
+                                                        DsxStepScalars* __restrict__ out) {
+  const int64_t slot_blocks = (int64_t)gridDim.x - 1;
+  double x = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += kBlock) x += partials[i];  // reduce_partials' order
+  const double sumsq = block_sum_all(x);
+  if (blockIdx.x == slot_blocks) {
+    if (threadIdx.x == 0) {
+      DsxState f = *state;
+      f.clip_once = f.step_t2 & 1;  // K1 consumed the live flag into step_t2
+      const Decision d = decide(sumsq, f, grp, false);
+      for (int k = 0; k < grp.ngroups; ++k) out[k] = record(d, f, grp, k, sumsq);
+      advance(d, f, scfg);
+      state->scale = f.scale;
+      state->good_steps = f.good_steps;
+      state->hyst_left = f.hyst_left;
+      state->t = f.t;
+      state->iter = f.iter;
+      state->overflow_count = f.overflow_count;
+      state->error = f.error;
+      state->last_skip = f.last_skip;
+      state->last_norm = f.last_norm;
+      state->clip_once = 0;
     }
-    for (int64_t e = done + threadIdx.x; e < len; e += kBlock) {
-      float pe = p[e], me = m[e], ve = v[e];
-      adamw_elt(G::one(g[e]), pe, me, ve, s);
-      p[e] = pe; m[e] = me; v[e] = ve;
-      if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
-    }
+    return;
+  }
+  DsxState s = {};
+  const int32_t t2 = state->step_t2;
+  s.scale = state->step_scale;
+  s.t = t2 >> 1;
+  s.clip_once = t2 & 1;
+  s.clip_once_coef = state->clip_once_coef;
+  const Decision d = decide(sumsq, s, grp, false);
+  if (d.skip) return;
+  for (int64_t c = blockIdx.x; c < nchunks; c += slot_blocks) {
+    const DsxChunk ch = chunks[c];
+    const DsxTensorRef tr = tensors[ch.tensor];
+    if (tr.group >= d.ng) continue;
+    k3_chunk<GD, PD, 2, NT, false>(tr, ch, uniform_sc(load_sc(record(d, s, grp, tr.group, sumsq))));
   }
 }
 
@@ -1558,6 +1619,89 @@ int noalloc_scratch(hipStream_t s, unsigned char** out) {
   }
   *out = g_scratch_ptr[dev];
   return DSX_OK;
+}
+
+int do_unscale_norm_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int gdt,
+                          const DsxState* state, double* partials, int32_t nparts, hipStream_t s, DsxState* fold) {
+  const dim3 grid(nparts), blk(kBlock);
+  switch (gdt) {
+    case DSX_BF16:
+      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_BF16>), grid, blk, 0, s, tensors, chunks, nchunks, state,
+                         partials, fold);
+      break;
+    case DSX_F16:
+      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_F16>), grid, blk, 0, s, tensors, chunks, nchunks, state,
+                         partials, fold);
+      break;
+    default:
+      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_F32>), grid, blk, 0, s, tensors, chunks, nchunks, state,
+                         partials, fold);
+      break;
+  }
+  return launch_status("dsx_unscale_norm_multi");
+}
+
+int do_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int param_dtype,
+                   int grad_dtype, const DsxStepScalars* scalars, hipStream_t s) {
+  if (nchunks == 0) return DSX_OK;
+  // Chunks are handed out statically (block b takes b, b + grid, ...). The
+  // default shape, from sweeps on MI355X over ragged lists of 1e6 to 8.3e9
+  // elements, two slots per trip throughout: up to 20 chunks per CU, one
+  // chunk per block (all of a small list in flight at once: 1-11% faster
+  // from 2 Mi to 16 Mi elements in 4096-element chunks, 2.5% slower at 30
+  // chunks per CU); up to 256 chunks per
+  // CU, one block per CU walking the list as one front (like K2's
+  // grid-stride); from 256 chunks per CU on, a grid of about four chunks per
+  // block, far more blocks than the CUs hold at once, with K2's drain, is
+  // 4-5% faster (the blocks start as others finish).
+  const int64_t cus = cu_count();
+  int64_t bpc = g_tune.k3_blocks_per_cu;
+  int unroll = g_tune.k3_unroll;
+  bool drain = g_tune.k3_drain > 0;
+  if (bpc == 0) {
+    const int64_t per_cu = nchunks / cus;
+    const bool many = per_cu >= 256;
+    if (nchunks <= kK3OneChunkPerCu * cus)
+      bpc = ceil_div(nchunks, cus);  // one chunk per block
+    else
+      bpc = many ? per_cu / 4 : 1;
+    unroll = 2;
+    drain = g_tune.k3_drain >= 0 ? g_tune.k3_drain > 0 : many;
+  }
+  int64_t blocks = cus * bpc;
+  if (blocks > nchunks) blocks = nchunks;
+  // Blocks take chunks grid-stride, so any grid covers the table; keep it
+  // within HIP's 2^32 work-items per grid dimension.
+  if (blocks > kMaxGridBlocks) blocks = kMaxGridBlocks;
+  const dim3 grid((unsigned)blocks);
+  switch (grad_dtype) {
+    case DSX_BF16: launch_k3<DSX_BF16>(param_dtype, unroll, drain, grid, tensors, chunks, nchunks, scalars, s); break;
+    case DSX_F16: launch_k3<DSX_F16>(param_dtype, unroll, drain, grid, tensors, chunks, nchunks, scalars, s); break;
+    default: launch_k3<DSX_F32>(param_dtype, unroll, drain, grid, tensors, chunks, nchunks, scalars, s); break;
+  }
+  return launch_status("dsx_adamw_multi");
+}
+
+template <int GD>
+void launch_k3_fold(int pd, dim3 grid, const DsxTensorRef* t, const DsxChunk* c, int64_t nc, const double* partials,
+                    int32_t nparts, DsxState* state, const DsxScalerConfig& scfg, const DsxGroupsDev& grp,
+                    DsxStepScalars* out, hipStream_t s) {
+  const bool nt = g_tune.k3_nontemporal != 0;
+  if (pd == DSX_BF16) {
+    if (nt)
+      hipLaunchKernelGGL((k3_adamw_fold<GD, DSX_BF16, true>), grid, dim3(kBlock), 0, s, t, c, nc, partials, nparts,
+                         state, scfg, grp, out);
+    else
+      hipLaunchKernelGGL((k3_adamw_fold<GD, DSX_BF16, false>), grid, dim3(kBlock), 0, s, t, c, nc, partials, nparts,
+                         state, scfg, grp, out);
+  } else {
+    if (nt)
+      hipLaunchKernelGGL((k3_adamw_fold<GD, DSX_F16, true>), grid, dim3(kBlock), 0, s, t, c, nc, partials, nparts,
+                         state, scfg, grp, out);
+    else
+      hipLaunchKernelGGL((k3_adamw_fold<GD, DSX_F16, false>), grid, dim3(kBlock), 0, s, t, c, nc, partials, nparts,
+                         state, scfg, grp, out);
+  }
 }
 
 // The flat plan's own checks (everything but the group block).
@@ -2003,23 +2147,8 @@ int dsx_unscale_norm_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, 
   if (!state) return fail(DSX_EINVAL, "null state");
   int rc = check_parts(partials, nparts);
   if (rc) return rc;
-  hipStream_t s = as_stream(stream);
-  const dim3 grid(nparts), blk(kBlock);
-  switch (grad_dtype) {
-    case DSX_BF16:
-      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_BF16>), grid, blk, 0, s, tensors, chunks, nchunks, state,
-                         partials);
-      break;
-    case DSX_F16:
-      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_F16>), grid, blk, 0, s, tensors, chunks, nchunks, state,
-                         partials);
-      break;
-    default:
-      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_F32>), grid, blk, 0, s, tensors, chunks, nchunks, state,
-                         partials);
-      break;
-  }
-  return launch_status("dsx_unscale_norm_multi");
+  return do_unscale_norm_multi(tensors, chunks, nchunks, grad_dtype, state, partials, nparts, as_stream(stream),
+                               nullptr);
 }
 
 int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int param_dtype,
@@ -2029,44 +2158,54 @@ int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t
   if (!is16(param_dtype)) return fail(DSX_EINVAL, "param16 dtype must be DSX_F16 or DSX_BF16 (got %d)", param_dtype);
   if (nchunks < 0 || (nchunks > 0 && (!tensors || !chunks))) return fail(DSX_EINVAL, "bad chunk table");
   if (!scalars) return fail(DSX_EINVAL, "null scalars");
-  if (nchunks == 0) return DSX_OK;
-  // Chunks are handed out statically (block b takes b, b + grid, ...). The
-  // default shape, from sweeps on MI355X over ragged lists of 1e6 to 8.3e9
-  // elements, two slots per trip throughout: up to 20 chunks per CU, one
-  // chunk per block (all of a small list in flight at once: 1-11% faster
-  // from 2 Mi to 16 Mi elements in 4096-element chunks, 2.5% slower at 30
-  // chunks per CU); up to 256 chunks per
-  // CU, one block per CU walking the list as one front (like K2's
-  // grid-stride); from 256 chunks per CU on, a grid of about four chunks per
-  // block, far more blocks than the CUs hold at once, with K2's drain, is
-  // 4-5% faster (the blocks start as others finish).
-  const int64_t cus = cu_count();
-  int64_t bpc = g_tune.k3_blocks_per_cu;
-  int unroll = g_tune.k3_unroll;
-  bool drain = g_tune.k3_drain > 0;
-  if (bpc == 0) {
-    const int64_t per_cu = nchunks / cus;
-    const bool many = per_cu >= 256;
-    if (nchunks <= kK3OneChunkPerCu * cus)
-      bpc = ceil_div(nchunks, cus);  // one chunk per block
-    else
-      bpc = many ? per_cu / 4 : 1;
-    unroll = 2;
-    drain = g_tune.k3_drain >= 0 ? g_tune.k3_drain > 0 : many;
+  return do_adamw_multi(tensors, chunks, nchunks, param_dtype, grad_dtype, scalars, as_stream(stream));
+}
+
+int dsx_zero_step_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int64_t numel,
+                        int param_dtype, int grad_dtype, DsxState* state, DsxScalerConfig scaler,
+                        const DsxGroupsDev* groups, double* partials, int32_t nparts, DsxStepScalars* out,
+                        void* stream) {
+  if (!is_grad_dtype(grad_dtype))
+    return fail(DSX_EINVAL, "grad dtype must be DSX_F16, DSX_BF16 or DSX_F32 (got %d)", grad_dtype);
+  if (!is16(param_dtype)) return fail(DSX_EINVAL, "param16 dtype must be DSX_F16 or DSX_BF16 (got %d)", param_dtype);
+  if (nchunks < 0 || (nchunks > 0 && (!tensors || !chunks))) return fail(DSX_EINVAL, "bad chunk table");
+  if (numel < 0) return fail(DSX_EINVAL, "numel must be >= 0");
+  if (!state || !out || !groups) return fail(DSX_EINVAL, "null state, scalars or groups");
+  int rc = check_parts(partials, nparts);
+  if (!rc) rc = check_scaler(scaler);
+  if (rc) return rc;
+  const DsxGroupsDev& G = *groups;
+  if (G.ngroups < 1 || G.ngroups > DSX_MAX_GROUPS)
+    return fail(DSX_EINVAL, "ngroups must be in [1, %d] (got %d)", DSX_MAX_GROUPS, G.ngroups);
+  if (G.bc_len < 0) return fail(DSX_EINVAL, "bad bias-correction table length");
+  for (int k = 0; k < G.ngroups; ++k) {
+    rc = check_hyper(G.hyper[k]);
+    if (rc) return rc;
+    if (G.bc_len > 0 && !G.bc_table[k]) return fail(DSX_EINVAL, "null bias-correction table for group %d", k);
+    if (G.t_offset[k] < 0) return fail(DSX_EINVAL, "negative t_offset for group %d", k);
   }
-  int64_t blocks = cus * bpc;
-  if (blocks > nchunks) blocks = nchunks;
-  // Blocks take chunks grid-stride, so any grid covers the table; keep it
-  // within HIP's 2^32 work-items per grid dimension.
-  if (blocks > kMaxGridBlocks) blocks = kMaxGridBlocks;
   hipStream_t s = as_stream(stream);
-  const dim3 grid((unsigned)blocks);
-  switch (grad_dtype) {
-    case DSX_BF16: launch_k3<DSX_BF16>(param_dtype, unroll, drain, grid, tensors, chunks, nchunks, scalars, s); break;
-    case DSX_F16: launch_k3<DSX_F16>(param_dtype, unroll, drain, grid, tensors, chunks, nchunks, scalars, s); break;
-    default: launch_k3<DSX_F32>(param_dtype, unroll, drain, grid, tensors, chunks, nchunks, scalars, s); break;
+  // Two launches where the fold applies and the list takes K3's one-chunk-
+  // per-block shape; else K1, K0, K3.
+  const bool fold = nchunks > 0 && fold_applies(numel, nparts) && nchunks <= kK3OneChunkPerCu * cu_count();
+  rc = do_unscale_norm_multi(tensors, chunks, nchunks, grad_dtype, state, partials, nparts, s,
+                             fold ? state : nullptr);
+  if (rc) return rc;
+  if (!fold) {
+    rc = do_finalize(partials, nparts, state, scaler, G, out, s);
+    if (!rc) rc = do_adamw_multi(tensors, chunks, nchunks, param_dtype, grad_dtype, out, s);
+    return rc;
   }
-  return launch_status("dsx_adamw_multi");
+  const dim3 grid((unsigned)(nchunks + 1));  // one chunk per block, and the writer
+  switch (grad_dtype) {
+    case DSX_BF16: launch_k3_fold<DSX_BF16>(param_dtype, grid, tensors, chunks, nchunks, partials, nparts, state,
+                                            scaler, G, out, s); break;
+    case DSX_F16: launch_k3_fold<DSX_F16>(param_dtype, grid, tensors, chunks, nchunks, partials, nparts, state,
+                                          scaler, G, out, s); break;
+    default: launch_k3_fold<DSX_F32>(param_dtype, grid, tensors, chunks, nchunks, partials, nparts, state, scaler,
+                                     G, out, s); break;
+  }
+  return launch_status("dsx_zero_step_multi (finalize folded in)");
 }
 
 }  // extern "C"

@@ -209,6 +209,24 @@ class _FusedAdamWBase(torch.optim.Optimizer):
                 post(self, args, kwargs)
         return out
 
+    def _refresh_group_block(self) -> None:
+        """The host group block (self._gblock: per-group hyper-parameters,
+        bias tables, t offsets) of the one-call steps, refilled only when a
+        value in param_groups or max_grad_norm changed or the bias tables
+        must grow."""
+        key = (tuple((float(g["lr"]), g["betas"], g["eps"], g["weight_decay"]) for g in self.param_groups),
+               self.max_grad_norm, self.clip_eps)
+        if key != self._gkey or self.steps_issued > self._gblock.bc_len:
+            hs, tables, bc_len = self._hypers()
+            blk = self._gblock
+            for k, h in enumerate(hs):
+                blk.hyper[k] = h
+                blk.bc_table[k] = tables[k].data_ptr()
+                blk.t_offset[k] = self._t_offsets[k]
+            blk.ngroups, blk.bc_len = len(hs), bc_len
+            self._gtables = tables  # the block holds their addresses
+            self._gkey = key
+
     def _hypers(self):
         hs, tabs = [], []
         for g in self.param_groups:
@@ -495,22 +513,10 @@ class AdamWOptimizer(_FusedAdamWBase):
         self._plan_args = (ctypes.byref(P), ctypes.byref(self._gblock))
 
     def _step_plan(self) -> None:
-        """K1 -> K0 -> K2 through dsx_zero_step_plan. The group block (the
-        per-group hyper-parameters and bias tables) is refilled only when a
-        value in param_groups or max_grad_norm changed, or the bias tables
-        must grow; the scaler settings only when they changed."""
-        key = (tuple((float(g["lr"]), g["betas"], g["eps"], g["weight_decay"]) for g in self.param_groups),
-               self.max_grad_norm, self.clip_eps)
-        if key != self._gkey or self.steps_issued > self._gblock.bc_len:
-            hs, tables, bc_len = self._hypers()
-            blk = self._gblock
-            for k, h in enumerate(hs):
-                blk.hyper[k] = h
-                blk.bc_table[k] = tables[k].data_ptr()
-                blk.t_offset[k] = self._t_offsets[k]
-            blk.ngroups, blk.bc_len = len(hs), bc_len
-            self._gtables = tables  # the block holds their addresses
-            self._gkey = key
+        """K1 -> K0 -> K2 (or K1 and K2 with K0 folded in) through
+        dsx_zero_step_plan. The group block is refilled only when it must be
+        (_refresh_group_block); the scaler settings only when they changed."""
+        self._refresh_group_block()
         sc = self.scaler
         skey = (sc.mode, sc.window, sc.hysteresis, sc.min_scale, sc.growth_factor, sc.backoff_factor)
         if skey != self._skey:
@@ -635,6 +641,9 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
         self._bind_state()
         self._k0 = ops.FinalizeGroups(self.partials, self.nparts, self.dstate, self.scalars, len(self.param_groups))
         self._plans_for = None  # the chunk table the bound K1 / K3 launches point at
+        self._gblock = _lib.DsxGroupsDev()  # the one-call step's host group block
+        self._gkey = None
+        self._one_call = None
 
     def _zero_grads_in_place(self) -> None:
         with torch.no_grad():
@@ -662,6 +671,15 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
                               st.master[i].numel(), base + ops.SCALARS_BYTES * st.group_of[i])
                              for i in st.k2_tensors]
             self._k2_meta = (pdt, gdt)
+            # The whole step in one call (dsx_zero_step_multi) when no tensor
+            # goes through K2: its fixed arguments, bound once per table.
+            self._one_call = None
+            if not st.k2_tensors:
+                self._one_call = (_lib.load().dsx_zero_step_multi,
+                                  (ops._ptr(table.tensors), ops._ptr(table.chunks), ctypes.c_int64(table.nchunks),
+                                   ctypes.c_int64(table.numel), table.pdt, table.gdt, ops._ptr(self.dstate)),
+                                  (ctypes.byref(self._gblock), ops._ptr(self.partials), int(self.nparts),
+                                   ops._ptr(self.scalars)))
             self._plans_for = table
         return self._k1, self._k3
 
@@ -692,8 +710,18 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
         self._note_stepped()
         k1, k3 = self._plans()
         self.steps_issued += 1
-        hs, tables, bc_len = self._hypers()
         s = ops.stream_of(self.device)
+        if self._one_call is not None and self._skip_host is None:
+            # one C call (K1, K0, K3, or K1 and K3 with K0 folded in); with
+            # track_skips on, the launches stay separate so that the skip
+            # flag's copy sits between K0 and K3
+            self._refresh_group_block()
+            fn, head, tail = self._one_call
+            rc = fn(*head, self.scaler.to_c(), *tail, s)
+            if rc:
+                raise _lib.DsxError("dsx_zero_step_multi", rc, _lib.last_error())
+            return
+        hs, tables, bc_len = self._hypers()
         k1(s)
         self._k0(self.scaler.to_c(), hs, tables, self._t_offsets, bc_len, s)
         self._after_finalize()

@@ -482,6 +482,22 @@ int dsx_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks,
                     int64_t nchunks, int param_dtype, int grad_dtype,
                     const DsxStepScalars* scalars, void* stream);
 
+/* The ragged list's whole step in one call: K1 over the list, K0 with the
+ * HOST group block `groups` (as dsx_finalize_groups takes it; checked here),
+ * K3 -- or, for lists of at most dsx_set_tuning_fold's bound in elements
+ * (numel, the sum of the chunk lengths) with at most 512 partials and at
+ * most 20 chunks per CU, two launches: K1 recording the entry values, and K3
+ * with K0's finalize folded in (every block decides the step with K0's code;
+ * one extra block writes the state and the records), the same bits. out
+ * holds groups->ngroups records. Replaces ZeROOptimizer.step over a list of
+ * tensors (Src/zero/optimizer.py:212-274, torch AdamW's per-tensor loop
+ * behind Src/zero/stage2.py:609-612). */
+int dsx_zero_step_multi(const DsxTensorRef* tensors, const DsxChunk* chunks,
+                        int64_t nchunks, int64_t numel, int param_dtype,
+                        int grad_dtype, DsxState* state, DsxScalerConfig scaler,
+                        const DsxGroupsDev* groups /* host */, double* partials,
+                        int32_t nparts, DsxStepScalars* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

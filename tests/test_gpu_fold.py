@@ -347,3 +347,74 @@ def test_dev_block_step_two_and_three_launches(gpu, case):
         assert moved == [True, False, False]
     else:
         assert s.error == 0 and s.t == 3 and all(x.skip == 0 for x in sc) and all(moved)
+
+
+@pytest.mark.parametrize("dtype_name", ["float16", "bfloat16"])
+def test_ragged_two_launch_step_matches_three_launches(gpu, dtype_name):
+    """The ragged form's one-call step (dsx_zero_step_multi): K1 over the
+    list and K3 with K0 folded in, against the same call with the fold off
+    (K1, K0, K3) and against separate launches (track_skips), bit for bit
+    over 12 steps: three parameter groups, one of them empty, a tensor whose
+    storage sits one element off 16-byte alignment (K3's element-wise path), a
+    NaN overflow (fp16: a dynamic scale backing off), a one-shot clip, and
+    the bias corrections of each group's betas."""
+    import torch
+    from distributedspeed_amd import _lib
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import MultiTensorAdamWOptimizer
+    dt = getattr(torch, dtype_name)
+    shapes = [(130, 7), (64, 33), (1000,), (5,), (40, 9)]
+    torch.manual_seed(8)
+    init = [torch.randn(s) * 0.05 for s in shapes]
+    fp16 = dt == torch.float16
+
+    def build(track):
+        ps = []
+        for k, t in enumerate(init):
+            if k == 2:  # storage one element past a 16-byte boundary
+                buf = torch.empty(t.numel() + 1, dtype=dt, device=gpu)
+                v = buf[1:].view(t.shape)
+                v.copy_(t)
+                ps.append(torch.nn.Parameter(v))
+            else:
+                ps.append(torch.nn.Parameter(t.clone().to(gpu, dt)))
+        groups = [{"params": ps[:2]}, {"params": [], "lr": 5e-3}, {"params": ps[2:], "lr": 2e-3, "betas": (0.8, 0.99)}]
+        sc = (ScalerConfig(mode="dynamic", init_scale=2.0 ** 8, window=3, hysteresis=1) if fp16
+              else ScalerConfig(mode="none"))
+        opt = MultiTensorAdamWOptimizer(groups, lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1, max_grad_norm=0.5,
+                                        param_dtype=dt, device=gpu, loss_scaler=sc)
+        opt.track_skips(track)
+        return opt
+
+    fold, three, split = build(False), build(False), build(True)
+    gen = torch.Generator(device=gpu).manual_seed(9)
+    _say(f"ragged fold vs three launches, {dtype_name}")
+    try:
+        for step in range(12):
+            for k, opts in enumerate(zip(fold.dsx_params, three.dsx_params, split.dsx_params)):
+                g = (torch.randn(opts[0].shape, device=gpu, generator=gen) * 1e-2 * (256 if fp16 else 1)).to(dt)
+                if step == 4 and k == 1:
+                    g.view(-1)[3] = float("nan")
+                for p in opts:
+                    p.grad = g.clone()
+            if step == 8:
+                na, nb, nc = (o.clip_grad_norm_(0.01) for o in (fold, three, split))
+                assert torch.equal(na, nb) and torch.equal(na, nc)
+            _lib.call("dsx_set_tuning_fold", ctypes.c_int64(FOLD_DEFAULT))
+            fold.step()
+            split.step()
+            _lib.call("dsx_set_tuning_fold", ctypes.c_int64(0))
+            three.step()
+    finally:
+        _lib.call("dsx_set_tuning_fold", ctypes.c_int64(FOLD_DEFAULT))
+    torch.cuda.synchronize()
+    for other, tag in ((three, "three launches"), (split, "separate launches")):
+        for i in range(len(shapes)):
+            a, b = fold.store.views_of(i), other.store.views_of(i)
+            for name in ("master", "exp_avg", "exp_avg_sq"):
+                assert torch.equal(a[name].view(torch.int32), b[name].view(torch.int32)), (tag, i, name)
+            assert torch.equal(fold.dsx_params[i].detach().view(torch.int16),
+                               other.dsx_params[i].detach().view(torch.int16)), (tag, i, "param16")
+        assert bytes(fold.read_state()) == bytes(other.read_state()), tag
+    st = fold.read_state()
+    assert st.t == 11 and st.overflow_count == 1 and st.error == 0
