@@ -192,6 +192,21 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.dsx_zero_step_dev(ctypes.byref(plan), al, None) == EINVAL
     assert b"group_end" in lib.dsx_last_error()
     plan.group_end[0] = 32
+    # the ragged one-call step
+    gb1 = _lib.DsxGroupsDev()
+    gb1.ngroups, gb1.bc_len = 1, 4
+    gb1.hyper[0] = _lib.DsxAdamwHyper(1e-3, 0.9, 0.999, 1e-8, 0.0, 0.0, 1e-6)
+    gb1.bc_table[0] = al
+    multi = lambda pdt, gdt, groups, nparts=1: lib.dsx_zero_step_multi(  # noqa: E731
+        al, al, 1, 16, pdt, gdt, al, scfg, groups, al, nparts, al, None)
+    assert multi(1, 1, None) == EINVAL
+    assert multi(0, 1, ctypes.byref(gb1)) == EINVAL and b"param16 dtype" in lib.dsx_last_error()
+    assert multi(1, 7, ctypes.byref(gb1)) == EINVAL
+    assert multi(1, 1, ctypes.byref(gb1), nparts=0) == EINVAL
+    gb1.ngroups = 0
+    assert multi(1, 1, ctypes.byref(gb1)) == EINVAL and b"ngroups" in lib.dsx_last_error()
+    gb1.ngroups, gb1.hyper[0].eps = 1, -1.0
+    assert multi(1, 1, ctypes.byref(gb1)) == EINVAL and b"epsilon" in lib.dsx_last_error()
     # tuning validation
     assert lib.dsx_set_tuning(8, 8, 3, 1) == EINVAL
     assert lib.dsx_set_tuning(0, 8, 4, 1) == EINVAL
