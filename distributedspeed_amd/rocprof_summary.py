@@ -21,7 +21,8 @@ import json
 import os
 
 KERNELS = {"k2_adamw_flat": 28, "k2_adamw_fold": 28, "k2_adamw_fold_dev": 28, "k1_unscale_norm": 2, "k0_finalize": 0,
-           "k0_finalize_dev": 0, "k2_adamw_multi": 28, "k1_unscale_norm_multi": 2, "k2_traffic_probe": 28}
+           "k0_finalize_dev": 0, "k2_adamw_multi": 28, "k3_adamw_fold": 28, "k1_unscale_norm_multi": 2,
+           "k2_traffic_probe": 28}
 
 # The launches of one step, by form: K1, K0 (None where the finalize is
 # folded into K2) and K2 (which may repeat: K2 over a partition above 2^26
@@ -34,6 +35,7 @@ STEP_FORMS = {
     "flat, eager, three launches": ("k1_unscale_norm", "k0_finalize", "k2_adamw_flat"),
     "flat, HIP graph replay, three launches": ("k1_unscale_norm", "k0_finalize_dev", "k2_adamw_flat"),
     "ragged (chunk table)": ("k1_unscale_norm_multi", "k0_finalize", "k2_adamw_multi"),
+    "ragged, two launches (K0 folded into K3)": ("k1_unscale_norm_multi", None, "k3_adamw_fold"),
 }
 COPY_NAME = "__amd_rocclr_copyBuffer"
 COPY_BYTES = 1 << 30
