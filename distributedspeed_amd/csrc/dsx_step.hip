@@ -1186,20 +1186,30 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __r
 // K3 with K0's finalize folded in (the ragged form of k2_adamw_fold, after a
 // K1 over the list launched with fold): every block reduces the partials in
 // K0's order and decides the step with K0's code on the entry values, then
-// steps its chunks with its group's scalars; the last block does no chunk
-// work and writes the step records and the state's updated fields. Chunks
-// go one per block (the small-list shape), grid-stride over the rest.
+// steps its chunk with its group's scalars; the last block does no chunk
+// work and writes the step records and the state's updated fields. One
+// chunk per block (the small-list shape: the grid is the chunk count and the
+// writer); 1 <= nparts <= kFoldMaxParts.
+// Chunk and tensor records of the block's chunk (uniform, never written by
+// a kernel), read through the constant address space: scalar loads, and the
+// pointers they hold are known to address global memory.
+typedef const DsxChunk __attribute__((address_space(4)))* ConstChunk;
+typedef const DsxTensorRef __attribute__((address_space(4)))* ConstTensorRef;
+
 template <int GD, int PD, bool NT>
 __global__ __launch_bounds__(kBlock) void k3_adamw_fold(const DsxTensorRef* __restrict__ tensors,
                                                         const DsxChunk* __restrict__ chunks, int64_t nchunks,
                                                         const double* __restrict__ partials, int32_t nparts,
                                                         DsxState* state, DsxScalerConfig scfg, DsxGroupsDev grp,
                                                         DsxStepScalars* __restrict__ out) {
+  using G = Grad<GD>;
+  using GS = typename G::slot4;
+  constexpr int U = 2;
   const int64_t slot_blocks = (int64_t)gridDim.x - 1;
-  double x = 0.0;
-  for (int i = threadIdx.x; i < nparts; i += kBlock) x += partials[i];  // reduce_partials' order
-  const double sumsq = block_sum_all(x);
   if (blockIdx.x == slot_blocks) {
+    double x = 0.0;
+    for (int i = threadIdx.x; i < nparts; i += kBlock) x += partials[i];  // reduce_partials' order
+    const double sumsq = block_sum_all(x);
     if (threadIdx.x == 0) {
       DsxState f = *state;
       f.clip_once = f.step_t2 & 1;  // K1 consumed the live flag into step_t2
@@ -1219,19 +1229,131 @@ __global__ __launch_bounds__(kBlock) void k3_adamw_fold(const DsxTensorRef* __re
     }
     return;
   }
+  // As in k2_adamw_fold: the entry values, the partials' loads and this
+  // block's chunk's first trip of slot loads are all issued before any is
+  // used (an unaligned chunk's slot loads read the tensor table instead, and
+  // are not used: every path issues the same loads).
+  int32_t t2 = state->step_t2;
+  float scale0 = state->step_scale, coef1 = state->clip_once_coef;
+  double pv[kFoldParts];
+#pragma unroll
+  for (int j = 0; j < kFoldParts; ++j) {
+    const int i = threadIdx.x + j * kBlock;
+    const double x = partials[i < nparts ? i : nparts - 1];
+    pv[j] = i < nparts ? x : 0.0;
+  }
+  const int64_t c0 = blockIdx.x;  // < nchunks: nchunks slot blocks and the writer
+  DsxChunk ch;
+  {
+    const ConstChunk cc = (ConstChunk)(uintptr_t)(chunks + c0);
+    ch.tensor = cc->tensor;
+    ch.reserved = 0;
+    ch.start = cc->start;
+    ch.len = cc->len;
+  }
+  DsxTensorRef tr;
+  {
+    const ConstTensorRef ct = (ConstTensorRef)(uintptr_t)(tensors + ch.tensor);
+    tr.master = ct->master;
+    tr.exp_avg = ct->exp_avg;
+    tr.exp_avg_sq = ct->exp_avg_sq;
+    tr.param16 = ct->param16;
+    tr.grad = ct->grad;
+    tr.numel = ct->numel;
+    tr.group = ct->group;
+    tr.reserved = 0;
+  }
+  float* p = tr.master + ch.start;
+  float* m = tr.exp_avg + ch.start;
+  float* v = tr.exp_avg_sq + ch.start;
+  uint16_t* p16 = tr.param16 ? static_cast<uint16_t*>(tr.param16) + ch.start : nullptr;
+  const typename G::elem* g = static_cast<const typename G::elem*>(tr.grad) + ch.start;
+  const int64_t nvec = ch.len >> 2;
+  const bool vec = nvec > 0 &&
+                   !((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(m) |
+                      reinterpret_cast<uintptr_t>(v)) & 15u) &&
+                   !(reinterpret_cast<uintptr_t>(g) & (sizeof(GS) - 1)) &&
+                   !(p16 && (reinterpret_cast<uintptr_t>(p16) & 7u));
+  const f4* lp = vec ? reinterpret_cast<const f4*>(p) : reinterpret_cast<const f4*>(tensors);
+  const f4* lm = vec ? reinterpret_cast<const f4*>(m) : reinterpret_cast<const f4*>(tensors);
+  const f4* lv = vec ? reinterpret_cast<const f4*>(v) : reinterpret_cast<const f4*>(tensors);
+  const GS* lg = vec ? reinterpret_cast<const GS*>(g) : reinterpret_cast<const GS*>(tensors);
+  GS Gs[U];
+  f4 P[U], M[U], V[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int64_t i = (int64_t)threadIdx.x + (int64_t)u * kBlock;
+    i = !vec ? 0 : (i < nvec ? i : nvec - 1);
+    Gs[u] = ld<NT>(lg + i);
+    P[u] = ld<NT>(lp + i);
+    M[u] = ld<NT>(lm + i);
+    V[u] = ld<NT>(lv + i);
+  }
+  asm volatile("" ::: "memory");  // the slot loads issue here
+  asm volatile("" : "+v"(t2), "+v"(scale0), "+v"(coef1));
   DsxState s = {};
-  const int32_t t2 = state->step_t2;
-  s.scale = state->step_scale;
+  s.scale = scale0;
+  t2 = __builtin_amdgcn_readfirstlane(t2);
   s.t = t2 >> 1;
   s.clip_once = t2 & 1;
-  s.clip_once_coef = state->clip_once_coef;
+  s.clip_once_coef = coef1;
+  double bc1 = 1.0, bc2s = 1.0;
+  if (tr.group < grp.ngroups) bc_of(grp, tr.group, s.t + 1, bc1, bc2s);
+  asm volatile("" : "+v"(pv[0]), "+v"(pv[1]));
+  double x = 0.0;
+#pragma unroll
+  for (int j = 0; j < kFoldParts; ++j) x += pv[j];  // reduce_partials' order
+  const double sumsq = block_sum_all(x);
   const Decision d = decide(sumsq, s, grp, false);
-  if (d.skip) return;
-  for (int64_t c = blockIdx.x; c < nchunks; c += slot_blocks) {
-    const DsxChunk ch = chunks[c];
-    const DsxTensorRef tr = tensors[ch.tensor];
-    if (tr.group >= d.ng) continue;
-    k3_chunk<GD, PD, 2, NT, false>(tr, ch, uniform_sc(load_sc(record(d, s, grp, tr.group, sumsq))));
+  if (d.skip || tr.group >= d.ng) return;
+  const Sc sc = uniform_sc(load_sc(record_bc(d, s, grp, tr.group, sumsq, bc1, bc2s)));
+  const bool cast = p16 != nullptr;
+  if (!vec) {  // element by element (k3_chunk's path for such a chunk)
+    for (int64_t e = threadIdx.x; e < ch.len; e += kBlock) {
+      float pe = p[e], me = m[e], ve = v[e];
+      adamw_elt(G::one(g[e]), pe, me, ve, sc);
+      p[e] = pe; m[e] = me; v[e] = ve;
+      if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
+    }
+    return;
+  }
+  f4* p4 = reinterpret_cast<f4*>(p);
+  f4* m4 = reinterpret_cast<f4*>(m);
+  f4* v4 = reinterpret_cast<f4*>(v);
+  u2* o2 = reinterpret_cast<u2*>(p16);
+  const GS* g4 = reinterpret_cast<const GS*>(g);
+  for (int64_t i0 = threadIdx.x;;) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * kBlock;
+      if (i < nvec) {
+        float gf[4];
+        G::four(Gs[u], gf);
+        f4 pp = P[u], mm = M[u], vv = V[u];
+        adamw4(gf, pp, mm, vv, sc);
+        st<NT>(p4 + i, pp);
+        st<NT>(m4 + i, mm);
+        st<NT>(v4 + i, vv);
+        if (cast) st<NT>(o2 + i, pack4<PD>(pp));
+      }
+    }
+    i0 += (int64_t)kBlock * U;
+    if (i0 >= nvec) break;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int64_t i = i0 + (int64_t)u * kBlock;
+      i = i < nvec ? i : nvec - 1;
+      Gs[u] = ld<NT>(g4 + i);
+      P[u] = ld<NT>(p4 + i);
+      M[u] = ld<NT>(m4 + i);
+      V[u] = ld<NT>(v4 + i);
+    }
+  }
+  for (int64_t e = (nvec << 2) + threadIdx.x; e < ch.len; e += kBlock) {
+    float pe = p[e], me = m[e], ve = v[e];
+    adamw_elt(G::one(g[e]), pe, me, ve, sc);
+    p[e] = pe; m[e] = me; v[e] = ve;
+    if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
   }
 }
 
