@@ -1106,53 +1106,142 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorR
   if (threadIdx.x == 0) partials[blockIdx.x] = s;
 }
 
-// One chunk of K3: the K2 slot loop (U slots per thread, all of a trip's
-// loads before any use) where every array is aligned for its 4-element
-// slot, element by element otherwise.
+// Chunk and tensor records (kernel-invariant: the host or an earlier launch
+// wrote them), read through the constant address space: scalar loads, and
+// the pointers a tensor record holds are then known to address global
+// memory, so a chunk's slot accesses compile to global loads and stores,
+// counted by vmcnt alone (flat ones also count on lgkmcnt, which ties every
+// wait for a scalar record to the stores still in flight).
+typedef const DsxChunk __attribute__((address_space(4)))* ConstChunk;
+typedef const DsxTensorRef __attribute__((address_space(4)))* ConstTensorRef;
+typedef const DsxStepScalars __attribute__((address_space(4)))* ConstScalars;
+
+__device__ __forceinline__ DsxChunk chunk_rec(const DsxChunk* chunks, int64_t c) {
+  const ConstChunk cc = (ConstChunk)(uintptr_t)(chunks + c);
+  DsxChunk ch;
+  ch.tensor = cc->tensor;
+  ch.reserved = 0;
+  ch.start = cc->start;
+  ch.len = cc->len;
+  return ch;
+}
+
+__device__ __forceinline__ DsxTensorRef tensor_rec(const DsxTensorRef* tensors, int32_t t) {
+  const ConstTensorRef ct = (ConstTensorRef)(uintptr_t)(tensors + t);
+  DsxTensorRef tr;
+  tr.master = ct->master;
+  tr.exp_avg = ct->exp_avg;
+  tr.exp_avg_sq = ct->exp_avg_sq;
+  tr.param16 = ct->param16;
+  tr.grad = ct->grad;
+  tr.numel = ct->numel;
+  tr.group = ct->group;
+  tr.reserved = 0;
+  return tr;
+}
+
+__device__ __forceinline__ Sc scalars_rec(const DsxStepScalars* scalars, int32_t group) {
+  const ConstScalars cs = (ConstScalars)(uintptr_t)(scalars + group);
+  Sc r;
+  r.inv = cs->inv_scale; r.coef = cs->clip_coef; r.decay = cs->decay;
+  r.w1 = cs->w1; r.w1c = cs->w1c; r.b2 = cs->b2; r.val2 = cs->val2;
+  r.eps = cs->eps; r.bc2s = cs->bc2s; r.nss = cs->nss;
+  r.small = fabsf(r.w1) < 0.5f;
+  return r;
+}
+
+// One chunk's arrays, and whether every one is aligned for its 4-element slot
+// (vec: the K2 slot loop; otherwise element by element).
+template <int GD>
+struct ChunkView {
+  float* p;
+  float* m;
+  float* v;
+  uint16_t* p16;
+  const typename Grad<GD>::elem* g;
+  int64_t len, nvec;
+  bool vec;
+};
+
+template <int GD>
+__device__ __forceinline__ ChunkView<GD> chunk_view(const DsxTensorRef& tr, const DsxChunk& ch) {
+  using G = Grad<GD>;
+  ChunkView<GD> c;
+  c.p = tr.master + ch.start;
+  c.m = tr.exp_avg + ch.start;
+  c.v = tr.exp_avg_sq + ch.start;
+  c.p16 = tr.param16 ? static_cast<uint16_t*>(tr.param16) + ch.start : nullptr;
+  c.g = static_cast<const typename G::elem*>(tr.grad) + ch.start;
+  c.len = ch.len;
+  c.nvec = ch.len >> 2;
+  c.vec = c.nvec > 0 &&
+          !((reinterpret_cast<uintptr_t>(c.p) | reinterpret_cast<uintptr_t>(c.m) |
+             reinterpret_cast<uintptr_t>(c.v)) & 15u) &&
+          !(reinterpret_cast<uintptr_t>(c.g) & (sizeof(typename G::slot4) - 1)) &&
+          !(c.p16 && (reinterpret_cast<uintptr_t>(c.p16) & 7u));
+  return c;
+}
+
+// A trip of U slots per thread in registers.
+template <int GD, int U>
+struct Trip {
+  typename Grad<GD>::slot4 g[U];
+  f4 p[U], m[U], v[U];
+};
+
+// Issue a chunk's first trip of slot loads. Every thread issues the same
+// loads whatever the chunk: indices clamped into the chunk, and for a chunk
+// off the slot path loads from `spare` (a readable 16-byte-aligned address
+// whose values go unused), so that the waits for them stay exact.
+template <int GD, int U, bool NT>
+__device__ __forceinline__ void first_trip(const ChunkView<GD>& c, const void* spare, Trip<GD, U>& T) {
+  using GS = typename Grad<GD>::slot4;
+  const f4* lp = c.vec ? reinterpret_cast<const f4*>(c.p) : static_cast<const f4*>(spare);
+  const f4* lm = c.vec ? reinterpret_cast<const f4*>(c.m) : static_cast<const f4*>(spare);
+  const f4* lv = c.vec ? reinterpret_cast<const f4*>(c.v) : static_cast<const f4*>(spare);
+  const GS* lg = c.vec ? reinterpret_cast<const GS*>(c.g) : static_cast<const GS*>(spare);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int64_t i = (int64_t)threadIdx.x + (int64_t)u * kBlock;
+    i = !c.vec ? 0 : (i < c.nvec ? i : c.nvec - 1);
+    T.g[u] = ld<NT>(lg + i);
+    T.p[u] = ld<NT>(lp + i);
+    T.m[u] = ld<NT>(lm + i);
+    T.v[u] = ld<NT>(lv + i);
+  }
+}
+
+// Step a chunk whose first trip first_trip has loaded: the K2 slot loop (U
+// slots per thread, each trip's loads issued before the previous trip's
+// math), then the tail elements; element by element for a chunk off the slot
+// path.
 template <int GD, int PD, int U, bool NT, bool DRAIN>
-__device__ __forceinline__ void k3_chunk(const DsxTensorRef& tr, const DsxChunk& ch, const Sc& s) {
+__device__ __forceinline__ void chunk_steps(const ChunkView<GD>& c, Trip<GD, U>& T, const Sc& sc) {
   using G = Grad<GD>;
   using GS = typename G::slot4;
-  float* p = tr.master + ch.start;
-  float* m = tr.exp_avg + ch.start;
-  float* v = tr.exp_avg_sq + ch.start;
-  uint16_t* p16 = tr.param16 ? static_cast<uint16_t*>(tr.param16) + ch.start : nullptr;
-  const typename G::elem* g = static_cast<const typename G::elem*>(tr.grad) + ch.start;
-  const bool cast = p16 != nullptr;
-  const int64_t len = ch.len;
-  const uintptr_t mis = (reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(m) |
-                         reinterpret_cast<uintptr_t>(v)) & 15u;
-  const uintptr_t gmis = reinterpret_cast<uintptr_t>(g) & (sizeof(GS) - 1);
-  const uintptr_t omis = cast ? (reinterpret_cast<uintptr_t>(p16) & 7u) : 0;
+  const bool cast = c.p16 != nullptr;
   int64_t done = 0;
-  if (!mis && !gmis && !omis) {
-    f4* p4 = reinterpret_cast<f4*>(p);
-    f4* m4 = reinterpret_cast<f4*>(m);
-    f4* v4 = reinterpret_cast<f4*>(v);
-    u2* o2 = reinterpret_cast<u2*>(p16);
-    const GS* g4 = reinterpret_cast<const GS*>(g);
-    const int64_t nvec = len >> 2;
-    for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += (int64_t)kBlock * U) {
-      GS Gs[U];
-      f4 P[U], M[U], V[U];
+  if (c.vec) {
+    f4* p4 = reinterpret_cast<f4*>(c.p);
+    f4* m4 = reinterpret_cast<f4*>(c.m);
+    f4* v4 = reinterpret_cast<f4*>(c.v);
+    u2* o2 = reinterpret_cast<u2*>(c.p16);
+    const GS* g4 = reinterpret_cast<const GS*>(c.g);
+    for (int64_t i0 = threadIdx.x;;) {
+      // Every slot's loads are taken in here, on every path: a slot past the
+      // end (a clamped copy, dropped below) would otherwise leave its loads
+      // pending into the next trip, whose first register writes would then
+      // wait for this trip's stores too.
+#pragma unroll
+      for (int u = 0; u < U; ++u) asm volatile("" : "+v"(T.g[u]), "+v"(T.p[u]), "+v"(T.m[u]), "+v"(T.v[u]));
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t i = i0 + (int64_t)u * kBlock;
-        if (i < nvec) {
-          Gs[u] = ld<NT>(g4 + i);
-          P[u] = ld<NT>(p4 + i);
-          M[u] = ld<NT>(m4 + i);
-          V[u] = ld<NT>(v4 + i);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t i = i0 + (int64_t)u * kBlock;
-        if (i < nvec) {
+        if (i < c.nvec) {
           float gf[4];
-          G::four(Gs[u], gf);
-          f4 pp = P[u], mm = M[u], vv = V[u];
-          adamw4(gf, pp, mm, vv, s);
+          G::four(T.g[u], gf);
+          f4 pp = T.p[u], mm = T.m[u], vv = T.v[u];
+          adamw4(gf, pp, mm, vv, sc);
           st<NT>(p4 + i, pp);
           st<NT>(m4 + i, mm);
           st<NT>(v4 + i, vv);
@@ -1160,26 +1249,53 @@ __device__ __forceinline__ void k3_chunk(const DsxTensorRef& tr, const DsxChunk&
         }
       }
       if constexpr (DRAIN) __builtin_amdgcn_s_waitcnt(0);  // as in k2_adamw_flat
+      i0 += (int64_t)kBlock * U;
+      if (i0 >= c.nvec) break;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        int64_t i = i0 + (int64_t)u * kBlock;
+        i = i < c.nvec ? i : c.nvec - 1;
+        T.g[u] = ld<NT>(g4 + i);
+        T.p[u] = ld<NT>(p4 + i);
+        T.m[u] = ld<NT>(m4 + i);
+        T.v[u] = ld<NT>(v4 + i);
+      }
     }
-    done = nvec << 2;
+    done = c.nvec << 2;
   }
-  for (int64_t e = done + threadIdx.x; e < len; e += kBlock) {
-    float pe = p[e], me = m[e], ve = v[e];
-    adamw_elt(G::one(g[e]), pe, me, ve, s);
-    p[e] = pe; m[e] = me; v[e] = ve;
-    if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
+  for (int64_t e = done + threadIdx.x; e < c.len; e += kBlock) {
+    float pe = c.p[e], me = c.m[e], ve = c.v[e];
+    adamw_elt(G::one(c.g[e]), pe, me, ve, sc);
+    c.p[e] = pe; c.m[e] = me; c.v[e] = ve;
+    if (cast) c.p16[e] = (uint16_t)f2h<PD>(pe);
   }
 }
 
+// K3: AdamW + cast over a chunk table. Block b steps chunks b, b + grid, ...
+// Each chunk's records are read while the block works: the next chunk's
+// record (a line of the table no block has read yet, so a trip to memory) is
+// requested once this chunk's first slot loads and its group's scalars are
+// in, and is consumed after this chunk's last trip.
 template <int GD, int PD, int U, bool NT, bool DRAIN>
 __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __restrict__ tensors,
                                                          const DsxChunk* __restrict__ chunks, int64_t nchunks,
                                                          const DsxStepScalars* __restrict__ scalars) {
-  if (scalars[0].skip) return;  // the skip decision is global
-  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
-    const DsxChunk ch = chunks[c];
-    const DsxTensorRef tr = tensors[ch.tensor];
-    k3_chunk<GD, PD, U, NT, DRAIN>(tr, ch, load_sc(scalars[tr.group]));
+  if (((ConstScalars)(uintptr_t)scalars)->skip) return;  // the skip decision is global
+  int64_t c = blockIdx.x;  // < nchunks: the grid is at most the chunk count
+  DsxChunk ch = chunk_rec(chunks, c);
+  for (;;) {
+    const DsxTensorRef tr = tensor_rec(tensors, ch.tensor);
+    const ChunkView<GD> cv = chunk_view<GD>(tr, ch);
+    Trip<GD, U> T;
+    first_trip<GD, U, NT>(cv, tensors, T);
+    const Sc sc = scalars_rec(scalars, tr.group);
+    asm volatile("" ::"s"(sc.nss) : "memory");  // the scalars are in before the next record is asked for
+    const int64_t cn = c + gridDim.x;
+    const DsxChunk chn = chunk_rec(chunks, cn < nchunks ? cn : c);
+    chunk_steps<GD, PD, U, NT, DRAIN>(cv, T, sc);
+    if (cn >= nchunks) break;
+    c = cn;
+    ch = chn;
   }
 }
 
@@ -1190,20 +1306,12 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __r
 // work and writes the step records and the state's updated fields. One
 // chunk per block (the small-list shape: the grid is the chunk count and the
 // writer); 1 <= nparts <= kFoldMaxParts.
-// Chunk and tensor records of the block's chunk (uniform, never written by
-// a kernel), read through the constant address space: scalar loads, and the
-// pointers they hold are known to address global memory.
-typedef const DsxChunk __attribute__((address_space(4)))* ConstChunk;
-typedef const DsxTensorRef __attribute__((address_space(4)))* ConstTensorRef;
-
 template <int GD, int PD, bool NT>
 __global__ __launch_bounds__(kBlock) void k3_adamw_fold(const DsxTensorRef* __restrict__ tensors,
                                                         const DsxChunk* __restrict__ chunks, int64_t nchunks,
                                                         const double* __restrict__ partials, int32_t nparts,
                                                         DsxState* state, DsxScalerConfig scfg, DsxGroupsDev grp,
                                                         DsxStepScalars* __restrict__ out) {
-  using G = Grad<GD>;
-  using GS = typename G::slot4;
   constexpr int U = 2;
   const int64_t slot_blocks = (int64_t)gridDim.x - 1;
   if (blockIdx.x == slot_blocks) {
@@ -1242,53 +1350,11 @@ __global__ __launch_bounds__(kBlock) void k3_adamw_fold(const DsxTensorRef* __re
     const double x = partials[i < nparts ? i : nparts - 1];
     pv[j] = i < nparts ? x : 0.0;
   }
-  const int64_t c0 = blockIdx.x;  // < nchunks: nchunks slot blocks and the writer
-  DsxChunk ch;
-  {
-    const ConstChunk cc = (ConstChunk)(uintptr_t)(chunks + c0);
-    ch.tensor = cc->tensor;
-    ch.reserved = 0;
-    ch.start = cc->start;
-    ch.len = cc->len;
-  }
-  DsxTensorRef tr;
-  {
-    const ConstTensorRef ct = (ConstTensorRef)(uintptr_t)(tensors + ch.tensor);
-    tr.master = ct->master;
-    tr.exp_avg = ct->exp_avg;
-    tr.exp_avg_sq = ct->exp_avg_sq;
-    tr.param16 = ct->param16;
-    tr.grad = ct->grad;
-    tr.numel = ct->numel;
-    tr.group = ct->group;
-    tr.reserved = 0;
-  }
-  float* p = tr.master + ch.start;
-  float* m = tr.exp_avg + ch.start;
-  float* v = tr.exp_avg_sq + ch.start;
-  uint16_t* p16 = tr.param16 ? static_cast<uint16_t*>(tr.param16) + ch.start : nullptr;
-  const typename G::elem* g = static_cast<const typename G::elem*>(tr.grad) + ch.start;
-  const int64_t nvec = ch.len >> 2;
-  const bool vec = nvec > 0 &&
-                   !((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(m) |
-                      reinterpret_cast<uintptr_t>(v)) & 15u) &&
-                   !(reinterpret_cast<uintptr_t>(g) & (sizeof(GS) - 1)) &&
-                   !(p16 && (reinterpret_cast<uintptr_t>(p16) & 7u));
-  const f4* lp = vec ? reinterpret_cast<const f4*>(p) : reinterpret_cast<const f4*>(tensors);
-  const f4* lm = vec ? reinterpret_cast<const f4*>(m) : reinterpret_cast<const f4*>(tensors);
-  const f4* lv = vec ? reinterpret_cast<const f4*>(v) : reinterpret_cast<const f4*>(tensors);
-  const GS* lg = vec ? reinterpret_cast<const GS*>(g) : reinterpret_cast<const GS*>(tensors);
-  GS Gs[U];
-  f4 P[U], M[U], V[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    int64_t i = (int64_t)threadIdx.x + (int64_t)u * kBlock;
-    i = !vec ? 0 : (i < nvec ? i : nvec - 1);
-    Gs[u] = ld<NT>(lg + i);
-    P[u] = ld<NT>(lp + i);
-    M[u] = ld<NT>(lm + i);
-    V[u] = ld<NT>(lv + i);
-  }
+  const DsxChunk ch = chunk_rec(chunks, blockIdx.x);  // < nchunks: nchunks slot blocks and the writer
+  const DsxTensorRef tr = tensor_rec(tensors, ch.tensor);
+  const ChunkView<GD> cv = chunk_view<GD>(tr, ch);
+  Trip<GD, U> T;
+  first_trip<GD, U, NT>(cv, tensors, T);
   asm volatile("" ::: "memory");  // the slot loads issue here
   asm volatile("" : "+v"(t2), "+v"(scale0), "+v"(coef1));
   DsxState s = {};
@@ -1307,54 +1373,7 @@ __global__ __launch_bounds__(kBlock) void k3_adamw_fold(const DsxTensorRef* __re
   const Decision d = decide(sumsq, s, grp, false);
   if (d.skip || tr.group >= d.ng) return;
   const Sc sc = uniform_sc(load_sc(record_bc(d, s, grp, tr.group, sumsq, bc1, bc2s)));
-  const bool cast = p16 != nullptr;
-  if (!vec) {  // element by element (k3_chunk's path for such a chunk)
-    for (int64_t e = threadIdx.x; e < ch.len; e += kBlock) {
-      float pe = p[e], me = m[e], ve = v[e];
-      adamw_elt(G::one(g[e]), pe, me, ve, sc);
-      p[e] = pe; m[e] = me; v[e] = ve;
-      if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
-    }
-    return;
-  }
-  f4* p4 = reinterpret_cast<f4*>(p);
-  f4* m4 = reinterpret_cast<f4*>(m);
-  f4* v4 = reinterpret_cast<f4*>(v);
-  u2* o2 = reinterpret_cast<u2*>(p16);
-  const GS* g4 = reinterpret_cast<const GS*>(g);
-  for (int64_t i0 = threadIdx.x;;) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = i0 + (int64_t)u * kBlock;
-      if (i < nvec) {
-        float gf[4];
-        G::four(Gs[u], gf);
-        f4 pp = P[u], mm = M[u], vv = V[u];
-        adamw4(gf, pp, mm, vv, sc);
-        st<NT>(p4 + i, pp);
-        st<NT>(m4 + i, mm);
-        st<NT>(v4 + i, vv);
-        if (cast) st<NT>(o2 + i, pack4<PD>(pp));
-      }
-    }
-    i0 += (int64_t)kBlock * U;
-    if (i0 >= nvec) break;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int64_t i = i0 + (int64_t)u * kBlock;
-      i = i < nvec ? i : nvec - 1;
-      Gs[u] = ld<NT>(g4 + i);
-      P[u] = ld<NT>(p4 + i);
-      M[u] = ld<NT>(m4 + i);
-      V[u] = ld<NT>(v4 + i);
-    }
-  }
-  for (int64_t e = (nvec << 2) + threadIdx.x; e < ch.len; e += kBlock) {
-    float pe = p[e], me = m[e], ve = v[e];
-    adamw_elt(G::one(g[e]), pe, me, ve, sc);
-    p[e] = pe; m[e] = me; v[e] = ve;
-    if (cast) p16[e] = (uint16_t)f2h<PD>(pe);
-  }
+  chunk_steps<GD, PD, U, NT, false>(cv, T, sc);
 }
 
 // ---- host-side dispatch ----------------------------------------------------------
