@@ -581,3 +581,51 @@ def test_k3_launch_shapes_give_identical_bits(gpu, oracle):
             assert np.array_equal(torch16_to_np(tp16)[covered], gp16[covered]), shape
     finally:
         _lib.call("dsx_set_tuning_multi", 0, 1, 1, -1)
+
+
+def test_k3_several_chunks_per_block_give_identical_bits(gpu, oracle):
+    """K3 with more chunks than blocks, so that every block steps several in
+    turn (each chunk's records read while the previous one streams): 700
+    tensors of 1 to 20000 elements, every third one off the 16-byte grid
+    (element-wise path) and the others with ragged tails, in 4096-element
+    chunks; one block per CU with 1, 2 and 4 slots, drain on and off.
+    Bit-identical to K2 over the same elements."""
+    import torch
+    from distributedspeed_amd import _lib, ops
+    O = oracle
+    rng = np.random.default_rng(31)
+    sizes = [int(x) for x in rng.integers(1, 20001, size=700)]
+    offs, pos = [], 0
+    for i, s in enumerate(sizes):
+        pos = (pos + 3) // 4 * 4 + (1 if i % 3 == 2 else 0)
+        offs.append(pos)
+        pos += s
+    total = pos
+    p, m, v, g16 = make_state(total, 13, F16, 1e-3 * 1024)
+    sc = O.step_scalars(O.Hyper(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01), 3, 1.0 / 1024, 0.6)
+    gp, gm, gv, gp16 = _run_k2(gpu, p, m, v, g16, F16, F16, sc)
+    hs = _lib.DsxStepScalars()
+    for k in ("inv_scale", "clip_coef", "decay", "w1", "w1c", "b2", "val2", "eps", "bc2s", "nss"):
+        setattr(hs, k, getattr(sc, k))
+    covered = np.zeros(total, bool)
+    for o, s in zip(offs, sizes):
+        covered[o:o + s] = True
+    try:
+        for shape in ((1, 1, 1, 0), (1, 2, 1, 0), (1, 2, 1, 1), (1, 4, 1, 1), (1, 2, 0, 0)):
+            _lib.call("dsx_set_tuning_multi", *shape)
+            tp, tm, tv = (f32_to_torch(a, gpu) for a in (p, m, v))
+            tg = np16_to_torch(g16, F16, gpu)
+            tp16 = torch.zeros(total, dtype=torch.float16, device=gpu)
+            views = lambda t: [t[o:o + s] for o, s in zip(offs, sizes)]  # noqa: E731
+            table = ops.ChunkTable(views(tp), views(tm), views(tv), views(tp16), views(tg), chunk_elems=4096)
+            _say(f"k3 shape {shape}, {table.nchunks} chunks")
+            assert table.nchunks > 2 * 256  # more chunks than any one-block-per-CU grid holds
+            ops.adamw_multi(table, ops.scalars_from_host(hs, gpu))
+            torch.cuda.synchronize()
+            for name, a, b in (("master", tp.cpu().numpy(), gp), ("exp_avg", tm.cpu().numpy(), gm),
+                               ("exp_avg_sq", tv.cpu().numpy(), gv)):
+                assert np.array_equal(a[covered].view(np.uint32), b[covered].view(np.uint32)), (name, shape)
+            assert np.array_equal(torch16_to_np(tp16)[covered], gp16[covered]), shape
+            assert not torch16_to_np(tp16)[~covered].any()  # nothing written between the tensors
+    finally:
+        _lib.call("dsx_set_tuning_multi", 0, 1, 1, -1)
