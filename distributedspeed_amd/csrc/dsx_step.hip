@@ -1061,51 +1061,6 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_fold(float* __restrict__ p, f
 
 // ---- K3: ragged lists ----------------------------------------------------------
 
-template <int GD>
-__global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorRef* __restrict__ tensors,
-                                                                const DsxChunk* __restrict__ chunks,
-                                                                int64_t nchunks, const DsxState* state,
-                                                                double* __restrict__ partials, DsxState* fold) {
-  using G = Grad<GD>;
-  const float inv = inv_of(state->scale);
-  if (fold != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {  // as k1_unscale_norm
-    const int32_t armed = fold->clip_once != 0 ? 1 : 0;
-    fold->step_scale = fold->scale;
-    fold->step_t2 = 2 * fold->t + armed;
-    fold->clip_once = 0;
-  }
-  double acc = 0.0;
-  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
-    const DsxChunk ch = chunks[c];
-    const typename G::elem* g = static_cast<const typename G::elem*>(tensors[ch.tensor].grad) + ch.start;
-    const int64_t len = ch.len;
-    int64_t done = 0;
-    if (aligned16(g)) {
-      // four 16-byte nontemporal loads in flight per thread before any use
-      constexpr int U = 4;
-      const u4* g16 = reinterpret_cast<const u4*>(g);
-      const int64_t nvec = len / G::per16;
-      for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += kBlock * U) {
-        u4 S[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int64_t i = i0 + (int64_t)u * kBlock;
-          S[u] = (i < nvec) ? ld<true>(g16 + i) : u4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) acc = G::sumsq16(S[u], inv, acc);
-      }
-      done = nvec * G::per16;
-    }
-    for (int64_t e = done + threadIdx.x; e < len; e += kBlock) {
-      const float a = G::one(g[e]) * inv;
-      acc = __builtin_fma((double)a, (double)a, acc);
-    }
-  }
-  const double s = block_sum(acc);
-  if (threadIdx.x == 0) partials[blockIdx.x] = s;
-}
-
 // Chunk and tensor records (kernel-invariant: the host or an earlier launch
 // wrote them), read through the constant address space: scalar loads, and
 // the pointers a tensor record holds are then known to address global
@@ -1148,6 +1103,63 @@ __device__ __forceinline__ Sc scalars_rec(const DsxStepScalars* scalars, int32_t
   r.eps = cs->eps; r.bc2s = cs->bc2s; r.nss = cs->nss;
   r.small = fabsf(r.w1) < 0.5f;
   return r;
+}
+
+// K1 over a chunk table. Block b reduces chunks b, b + grid, ... in order,
+// each as K1's slot loop (four 16-byte loads per thread in flight before any
+// use) when its grad is 16-byte aligned, element by element otherwise. The
+// next chunk's record is requested with the current chunk's tensor record, so
+// that it is in by the time the current chunk is done.
+template <int GD>
+__global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorRef* __restrict__ tensors,
+                                                                const DsxChunk* __restrict__ chunks,
+                                                                int64_t nchunks, const DsxState* state,
+                                                                double* __restrict__ partials, DsxState* fold) {
+  using G = Grad<GD>;
+  constexpr int U = 4;
+  const float inv = inv_of(state->scale);
+  if (fold != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {  // as k1_unscale_norm
+    const int32_t armed = fold->clip_once != 0 ? 1 : 0;
+    fold->step_scale = fold->scale;
+    fold->step_t2 = 2 * fold->t + armed;
+    fold->clip_once = 0;
+  }
+  double acc = 0.0;
+  const int64_t stride = gridDim.x;
+  int64_t c = blockIdx.x;
+  if (c < nchunks) {  // the grid is the partial count, which may exceed the chunk count
+    DsxChunk ch = chunk_rec(chunks, c);
+    for (;;) {
+      const typename G::elem* g = static_cast<const typename G::elem*>(tensor_rec(tensors, ch.tensor).grad) + ch.start;
+      const int64_t cn = c + stride;
+      const DsxChunk chn = chunk_rec(chunks, cn < nchunks ? cn : c);
+      int64_t done = 0;
+      if (aligned16(g)) {
+        const u4* g16 = reinterpret_cast<const u4*>(g);
+        const int64_t nvec = ch.len / G::per16;
+        for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += kBlock * U) {
+          u4 S[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + (int64_t)u * kBlock;
+            S[u] = (i < nvec) ? ld<true>(g16 + i) : u4{0u, 0u, 0u, 0u};
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc = G::sumsq16(S[u], inv, acc);
+        }
+        done = nvec * G::per16;
+      }
+      for (int64_t e = done + threadIdx.x; e < ch.len; e += kBlock) {
+        const float a = G::one(g[e]) * inv;
+        acc = __builtin_fma((double)a, (double)a, acc);
+      }
+      if (cn >= nchunks) break;
+      c = cn;
+      ch = chn;
+    }
+  }
+  const double s = block_sum(acc);
+  if (threadIdx.x == 0) partials[blockIdx.x] = s;
 }
 
 // One chunk's arrays, and whether every one is aligned for its 4-element slot
@@ -1281,6 +1293,7 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __r
                                                          const DsxChunk* __restrict__ chunks, int64_t nchunks,
                                                          const DsxStepScalars* __restrict__ scalars) {
   if (((ConstScalars)(uintptr_t)scalars)->skip) return;  // the skip decision is global
+  const int64_t stride = gridDim.x;  // in a register: the loop's asm barrier would reload it
   int64_t c = blockIdx.x;  // < nchunks: the grid is at most the chunk count
   DsxChunk ch = chunk_rec(chunks, c);
   for (;;) {
@@ -1290,7 +1303,7 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_multi(const DsxTensorRef* __r
     first_trip<GD, U, NT>(cv, tensors, T);
     const Sc sc = scalars_rec(scalars, tr.group);
     asm volatile("" ::"s"(sc.nss) : "memory");  // the scalars are in before the next record is asked for
-    const int64_t cn = c + gridDim.x;
+    const int64_t cn = c + stride;
     const DsxChunk chn = chunk_rec(chunks, cn < nchunks ? cn : c);
     chunk_steps<GD, PD, U, NT, DRAIN>(cv, T, sc);
     if (cn >= nchunks) break;
