@@ -157,7 +157,13 @@ typedef struct DsxTensorRef {
   int32_t     reserved;
 } DsxTensorRef;
 
-/* One chunk of a ragged list: elements [start, start+len) of tensor `tensor`. */
+/* One chunk of a ragged list: elements [start, start+len) of tensor `tensor`.
+ * The kernels take both tables as given (they live in device memory, out of
+ * the host's sight): each chunk needs 0 <= tensor < the tensor count,
+ * start >= 0, len >= 0 and start + len <= that tensor's numel, and each
+ * tensor's arrays numel elements; dsx_build_chunks writes such tables. The
+ * tables are read through the scalar (constant) cache, so they must not
+ * change while a launch that reads them runs. */
 typedef struct DsxChunk {
   int32_t tensor;
   int32_t reserved;
