@@ -1203,11 +1203,14 @@ struct Trip {
 
 // Issue a chunk's first trip of slot loads. Every thread issues the same
 // loads whatever the chunk: indices clamped into the chunk, and for a chunk
-// off the slot path loads from `spare` (a readable 16-byte-aligned address
-// whose values go unused), so that the waits for them stay exact.
+// off the slot path loads from `spare` rounded down to 16 bytes (the tensor
+// table: device allocations start on 256-byte boundaries, so that stays in
+// the table's allocation; the values go unused), so that the waits for them
+// stay exact.
 template <int GD, int U, bool NT>
-__device__ __forceinline__ void first_trip(const ChunkView<GD>& c, const void* spare, Trip<GD, U>& T) {
+__device__ __forceinline__ void first_trip(const ChunkView<GD>& c, const void* spare_any, Trip<GD, U>& T) {
   using GS = typename Grad<GD>::slot4;
+  const void* spare = reinterpret_cast<const void*>(reinterpret_cast<uintptr_t>(spare_any) & ~uintptr_t(15));
   const f4* lp = c.vec ? reinterpret_cast<const f4*>(c.p) : static_cast<const f4*>(spare);
   const f4* lm = c.vec ? reinterpret_cast<const f4*>(c.m) : static_cast<const f4*>(spare);
   const f4* lv = c.vec ? reinterpret_cast<const f4*>(c.v) : static_cast<const f4*>(spare);
