@@ -38,10 +38,21 @@ def auto_chunk_elems(numel: int) -> int:
     """Chunk size for a list of `numel` elements: 65536 for large lists; for
     smaller ones a power of two down to 4096, so that the list still splits
     into about 4096 chunks (the kernels hand chunks to blocks statically, and
-    a GPU of 256 CUs needs several rounds of them to balance)."""
+    a GPU of 256 CUs needs several rounds of them to balance). A list that
+    fits in at most 1024 chunks of 2048 elements (2.1e6 elements) takes 2048:
+    one trip of K3's slot loop per chunk (256 threads x 2 slots x 4
+    elements), so that in K3's one-chunk-per-block shape, and in the
+    two-launch step with K0 folded into K3, all of a chunk's loads are in
+    flight at once. Eager drop-in steps on MI355X, one process: configs[0]'s
+    MLP list (1.86e6 elements) 17.1-17.6 us per step in 4096-element chunks,
+    14.9-15.2 in 2048 (1024: 19.8-20.0; 8192: 18.8-19.2); larger lists lose
+    with 2048 (K1 walks twice the chunks): 3.9e6 elements 27.2 against 26.0
+    us, 6.3e6 39.8 against 38.3."""
     c = 65536
     while c > 4096 and numel // c < 4096:
         c //= 2
+    if c == 4096 and -(-numel // 2048) <= 1024:
+        c = 2048
     return c
 
 

@@ -317,10 +317,13 @@ def test_ragged_store_fp32_master_is_the_param():
 def test_ragged_chunk_size_fills_the_gpu():
     from distributedspeed_amd.ragged import auto_chunk_elems
     assert auto_chunk_elems(8_310_226_944) == 65536 and auto_chunk_elems(124_439_808) == 16384
-    assert auto_chunk_elems(1_863_690) == 4096 and auto_chunk_elems(10) == 4096
-    for n in (1 << 20, 1 << 27, 3 << 28):
+    # small lists: one trip of K3's slot loop per chunk while the list fits in 1024 chunks of 2048
+    assert auto_chunk_elems(1_863_690) == 2048 and auto_chunk_elems(10) == 2048
+    assert auto_chunk_elems(1024 * 2048) == 2048 and auto_chunk_elems(1024 * 2048 + 1) == 4096
+    assert auto_chunk_elems(3_900_000) == 4096
+    for n in (1 << 20, 1 << 22, 1 << 27, 3 << 28):
         c = auto_chunk_elems(n)
-        assert c % 8 == 0 and (c == 4096 or n // c >= 4096)
+        assert c % 8 == 0 and (c == 4096 or n // c >= 4096 or (c == 2048 and -(-n // c) <= 1024))
 
 
 def test_optimizer_step_hooks_still_run():
