@@ -1107,16 +1107,22 @@ __device__ __forceinline__ Sc scalars_rec(const DsxStepScalars* scalars, int32_t
 
 // K1 over a chunk table. Block b reduces chunks b, b + grid, ... in order,
 // each as K1's slot loop (four 16-byte loads per thread in flight before any
-// use) when its grad is 16-byte aligned, element by element otherwise. The
-// next chunk's record is requested with the current chunk's tensor record, so
-// that it is in by the time the current chunk is done.
-template <int GD>
+// use) when its grad is 16-byte aligned, element by element otherwise. With
+// WAVE, each wave takes its own chunks (wave w of block b: chunks 4b + w,
+// 4b + w + 4 grid, ...): for tables of small chunks, where a block's 256
+// threads would leave most of a trip empty (a 2048-element 16-bit chunk is
+// one trip of one wave). The next chunk's record is requested with the
+// current chunk's tensor record, so that it is in by the time the current
+// chunk is done.
+template <int GD, bool WAVE>
 __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorRef* __restrict__ tensors,
                                                                 const DsxChunk* __restrict__ chunks,
                                                                 int64_t nchunks, const DsxState* state,
                                                                 double* __restrict__ partials, DsxState* fold) {
   using G = Grad<GD>;
   constexpr int U = 4;
+  constexpr int kWaves = kBlock / 64;
+  constexpr int kLanes = WAVE ? 64 : kBlock;
   const float inv = inv_of(state->scale);
   if (fold != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {  // as k1_unscale_norm
     const int32_t armed = fold->clip_once != 0 ? 1 : 0;
@@ -1125,8 +1131,10 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorR
     fold->clip_once = 0;
   }
   double acc = 0.0;
-  const int64_t stride = gridDim.x;
-  int64_t c = blockIdx.x;
+  const int lane = WAVE ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
+  const int64_t stride = WAVE ? (int64_t)gridDim.x * kWaves : (int64_t)gridDim.x;
+  int64_t c = WAVE ? (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)
+                   : (int64_t)blockIdx.x;
   if (c < nchunks) {  // the grid is the partial count, which may exceed the chunk count
     DsxChunk ch = chunk_rec(chunks, c);
     for (;;) {
@@ -1137,11 +1145,11 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorR
       if (aligned16(g)) {
         const u4* g16 = reinterpret_cast<const u4*>(g);
         const int64_t nvec = ch.len / G::per16;
-        for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += kBlock * U) {
+        for (int64_t i0 = lane; i0 < nvec; i0 += kLanes * U) {
           u4 S[U];
 #pragma unroll
           for (int u = 0; u < U; ++u) {
-            const int64_t i = i0 + (int64_t)u * kBlock;
+            const int64_t i = i0 + (int64_t)u * kLanes;
             S[u] = (i < nvec) ? ld<true>(g16 + i) : u4{0u, 0u, 0u, 0u};
           }
 #pragma unroll
@@ -1149,7 +1157,7 @@ __global__ __launch_bounds__(kBlock) void k1_unscale_norm_multi(const DsxTensorR
         }
         done = nvec * G::per16;
       }
-      for (int64_t e = done + threadIdx.x; e < ch.len; e += kBlock) {
+      for (int64_t e = done + lane; e < ch.len; e += kLanes) {
         const float a = G::one(g[e]) * inv;
         acc = __builtin_fma((double)a, (double)a, acc);
       }
@@ -1778,22 +1786,26 @@ int noalloc_scratch(hipStream_t s, unsigned char** out) {
   return DSX_OK;
 }
 
+template <int GD>
+void launch_k1_multi(bool wave, dim3 grid, const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks,
+                     const DsxState* state, double* partials, DsxState* fold, hipStream_t s) {
+  if (wave)
+    hipLaunchKernelGGL((k1_unscale_norm_multi<GD, true>), grid, dim3(kBlock), 0, s, tensors, chunks, nchunks,
+                       state, partials, fold);
+  else
+    hipLaunchKernelGGL((k1_unscale_norm_multi<GD, false>), grid, dim3(kBlock), 0, s, tensors, chunks, nchunks,
+                       state, partials, fold);
+}
+
+// K1 over a chunk table; wave: one wave per chunk (tables of small chunks).
 int do_unscale_norm_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int gdt,
-                          const DsxState* state, double* partials, int32_t nparts, hipStream_t s, DsxState* fold) {
-  const dim3 grid(nparts), blk(kBlock);
+                          const DsxState* state, double* partials, int32_t nparts, hipStream_t s, DsxState* fold,
+                          bool wave = false) {
+  const dim3 grid(nparts);
   switch (gdt) {
-    case DSX_BF16:
-      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_BF16>), grid, blk, 0, s, tensors, chunks, nchunks, state,
-                         partials, fold);
-      break;
-    case DSX_F16:
-      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_F16>), grid, blk, 0, s, tensors, chunks, nchunks, state,
-                         partials, fold);
-      break;
-    default:
-      hipLaunchKernelGGL((k1_unscale_norm_multi<DSX_F32>), grid, blk, 0, s, tensors, chunks, nchunks, state,
-                         partials, fold);
-      break;
+    case DSX_BF16: launch_k1_multi<DSX_BF16>(wave, grid, tensors, chunks, nchunks, state, partials, fold, s); break;
+    case DSX_F16: launch_k1_multi<DSX_F16>(wave, grid, tensors, chunks, nchunks, state, partials, fold, s); break;
+    default: launch_k1_multi<DSX_F32>(wave, grid, tensors, chunks, nchunks, state, partials, fold, s); break;
   }
   return launch_status("dsx_unscale_norm_multi");
 }
@@ -2345,8 +2357,10 @@ int dsx_zero_step_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int
   // Two launches where the fold applies and the list takes K3's one-chunk-
   // per-block shape; else K1, K0, K3.
   const bool fold = nchunks > 0 && fold_applies(numel, nparts) && nchunks <= kK3OneChunkPerCu * cu_count();
+  // K1 one wave per chunk when the chunks average at most 4096 elements.
+  const bool wave = nchunks > 0 && numel <= 4096 * nchunks;
   rc = do_unscale_norm_multi(tensors, chunks, nchunks, grad_dtype, state, partials, nparts, s,
-                             fold ? state : nullptr);
+                             fold ? state : nullptr, wave);
   if (rc) return rc;
   if (!fold) {
     rc = do_finalize(partials, nparts, state, scaler, G, out, s);
