@@ -1797,11 +1797,21 @@ void launch_k1_multi(bool wave, dim3 grid, const DsxTensorRef* tensors, const Ds
                        state, partials, fold);
 }
 
-// K1 over a chunk table; wave: one wave per chunk (tables of small chunks).
+// K1 over a chunk table. Each wave takes its own chunks when the table has
+// at most 16 chunks per block (kK1WaveChunksPerPart), one block per chunk
+// otherwise: decided from the chunk and partial counts alone, so that every
+// entry point over the same table and partials takes the same shape and sums
+// in the same order. The tables the library builds have chunks of 2048 to
+// 16384 elements up to that count, 65536 beyond it; per launch on MI355X
+// (one process, alternated): 4096-element chunks over 2.1e7 elements 12.7 ->
+// 9.3 us and over 8.6e7 49.7 -> 28.7 us, 16384-element chunks over 1.2e8
+// 39.1 -> 39.5 us, 65536-element chunks over 2.9e9 and 8.3e9 elements 2-4%
+// slower one wave per chunk.
+constexpr int64_t kK1WaveChunksPerPart = 16;
 int do_unscale_norm_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t nchunks, int gdt,
-                          const DsxState* state, double* partials, int32_t nparts, hipStream_t s, DsxState* fold,
-                          bool wave = false) {
+                          const DsxState* state, double* partials, int32_t nparts, hipStream_t s, DsxState* fold) {
   const dim3 grid(nparts);
+  const bool wave = nchunks <= kK1WaveChunksPerPart * nparts;
   switch (gdt) {
     case DSX_BF16: launch_k1_multi<DSX_BF16>(wave, grid, tensors, chunks, nchunks, state, partials, fold, s); break;
     case DSX_F16: launch_k1_multi<DSX_F16>(wave, grid, tensors, chunks, nchunks, state, partials, fold, s); break;
@@ -2357,10 +2367,8 @@ int dsx_zero_step_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int
   // Two launches where the fold applies and the list takes K3's one-chunk-
   // per-block shape; else K1, K0, K3.
   const bool fold = nchunks > 0 && fold_applies(numel, nparts) && nchunks <= kK3OneChunkPerCu * cu_count();
-  // K1 one wave per chunk when the chunks average at most 4096 elements.
-  const bool wave = nchunks > 0 && numel <= 4096 * nchunks;
   rc = do_unscale_norm_multi(tensors, chunks, nchunks, grad_dtype, state, partials, nparts, s,
-                             fold ? state : nullptr, wave);
+                             fold ? state : nullptr);
   if (rc) return rc;
   if (!fold) {
     rc = do_finalize(partials, nparts, state, scaler, G, out, s);
