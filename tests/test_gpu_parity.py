@@ -629,3 +629,40 @@ def test_k3_several_chunks_per_block_give_identical_bits(gpu, oracle):
             assert not torch16_to_np(tp16)[~covered].any()  # nothing written between the tensors
     finally:
         _lib.call("dsx_set_tuning_multi", 0, 1, 1, -1)
+
+
+@pytest.mark.parametrize("gdt", [F16, BF16, 0], ids=["fp16", "bf16", "fp32"])
+def test_k1_multi_both_shapes_match_oracle(gpu, oracle, gdt):
+    """K1 over a chunk table in both of its shapes -- one wave per chunk (at
+    most 16 chunks per partial block) and one block per chunk (more) -- over
+    the same ragged list (tensors off the 16-byte grid, ragged tails, tiny
+    tensors): each within 1e-12 of the oracle's fp64 sum. The shape follows
+    from the chunk and partial counts alone, which the one-call step shares."""
+    import torch
+    from distributedspeed_amd import ops
+    O = oracle
+    rng = np.random.default_rng(41)
+    sizes = [int(x) for x in rng.integers(1, 9000, size=60)] + [2048, 4096, 3, 20000]
+    offs, pos = [], 0
+    for i, s in enumerate(sizes):
+        pos += i % 3
+        offs.append(pos)
+        pos += s
+    total = pos
+    scale = 2.0 ** 10 if gdt == F16 else 1.0
+    g32 = (rng.standard_normal(total) * 1e-3 * scale).astype(np.float32)
+    g = g32 if gdt == 0 else O.cast16(g32, gdt)
+    tdt = {F16: torch.float16, BF16: torch.bfloat16, 0: torch.float32}[gdt]
+    tg = (torch.from_numpy(g.view(np.int16)).view(tdt) if gdt else torch.from_numpy(g)).to(gpu)
+    f32 = torch.zeros(total, device=gpu)
+    views = lambda t: [t[o:o + s] for o, s in zip(offs, sizes)]  # noqa: E731
+    table = ops.ChunkTable(views(f32), views(f32), views(f32), None, views(tg), chunk_elems=2048)
+    ref = sum(O.sumsq(np.ascontiguousarray(g[o:o + s]), gdt if gdt else 0, O.inv_scale_of(scale))
+              for o, s in zip(offs, sizes))
+    st = ops.new_state(gpu, scale, 1)
+    for nparts in (4, (table.nchunks + 15) // 16, 256):  # block, wave (the bound), wave
+        parts = torch.zeros(nparts, dtype=torch.float64, device=gpu)
+        ops.unscale_norm_multi(table, st, parts, nparts)
+        torch.cuda.synchronize()
+        got = float(parts.sum().item())
+        assert got == pytest.approx(ref, rel=1e-12), (nparts, table.nchunks, got, ref)
