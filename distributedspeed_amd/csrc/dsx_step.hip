@@ -281,9 +281,39 @@ __device__ __forceinline__ u2 pack4(const f4& p) {
 
 // ---- block reduction of a double -------------------------------------------
 
+// One DPP lane exchange of a double (two 32-bit moves; every source lane of
+// the patterns used lies in the same row, so every lane is written).
+template <int kCtrl>
+__device__ __forceinline__ double dpp_pair(double x) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, kCtrl, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), kCtrl, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Lane i's partner i ^ 16 within each 32 lanes, through ds_swizzle (bitmask
+// mode: and 0x1f, or 0, xor 0x10).
+__device__ __forceinline__ double swizzle_xor16(double x) {
+  constexpr int kXor16 = 0x1f | (0x10 << 10);
+  const uint64_t u = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)u, kXor16);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)(u >> 32), kXor16);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Sum over the wave, in every lane. Within each row of 16 lanes through DPP:
+// quad_perm for partners i ^ 1 and i ^ 2, then row_half_mirror (7 - i within
+// 8) and row_mirror (15 - i within 16) in place of i ^ 4 and i ^ 8 -- by then
+// every lane of a quad, then of an 8-lane half, holds the same sum (a + b ==
+// b + a bit for bit), so the mirror partner holds what the xor partner would.
+// Across rows: ds_swizzle for i ^ 16, ds_bpermute for i ^ 32.
 __device__ __forceinline__ double wave_sum(double x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  x += dpp_pair<0xb1>(x);   // quad_perm [1, 0, 3, 2]
+  x += dpp_pair<0x4e>(x);   // quad_perm [2, 3, 0, 1]
+  x += dpp_pair<0x141>(x);  // row_half_mirror
+  x += dpp_pair<0x140>(x);  // row_mirror
+  x += swizzle_xor16(x);
+  x += __shfl_xor(x, 32, 64);
   return x;
 }
 
