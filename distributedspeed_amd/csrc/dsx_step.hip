@@ -301,20 +301,26 @@ __device__ __forceinline__ double swizzle_xor16(double x) {
   return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
-// Sum over the wave, in every lane. Within each row of 16 lanes through DPP:
+// Reduce over the wave with comb (commutative: comb(a, b) == comb(b, a)),
+// the result in every lane. Within each row of 16 lanes through DPP:
 // quad_perm for partners i ^ 1 and i ^ 2, then row_half_mirror (7 - i within
 // 8) and row_mirror (15 - i within 16) in place of i ^ 4 and i ^ 8 -- by then
-// every lane of a quad, then of an 8-lane half, holds the same sum (a + b ==
-// b + a bit for bit), so the mirror partner holds what the xor partner would.
-// Across rows: ds_swizzle for i ^ 16, ds_bpermute for i ^ 32.
-__device__ __forceinline__ double wave_sum(double x) {
-  x += dpp_pair<0xb1>(x);   // quad_perm [1, 0, 3, 2]
-  x += dpp_pair<0x4e>(x);   // quad_perm [2, 3, 0, 1]
-  x += dpp_pair<0x141>(x);  // row_half_mirror
-  x += dpp_pair<0x140>(x);  // row_mirror
-  x += swizzle_xor16(x);
-  x += __shfl_xor(x, 32, 64);
+// every lane of a quad, then of an 8-lane half, holds the same value, so the
+// mirror partner holds what the xor partner would. Across rows: ds_swizzle
+// for i ^ 16, ds_bpermute for i ^ 32.
+template <class Comb>
+__device__ __forceinline__ double wave_reduce(double x, Comb comb) {
+  x = comb(x, dpp_pair<0xb1>(x));   // quad_perm [1, 0, 3, 2]
+  x = comb(x, dpp_pair<0x4e>(x));   // quad_perm [2, 3, 0, 1]
+  x = comb(x, dpp_pair<0x141>(x));  // row_half_mirror
+  x = comb(x, dpp_pair<0x140>(x));  // row_mirror
+  x = comb(x, swizzle_xor16(x));
+  x = comb(x, __shfl_xor(x, 32, 64));
   return x;
+}
+
+__device__ __forceinline__ double wave_sum(double x) {
+  return wave_reduce(x, [](double a, double b) { return a + b; });
 }
 
 // Sum over the block; the result is valid in thread 0.
@@ -339,6 +345,7 @@ __device__ __forceinline__ double block_sum(double x) {
 // x is the unscaled fp32 grad; every accumulation is in fp64.
 enum NormKind { kNormSq = 0, kNormAbs = 1, kNormMax = 2, kNormPow = 3 };
 
+// Commutative on what it combines (sums, or maxima of magnitudes: no -0).
 template <int K>
 __device__ __forceinline__ double norm_comb(double a, double b) {
   if constexpr (K == kNormMax) return (b > a || b != b) ? b : a;  // a NaN stays (b > NaN is false)
@@ -372,8 +379,7 @@ __device__ __forceinline__ double norm_acc16(const u4& s, float inv, double p, d
 template <int K>
 __device__ __forceinline__ double block_reduce(double x) {
   __shared__ double lds[kWaves];
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x = norm_comb<K>(x, __shfl_xor(x, off, 64));
+  x = wave_reduce(x, [](double a, double b) { return norm_comb<K>(a, b); });
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) lds[wave] = x;
   __syncthreads();
