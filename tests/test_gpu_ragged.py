@@ -258,3 +258,74 @@ def test_bound_launches_keep_their_buffers_alive(gpu):
     assert wp() is not None
     del k2
 
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_ragged_random_lists_match_flat(gpu, seed):
+    """Random lists through the ragged form's one-call step against the flat
+    form, bit for bit, five steps each. Lists of 2e4-2e6 elements (2048-element
+    chunks, K3 one chunk per block), 3e6-8e6 (4096-element chunks) and
+    2.2e7-3e7 (over 20 chunks per CU: K1, K0 and K3 as one block per CU
+    walking the list), split at random over 2 to 60 tensors, or 150 to 300
+    tensors of at most 60 elements; a third of the tensors one element off
+    the 16-byte grid, two groups with their own lr and betas, clipping, fp16
+    with a dynamic scale and an inf at step 2 or bf16; odd seeds with the fold
+    switched off (K1, K0, K3)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+    from distributedspeed_amd import _lib
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
+    rng = np.random.default_rng(100 + seed)
+    if seed == 3:  # many tiny tensors
+        nt = int(rng.integers(150, 301))
+        sizes = [int(x) for x in rng.integers(1, 61, size=nt)]
+    else:
+        lo, hi = ((2e4, 2e6), (3e6, 8e6), (2.2e7, 3e7))[seed % 3]
+        total = int(rng.uniform(lo, hi))
+        nt = int(rng.integers(2, 61))
+        w = rng.dirichlet(np.ones(nt))
+        sizes = [max(1, int(x)) for x in w * total]
+    shapes = [(s,) if rng.random() < 0.5 or s < 4 else (s // 3, 3) if s >= 3 else (s,) for s in sizes]
+    dt = torch.float16 if seed % 2 == 0 else torch.bfloat16
+    fp16 = dt == torch.float16
+    sc = (ScalerConfig(mode="dynamic", init_scale=2.0 ** 10, window=2, hysteresis=1) if fp16
+          else ScalerConfig(mode="none"))
+    gen = torch.Generator().manual_seed(seed)
+    init = [torch.randn(s, generator=gen) * 0.05 for s in shapes]
+
+    def build(cls):
+        ps = []
+        for k, t in enumerate(init):
+            if k % 3 == 1:  # one element past a 16-byte boundary
+                buf = torch.empty(t.numel() + 1, dtype=dt, device=gpu)
+                v = buf[1:].view(t.shape)
+                v.copy_(t)
+                ps.append(torch.nn.Parameter(v))
+            else:
+                ps.append(torch.nn.Parameter(t.to(gpu, dt)))
+        cut = max(1, len(ps) // 3)
+        groups = [{"params": ps[:cut]}, {"params": ps[cut:], "lr": 3e-4, "betas": (0.8, 0.95)}]
+        return cls(groups, lr=1e-3, weight_decay=0.05, max_grad_norm=0.3, param_dtype=dt, device=gpu,
+                   loss_scaler=sc)
+
+    flat, rag = build(AdamWOptimizer), build(MultiTensorAdamWOptimizer)
+    _say(f"random list seed {seed}: {nt} tensors, {sum(sizes)} elements, {dt}, "
+         f"chunks of {rag.store.chunk_elems}, fold {'off' if seed % 2 else 'on'}")
+    ggen = torch.Generator(device=gpu).manual_seed(seed)
+    fold_default = 1 << 24
+    try:
+        if seed % 2:
+            _lib.call("dsx_set_tuning_fold", ctypes.c_int64(0))
+        for step in range(5):
+            scale = float(flat.read_state().scale) if fp16 else 1.0
+            _set_grads(flat, rag, ggen, scale, dt, inf_at=(nt // 2 if fp16 and step == 2 else None))
+            flat.step()
+            rag.step()
+            _check(flat, rag, f"seed {seed} step {step}")
+    finally:
+        _lib.call("dsx_set_tuning_fold", ctypes.c_int64(fold_default))
+    st = rag.read_state()
+    assert st.t == (4 if fp16 else 5) and st.error == 0
