@@ -61,7 +61,7 @@ def _args():
                     help="K2 part size in elements (dsx_set_tuning_k2_chunk; 0: one launch; default: the library's 2^26)")
     ap.add_argument("--fold", type=int, default=None,
                     help="largest partition whose one-call step runs as two launches, K0 folded into K2 "
-                         "(dsx_set_tuning_fold; 0: always three launches; default: the library's 2^24)")
+                         "(dsx_set_tuning_fold; 0: always three launches; default: the library's 3*2^23)")
     ap.add_argument("--tuning-multi", default="",
                     help="k3_bpc,k3_unroll,nt,drain (K3 launch-shape override; k3_bpc 0 picks by chunk count)")
     ap.add_argument("--workload", default="llama8b-shard",

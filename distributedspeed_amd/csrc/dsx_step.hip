@@ -124,9 +124,13 @@ struct Tuning {
   int64_t k2_chunk_elems = int64_t(1) << 26;
   // Steps over at most this many elements (with at most kFoldMaxParts
   // partials) run as two launches, K1 and K2 with the finalize folded in
-  // (k2_adamw_fold), instead of K1, K0, K2; 0: always three launches. 2^24
-  // elements is the end of K2's one-trip grid on 256 CUs.
-  int64_t fold_max_elems = int64_t(1) << 24;
+  // (k2_adamw_fold), instead of K1, K0, K2; 0: always three launches.
+  // 3 * 2^23: K2's one-trip grid on 256 CUs covers 2^24 elements, and up to
+  // one and a half sweeps of it the fold still wins (eager flat step on
+  // MI355X: 20 Mi elements 108.0 against 113.4 us, 24 Mi 130.7 against
+  // 133.9; 32 Mi even, 48 Mi 267.9 against 256.2: every block also reduces
+  // the partials).
+  int64_t fold_max_elems = int64_t(3) << 23;
 };
 Tuning g_tune;
 
@@ -1057,6 +1061,12 @@ __global__ __launch_bounds__(kBlock) void k2_adamw_fold(float* __restrict__ p, f
   if (!d.skip && group < d.ng) {
     const Sc sc = uniform_sc(load_sc(record_bc(d, s, grp, group, sumsq, bc1, bc2s)));
     for (;;) {
+      // Every slot's loads are taken in here, on every path, as in K3's
+      // chunk loop: a slot past the end would otherwise leave its loads
+      // pending into the next trip, whose register writes would then wait for
+      // this trip's stores too.
+#pragma unroll
+      for (int u = 0; u < U; ++u) asm volatile("" : "+v"(Gs[u]), "+v"(P[u]), "+v"(M[u]), "+v"(V[u]));
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t i = i0 + (int64_t)u * kBlock;

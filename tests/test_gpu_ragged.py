@@ -315,7 +315,7 @@ def test_ragged_random_lists_match_flat(gpu, seed):
     _say(f"random list seed {seed}: {nt} tensors, {sum(sizes)} elements, {dt}, "
          f"chunks of {rag.store.chunk_elems}, fold {'off' if seed % 2 else 'on'}")
     ggen = torch.Generator(device=gpu).manual_seed(seed)
-    fold_default = 1 << 24
+    fold_default = 3 << 23  # the library's default bound
     try:
         if seed % 2:
             _lib.call("dsx_set_tuning_fold", ctypes.c_int64(0))
