@@ -1654,10 +1654,10 @@ void launch_k2_fold_nt(dim3 grid, float* p, float* m, float* v, uint16_t* o, con
 template <int GD, int PD>
 void launch_k2_fold(float* p, float* m, float* v, void* p16, const void* g, int64_t n, const double* partials,
                     int32_t nparts, DsxState* state, const DsxScalerConfig& scfg, const FoldGroups& fg,
-                    int group, bool writer, DsxStepScalars* out, hipStream_t s) {
+                    int group, bool writer, DsxStepScalars* out, hipStream_t s, int64_t blocks_per_cu) {
   const int64_t slots = n >> 2;
   int64_t blocks = ceil_div(slots > 0 ? slots : 1, (int64_t)kBlock * 2);
-  const int64_t cap = (int64_t)cu_count() * kK2OneTripPerCu;
+  const int64_t cap = (int64_t)cu_count() * blocks_per_cu;
   if (blocks > cap) blocks = cap;
   if (writer) blocks += 1;  // the block that writes the records and the state
   uint16_t* o = static_cast<uint16_t*>(p16);
@@ -1672,30 +1672,51 @@ void launch_k2_fold(float* p, float* m, float* v, void* p16, const void* g, int6
 template <int GD>
 void k2_fold_by_param(int pd, float* p, float* m, float* v, void* p16, const void* g, int64_t n,
                       const double* partials, int32_t nparts, DsxState* state, const DsxScalerConfig& scfg,
-                      const FoldGroups& fg, int group, bool writer, DsxStepScalars* out, hipStream_t s) {
+                      const FoldGroups& fg, int group, bool writer, DsxStepScalars* out, hipStream_t s,
+                      int64_t bpc) {
   if (pd == DSX_BF16)
-    launch_k2_fold<GD, DSX_BF16>(p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s);
+    launch_k2_fold<GD, DSX_BF16>(p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s, bpc);
   else
-    launch_k2_fold<GD, DSX_F16>(p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s);
+    launch_k2_fold<GD, DSX_F16>(p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s, bpc);
 }
 
 bool fold_applies(int64_t n, int32_t nparts) {
   return g_tune.fold_max_elems > 0 && n >= 4 && n <= g_tune.fold_max_elems && nparts <= kFoldMaxParts;
 }
 
+// Above the fold's bound, K0 is folded into the first of K2's parts alone,
+// launched one block per CU (so that few blocks pay the partials' reduction),
+// and the other parts read the records that launch's writer block wrote.
+bool fold_first_applies(int64_t n, int32_t nparts) {
+  return g_tune.fold_max_elems > 0 && n > g_tune.fold_max_elems && nparts <= kFoldMaxParts;
+}
+
+// The length of K2's first part over n elements (k2_dispatch's split).
+int64_t k2_first_part(int64_t n) {
+  const int64_t want = g_tune.k2_chunk_elems;
+  if (want <= 0 || n <= want) return n;
+  return ceil_div(ceil_div(n, ceil_div(n, want)), 1024) * 1024;
+}
+
+// The folded K2 over n elements: K2's one-trip grid (at most
+// kK2OneTripPerCu blocks per CU), or at most bpc blocks per CU.
 int do_adamw_fold(float* p, float* m, float* v, void* p16, int pdt, const void* g, int gdt, int64_t n,
                   const double* partials, int32_t nparts, DsxState* state, const DsxScalerConfig& scfg,
-                  const FoldGroups& fg, int group, bool writer, DsxStepScalars* out, hipStream_t s) {
+                  const FoldGroups& fg, int group, bool writer, DsxStepScalars* out, hipStream_t s,
+                  int64_t bpc = kK2OneTripPerCu) {
   const int pd = p16 ? pdt : DSX_F16;
   switch (gdt) {
     case DSX_BF16:
-      k2_fold_by_param<DSX_BF16>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s);
+      k2_fold_by_param<DSX_BF16>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s,
+                                 bpc);
       break;
     case DSX_F16:
-      k2_fold_by_param<DSX_F16>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s);
+      k2_fold_by_param<DSX_F16>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s,
+                                bpc);
       break;
     default:
-      k2_fold_by_param<DSX_F32>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s);
+      k2_fold_by_param<DSX_F32>(pd, p, m, v, p16, g, n, partials, nparts, state, scfg, fg, group, writer, out, s,
+                                bpc);
       break;
   }
   return launch_status("dsx_adamw_flat (finalize folded in)");
@@ -1794,6 +1815,18 @@ int zero_step_flat(float* master, float* m, float* v, void* p16, int pdt, const 
     int rc = do_unscale_norm(g, gdt, n, state, partials, nparts, s, state);
     if (!rc) rc = do_adamw_fold(master, m, v, p16, pdt, g, gdt, n, partials, nparts, state, scaler,
                                 FoldGroups{&grp, nullptr, 1}, 0, true, out, s);
+    return rc;
+  }
+  if (fold_first_applies(n, nparts)) {
+    const int64_t a = k2_first_part(n);
+    int rc = do_unscale_norm(g, gdt, n, state, partials, nparts, s, state);
+    if (!rc) rc = do_adamw_fold(master, m, v, p16, pdt, g, gdt, a, partials, nparts, state, scaler,
+                                FoldGroups{&grp, nullptr, 1}, 0, true, out, s, 1);
+    if (!rc && a < n) {
+      void* p16a = p16 ? static_cast<void*>(static_cast<uint16_t*>(p16) + a) : nullptr;
+      const void* ga = static_cast<const char*>(g) + a * (gdt == DSX_F32 ? 4 : 2);
+      rc = do_adamw_flat(master + a, m + a, v + a, p16a, pdt, ga, gdt, n - a, out, s);
+    }
     return rc;
   }
   int rc = do_unscale_norm(g, gdt, n, state, partials, nparts, s);
@@ -1957,14 +1990,16 @@ int check_plan(const DsxFlatPlan& P) {
 // the device address Gdev (read by the kernels: the graph form).
 int plan_launches(const DsxFlatPlan& P, const DsxGroupsDev* G, const DsxGroupsDev* Gdev, hipStream_t s) {
   bool fold = fold_applies(P.n, P.nparts);
+  bool first = !fold && fold_first_applies(P.n, P.nparts);  // fold K0 into the first part alone
   int64_t prev = 0;
-  for (int k = 0; fold && k < P.ngroups; ++k) {
+  for (int k = 0; (fold || first) && k < P.ngroups; ++k) {
     const int64_t len = P.group_end[k] - prev;
     prev = P.group_end[k];
-    if (len > 0 && len < 4) fold = false;  // the folded K2 takes at least one 4-element slot
+    if (len > 0 && len < 4) fold = first = false;  // the folded K2 takes at least one 4-element slot
   }
-  int rc = do_unscale_norm(P.grad, P.grad_dtype, P.n, P.state, P.partials, P.nparts, s, fold ? P.state : nullptr);
-  if (!rc && !fold) {
+  int rc = do_unscale_norm(P.grad, P.grad_dtype, P.n, P.state, P.partials, P.nparts, s,
+                           fold || first ? P.state : nullptr);
+  if (!rc && !fold && !first) {
     if (G) {
       rc = do_finalize(P.partials, P.nparts, P.state, P.scaler, *G, P.out, s);
     } else {
@@ -1983,12 +2018,24 @@ int plan_launches(const DsxFlatPlan& P, const DsxGroupsDev* G, const DsxGroupsDe
     if (b == a) continue;
     void* p16 = P.param16 ? static_cast<void*>(static_cast<uint16_t*>(P.param16) + a) : nullptr;
     const void* ga = static_cast<const char*>(P.grad) + a * gsz;
-    if (fold)
+    if (fold) {
       rc = do_adamw_fold(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype, ga, P.grad_dtype, b - a,
                          P.partials, P.nparts, P.state, P.scaler, fg, k, writer, P.out, s);
-    else
+    } else if (first && writer) {
+      // The step's first part decides and writes the records; the rest of
+      // this group and the other groups read them.
+      const int64_t c = k2_first_part(b - a);
+      rc = do_adamw_fold(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype, ga, P.grad_dtype, c,
+                         P.partials, P.nparts, P.state, P.scaler, fg, k, true, P.out, s, 1);
+      if (!rc && c < b - a) {
+        void* p16c = p16 ? static_cast<void*>(static_cast<uint16_t*>(p16) + c) : nullptr;
+        rc = do_adamw_flat(P.master + a + c, P.exp_avg + a + c, P.exp_avg_sq + a + c, p16c, P.param_dtype,
+                           static_cast<const char*>(ga) + c * gsz, P.grad_dtype, b - a - c, P.out + k, s);
+      }
+    } else {
       rc = do_adamw_flat(P.master + a, P.exp_avg + a, P.exp_avg_sq + a, p16, P.param_dtype, ga, P.grad_dtype, b - a,
                          P.out + k, s);
+    }
     writer = false;
   }
   return rc;

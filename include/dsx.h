@@ -212,9 +212,11 @@ int dsx_set_tuning_k2_chunk(int64_t chunk_elems);
  * K0's code and order, so the bits are K0's; one extra block writes the
  * state and the step records). The folded K2 takes K2's one-trip grid (2
  * slots per thread, at most 32 blocks per CU) whatever dsx_set_tuning and
- * dsx_set_tuning_k2 set. 0 always runs K1, K0, K2. Default 3 * 2^23 (one and
- * a half sweeps of K2's one-trip grid on 256 CUs). No counterpart in the
- * reference. */
+ * dsx_set_tuning_k2 set. Above max_elems (same limits), K0's finalize is
+ * folded into the first of K2's parts alone, launched one block per CU, and
+ * the other parts read the records it writes. 0 always runs K1, K0, K2.
+ * Default 3 * 2^23 (one and a half sweeps of K2's one-trip grid on 256 CUs).
+ * No counterpart in the reference. */
 int dsx_set_tuning_fold(int64_t max_elems);
 
 /* The same for K3 (dsx_adamw_multi): blocks per CU (the grid is also capped

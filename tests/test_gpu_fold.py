@@ -39,6 +39,10 @@ CASES = [
     ("parts-513", 300_001, F16, F16, "dynamic", 513, FOLD_DEFAULT),
     ("strided", 40_000_003, BF16, BF16, "none", None, 1 << 26),
     ("f32-grads", 123_457, F32, BF16, "none", None, FOLD_DEFAULT),
+    # above the bound: K0 folded into K2's first part alone (one block per CU),
+    # here the whole partition (one part) and the first of two parts
+    ("first-part-whole", 3_000_007, F16, F16, "dynamic", None, 1 << 20),
+    ("first-of-two-parts", 70_000_001, BF16, BF16, "none", None, FOLD_DEFAULT),
 ]
 
 
@@ -185,7 +189,9 @@ def _plan_step(side, n, gdt, pdt, scaler, hypers, tables, ends, parts, stream):
 # group ends: the last group of 3 elements is one the fold does not take
 # (three launches on both sides); the others fold, with an empty group
 # between two nonempty ones (the first nonempty group's K2 writes the state).
-PLAN_CASES = [("fold", [1000, 1000, 2005]), ("tiny-last-group", [1000, 1000, 1003]), ("empty-first", [0, 2000])]
+PLAN_CASES = [("fold", [1000, 1000, 2005]), ("tiny-last-group", [1000, 1000, 1003]), ("empty-first", [0, 2000]),
+              # above the bound: the first nonempty group's first part decides
+              ("first-part", [20_000_000, 20_000_104, 30_000_000]), ("first-part-empty-first", [0, 30_000_000])]
 
 
 @pytest.mark.parametrize("pcase", PLAN_CASES, ids=[c[0] for c in PLAN_CASES])
@@ -279,18 +285,19 @@ def test_optimizer_with_empty_group_matches_three_launches(gpu):
     assert sa.t == 11 and sa.overflow_count == 1 and sa.error == 0 and not math.isnan(sa.last_norm)
 
 
-@pytest.mark.parametrize("case", ["ok", "ngroups", "lr", "ok_fewer"])
+@pytest.mark.parametrize("case", ["ok", "ngroups", "lr", "ok_fewer", "ok_big"])
 def test_dev_block_step_two_and_three_launches(gpu, case):
     """dsx_zero_step_dev (the group block in device memory, the graph form)
     with a block the device-side checks accept or reject: two launches and
     three give the same bits; a rejected block (ngroups above the plan's
     slots, a negative lr) skips the step in every slot and sets
     DSX_STATE_ERR_GROUPS; a block with fewer groups than the plan steps those
-    and writes the other slots as skipped."""
+    and writes the other slots as skipped. ok_big: 2.7e7 elements, above the
+    fold's bound (K0 folded into the first part alone)."""
     import torch
     from distributedspeed_amd import _lib, ops
     from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
-    n, ends = 48, [16, 32, 48]
+    n, ends = (27_000_000, [9_000_000, 18_000_000, 27_000_000]) if case == "ok_big" else (48, [16, 32, 48])
     scaler = ScalerConfig(mode="dynamic", init_scale=2.0 ** 6, window=2, hysteresis=1)
     tab = BiasCorrectionTable(gpu, 0.9, 0.999)
     h = [AdamWHyper(lr=1e-3 * (k + 1), weight_decay=0.01, max_grad_norm=1.0).to_c() for k in range(3)]
@@ -345,7 +352,7 @@ def test_dev_block_step_two_and_three_launches(gpu, case):
         assert s.error == 0 and s.t == 3
         assert sc[0].skip == 0 and sc[1].skip == 1 and sc[2].skip == 1
         assert moved == [True, False, False]
-    else:
+    else:  # ok, ok_big
         assert s.error == 0 and s.t == 3 and all(x.skip == 0 for x in sc) and all(moved)
 
 
