@@ -37,6 +37,9 @@ STEP_FORMS = {
     "ragged (chunk table)": ("k1_unscale_norm_multi", "k0_finalize", "k2_adamw_multi"),
     "ragged, two launches (K0 folded into K3)": ("k1_unscale_norm_multi", None, "k3_adamw_fold"),
 }
+# Above the fold's bound the folded K2 is a step's first part and K2's other
+# parts follow it: they belong to the step, and to its K2 column.
+STEP_TAIL = {"k2_adamw_fold": "k2_adamw_flat", "k2_adamw_fold_dev": "k2_adamw_flat"}
 COPY_NAME = "__amd_rocclr_copyBuffer"
 COPY_BYTES = 1 << 30
 
@@ -159,7 +162,7 @@ def step_chains(trace_dir: str) -> dict:
         while i < len(rows):
             if all(i + q < len(rows) and rows[i + q][2] == k for q, k in enumerate(pat)):
                 j = i + len(pat)
-                while j < len(rows) and rows[j][2] == pat[-1]:
+                while j < len(rows) and rows[j][2] in (pat[-1], STEP_TAIL.get(pat[-1])):
                     j += 1
                 steps.append(rows[i:j])
                 i = j
@@ -169,8 +172,9 @@ def step_chains(trace_dir: str) -> dict:
             continue
         per = {}
         for k in full:
+            ks = (k, STEP_TAIL.get(k))
             per[k or "k0 (folded)"] = (None if k is None else
-                                       med([sum(e - s for s, e, n in st if n == k) for st in steps]))
+                                       med([sum(e - s for s, e, n in st if n in ks) for st in steps]))
         busy = [sum(e - s for s, e, _ in st) for st in steps]
         span = [st[-1][1] - st[0][0] for st in steps]
         period = [steps[k + 1][0][0] - steps[k][0][0] for k in range(len(steps) - 1)]
