@@ -285,26 +285,28 @@ def test_optimizer_with_empty_group_matches_three_launches(gpu):
     assert sa.t == 11 and sa.overflow_count == 1 and sa.error == 0 and not math.isnan(sa.last_norm)
 
 
-@pytest.mark.parametrize("case", ["ok", "ngroups", "lr", "ok_fewer", "ok_big"])
+@pytest.mark.parametrize("case", ["ok", "ngroups", "lr", "ok_fewer", "ok_big", "lr_big"])
 def test_dev_block_step_two_and_three_launches(gpu, case):
     """dsx_zero_step_dev (the group block in device memory, the graph form)
     with a block the device-side checks accept or reject: two launches and
     three give the same bits; a rejected block (ngroups above the plan's
     slots, a negative lr) skips the step in every slot and sets
     DSX_STATE_ERR_GROUPS; a block with fewer groups than the plan steps those
-    and writes the other slots as skipped. ok_big: 2.7e7 elements, above the
-    fold's bound (K0 folded into the first part alone)."""
+    and writes the other slots as skipped. ok_big, lr_big: 2.7e7 elements,
+    above the fold's bound (K0 folded into the first part alone, whose records
+    the later parts read)."""
     import torch
     from distributedspeed_amd import _lib, ops
     from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
-    n, ends = (27_000_000, [9_000_000, 18_000_000, 27_000_000]) if case == "ok_big" else (48, [16, 32, 48])
+    big = case.endswith("_big")
+    n, ends = (27_000_000, [9_000_000, 18_000_000, 27_000_000]) if big else (48, [16, 32, 48])
     scaler = ScalerConfig(mode="dynamic", init_scale=2.0 ** 6, window=2, hysteresis=1)
     tab = BiasCorrectionTable(gpu, 0.9, 0.999)
     h = [AdamWHyper(lr=1e-3 * (k + 1), weight_decay=0.01, max_grad_norm=1.0).to_c() for k in range(3)]
     g = _lib.DsxGroupsDev.from_buffer_copy(ops.pack_groups(h, [tab.table] * 3, [0, 0, 0], tab.length))
     if case == "ngroups":
         g.ngroups = 5
-    elif case == "lr":
+    elif case in ("lr", "lr_big"):
         g.hyper[1].lr = -1.0
     elif case == "ok_fewer":
         g.ngroups = 1
@@ -345,7 +347,7 @@ def test_dev_block_step_two_and_three_launches(gpu, case):
     sc = [ops.read_scalars(a.out[k * ops.SCALARS_BYTES:(k + 1) * ops.SCALARS_BYTES]) for k in range(3)]
     p = a.p.cpu()
     moved = [not torch.equal(p[b - 16:b], master[b - 16:b].cpu()) for b in ends]
-    if case in ("ngroups", "lr"):
+    if case in ("ngroups", "lr", "lr_big"):
         assert s.error & _lib.DSX_STATE_ERR_GROUPS and s.t == 0 and s.last_skip == 1
         assert all(x.skip == 1 for x in sc) and not any(moved)
     elif case == "ok_fewer":
