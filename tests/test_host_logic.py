@@ -378,3 +378,44 @@ def test_k2_parts_per_call_follow_the_library_rule():
     assert parts_per_call(1003782656, 0) == 1 == k2_parts(1003782656, 0)
     assert parts_per_call(1003782656, 1 << 25) == 30 == k2_parts(1003782656, 1 << 25)
 
+
+
+def test_rocprof_step_chains_count_the_parts_after_a_folded_first_part(tmp_path):
+    """The kernel-trace summary (rocprof_summary --chains) groups a step's
+    launches by form: K1 then the folded K2 and the plain K2 parts after it
+    (one step above the fold's bound), K1/K0/K2 parts (three launches), K1
+    over a chunk table then the folded K3; K2's column sums every part."""
+    import csv
+    from distributedspeed_amd.rocprof_summary import step_chains
+    names = {"k1": "void (anonymous namespace)::k1_unscale_norm<2, 4, true>(void const*, long)",
+             "k2f": "void (anonymous namespace)::k2_adamw_fold<2, 2, 2, true, DsxGroupsDev>(float*)",
+             "k2": "void (anonymous namespace)::k2_adamw_flat<2, 2, 2, true, false>(float*)",
+             "k0": "(anonymous namespace)::k0_finalize(double const*, int)",
+             "k1m": "void (anonymous namespace)::k1_unscale_norm_multi<1, true>(DsxTensorRef const*)",
+             "k3f": "void (anonymous namespace)::k3_adamw_fold<1, 1, true>(DsxTensorRef const*)"}
+    rows, t = [], 0
+
+    def launch(k, dur):
+        nonlocal t
+        rows.append({"Start_Timestamp": t, "End_Timestamp": t + dur, "Kernel_Name": names[k]})
+        t += dur + 1000
+
+    for _ in range(4):  # folded first part + two plain parts
+        launch("k1", 10_000), launch("k2f", 100_000), launch("k2", 90_000), launch("k2", 80_000)
+    for _ in range(3):  # three launches, two parts
+        launch("k1", 10_000), launch("k0", 4_000), launch("k2", 95_000), launch("k2", 95_000)
+    for _ in range(3):  # ragged, folded
+        launch("k1m", 5_000), launch("k3f", 9_000)
+    with open(tmp_path / "t_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Start_Timestamp", "End_Timestamp", "Kernel_Name"])
+        w.writeheader()
+        w.writerows(rows)
+    res = step_chains(str(tmp_path))
+    two = res["flat, eager, two launches (K0 folded into K2)"]
+    assert two["steps"] == 4 and two["kernels_us"]["k2_adamw_fold"] == 270.0
+    assert two["kernels_us"]["k1_unscale_norm"] == 10.0 and two["kernel_busy_us"] == 280.0
+    three = res["flat, eager, three launches"]
+    assert three["steps"] == 3 and three["kernels_us"]["k2_adamw_flat"] == 190.0
+    assert three["kernels_us"]["k0_finalize"] == 4.0
+    rag = res["ragged, two launches (K0 folded into K3)"]
+    assert rag["steps"] == 3 and rag["kernels_us"]["k3_adamw_fold"] == 9.0
