@@ -17,9 +17,11 @@
  *                         chunk table (one launch per pass for any count).
  *
  * The one-call steps (dsx_zero_step_flat, dsx_zero_step_plan,
- * dsx_zero_step_dev) run without a K0 launch, with the same results: small
- * partitions (dsx_set_tuning_fold) as K1 and K2 with K0's finalize folded
- * in, larger ones with it folded into the first of K2's parts.
+ * dsx_zero_step_dev) run without a K0 launch where the fold's limits allow
+ * (at most 512 partials, every nonempty group at least 4 elements), with the
+ * same results: small partitions (dsx_set_tuning_fold) as K1 and K2 with
+ * K0's finalize folded in, larger ones with it folded into the first of K2's
+ * parts.
  *
  * Conventions
  *   - Every pointer argument is a DEVICE pointer owned by the caller, except
