@@ -122,3 +122,54 @@ def test_noalloc_picks_partials_and_rejects_oversize(gpu):
     torch.cuda.synchronize()
     for name, x, y in zip(("master", "exp_avg", "exp_avg_sq", "param16", "state"), a.host(n), b.host(n)):
         assert np.array_equal(x, y), f"{name} differs"
+
+
+def test_noalloc_step_matches_on_every_launch_form(gpu):
+    """The same comparison over the step's three launch forms: above the
+    fold's bound (K0 folded into the first of K2's two parts, the second part
+    reading its records; once with an inf in the second part, so the skip is
+    decided in the first part's launch), more partials than the fold takes
+    (K1, K0, K2 as three launches, K0's scalars in the library scratch), and
+    a partition the fold takes whole. fp16 grads with the dynamic scaler."""
+    import torch
+    from distributedspeed_amd import _lib, ops
+    from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
+    from oracle import oracle as O
+
+    dt = F16
+    big, small = 70_000_001, 3_000_017  # big: two K2 parts of 2^26 elements at most
+    scaler = ScalerConfig(mode="dynamic", init_scale=2.0 ** 16, window=1000, hysteresis=1)
+    hyper = AdamWHyper(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, max_grad_norm=1.0)
+    p, m, v, g16 = make_state(big, seed=91, gdt=dt, g_sigma=1e-3, scale=2.0 ** 16)
+    p16 = O.cast16(p, dt)
+    a = _Side(gpu, p, m, v, p16, g16, dt, scaler)
+    b = _Side(gpu, p, m, v, p16, g16, dt, scaler)
+    del p, m, v, p16, g16
+    bc = BiasCorrectionTable(gpu, hyper.beta1, hyper.beta2)
+    stream = ops.stream_of(gpu)
+    # (n, nparts (0: suggested), pass out, put an inf into the second part)
+    calls = [(big, 0, True, False), (big, 0, False, True), (small, 1024, False, False), (small, 0, True, False)]
+    skips = 0
+    for k, (n, nparts, pass_out, inf) in enumerate(calls):
+        if inf:
+            for side in (a, b):
+                side.g[3 * n // 4] = float("inf")
+            skips += 1
+        nparts = nparts or ops.suggest_partials(n)
+        partials = torch.zeros(nparts, dtype=torch.float64, device=gpu)
+        _say(f"noalloc forms call={k} n={n} nparts={nparts} out={'caller' if pass_out else 'scratch'} inf={inf}")
+        _lib.call("dsx_zero_step_flat", *_args(a, n, dt, scaler, hyper, bc, stream), _ptr(partials), nparts,
+                  _ptr(a.out), stream)
+        _lib.call("dsx_zero_step_flat_noalloc", *_args(b, n, dt, scaler, hyper, bc, stream), nparts,
+                  _ptr(b.out) if pass_out else None, stream)
+        torch.cuda.synchronize()
+        for name, x, y in zip(("master", "exp_avg", "exp_avg_sq", "param16", "state"), a.host(big), b.host(big)):
+            assert np.array_equal(x, y), f"call {k}: {name} differs ({(x != y).sum()} elements)"
+        if pass_out:
+            assert np.array_equal(a.out.cpu().numpy(), b.out.cpu().numpy()), f"call {k}: step scalars differ"
+        st = ops.read_state(b.state)
+        assert st.error == 0
+        assert st.last_skip == (1 if inf else 0)
+    st = ops.read_state(b.state)
+    assert st.t == len(calls) - skips
+    assert st.scale == 2.0 ** 15  # halved once, by the skipped step
