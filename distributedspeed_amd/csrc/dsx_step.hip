@@ -1690,8 +1690,10 @@ bool fold_applies(int64_t n, int32_t nparts) {
 // Above the fold's bound, K0 is folded into the first of K2's parts alone,
 // launched one block per CU (so that few blocks pay the partials' reduction),
 // and the other parts read the records that launch's writer block wrote.
+// Like the whole fold, it needs n >= 4 (a bound of 1 to 3 set through
+// dsx_set_tuning_fold would otherwise send 2 or 3 elements to it).
 bool fold_first_applies(int64_t n, int32_t nparts) {
-  return g_tune.fold_max_elems > 0 && n > g_tune.fold_max_elems && nparts <= kFoldMaxParts;
+  return g_tune.fold_max_elems > 0 && n >= 4 && n > g_tune.fold_max_elems && nparts <= kFoldMaxParts;
 }
 
 // The length of K2's first part over n elements (k2_dispatch's split).

@@ -43,6 +43,11 @@ CASES = [
     # here the whole partition (one part) and the first of two parts
     ("first-part-whole", 3_000_007, F16, F16, "dynamic", None, 1 << 20),
     ("first-of-two-parts", 70_000_001, BF16, BF16, "none", None, FOLD_DEFAULT),
+    # bounds under 4: 2 and 3 elements take three launches (the fold needs a
+    # 4-element slot), 4 elements above a bound of 3 fold into the first part
+    ("n2-bound1", 2, BF16, BF16, "none", 1, 1),
+    ("n3-bound2", 3, F16, F16, "dynamic", 1, 2),
+    ("n4-bound3", 4, F16, F16, "dynamic", 1, 3),
 ]
 
 
