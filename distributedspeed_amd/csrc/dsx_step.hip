@@ -146,7 +146,8 @@ int cu_count() {
   return cus;
 }
 
-int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// b > 0; exact for any a, with no intermediate that can overflow.
+int64_t ceil_div(int64_t a, int64_t b) { return a / b + (a % b > 0 ? 1 : 0); }
 
 // ---- element helpers -------------------------------------------------------
 
@@ -2120,7 +2121,12 @@ int64_t dsx_count_chunks(const int64_t* numels, int32_t ntensors, int64_t chunk_
       fail(DSX_EINVAL, "dsx_count_chunks: negative numel");
       return -1;
     }
-    c += ceil_div(numels[i], chunk_elems);
+    const int64_t add = ceil_div(numels[i], chunk_elems);
+    if (add > INT64_MAX - c) {
+      fail(DSX_EINVAL, "dsx_count_chunks: the chunk count overflows int64");
+      return -1;
+    }
+    c += add;
   }
   return c;
 }
@@ -2134,7 +2140,10 @@ int64_t dsx_build_chunks(const int64_t* numels, int32_t ntensors, int64_t chunk_
   }
   int64_t c = 0;
   for (int32_t i = 0; i < ntensors; ++i) {
-    for (int64_t s = 0; s < numels[i]; s += chunk_elems) {
+    // By chunk index: every start is below numels[i], so nothing overflows.
+    const int64_t nc = ceil_div(numels[i], chunk_elems);
+    for (int64_t j = 0; j < nc; ++j) {
+      const int64_t s = j * chunk_elems;
       out[c].tensor = i;
       out[c].reserved = 0;
       out[c].start = s;

@@ -71,6 +71,25 @@ def test_chunk_table_host_side(lib):
     assert b"capacity" in lib.dsx_last_error()
 
 
+def test_chunk_table_extreme_sizes(lib):
+    """Counts and starts near the int64 limit are exact (no intermediate
+    overflows), and a total count beyond int64 is refused."""
+    from distributedspeed_amd import _lib
+    big = 2 ** 63 - 1
+    arr = (ctypes.c_int64 * 2)(4096, big)
+    ce = 2 ** 63 - 8  # a chunk size whose ceil_div intermediate would overflow
+    assert lib.dsx_count_chunks(arr, 2, ce) == 1 + 2
+    ce = 2 ** 62
+    assert lib.dsx_count_chunks(arr, 2, ce) == 1 + 2
+    out = (_lib.DsxChunk * 3)()
+    assert lib.dsx_build_chunks(arr, 2, ce, out, 3) == 3
+    assert [(c.tensor, c.start, c.len) for c in out] == [(0, 0, 4096), (1, 0, ce), (1, ce, big - ce)]
+    many = (ctypes.c_int64 * 8)(*([big] * 8))  # 2^60 chunks each: 7 fit in int64, 8 do not
+    assert lib.dsx_count_chunks(many, 7, 8) == 7 * 2 ** 60
+    assert lib.dsx_count_chunks(many, 8, 8) == -1
+    assert b"overflows" in lib.dsx_last_error()
+
+
 def test_argument_checks_reject_before_launch(lib):
     """Rejected arguments return DSX_EINVAL with a message and never reach a
     HIP call (this runs without a GPU)."""
