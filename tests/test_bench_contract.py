@@ -62,3 +62,20 @@ def test_cpu_baseline_host_facts():
     assert info["cpu_model"]
     n, why = bench.cpu_threads()
     assert n >= 1 and why
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("workload", ["mlp", "mlp-train", "gpt2-small", "ffn-train"])
+def test_secondary_workloads_print_one_line(gpu, workload):
+    """The secondary workloads (configs[0] and [1] through the drop-in
+    classes, the training iterations) still run and print one JSON line with
+    a positive value. configs[3] and [4] run inside the headline line's
+    secondary_configs."""
+    print(f"[gpu-test] bench.py --workload {workload}", file=sys.stderr, flush=True)
+    r = _run(["--workload", workload, "--steps", "3", "--warmup", "1"], 280)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [x for x in r.stdout.splitlines() if x.startswith("{")]
+    assert len(lines) == 1, r.stdout[-2000:]
+    d = json.loads(lines[0])
+    assert d["metric"] and d["unit"] and d["value"] > 0, d
+    assert isinstance(d["config"], dict) and d["config"], d
