@@ -68,6 +68,14 @@ def _bind_hook(ref, i: int):
         if g is view:
             part._hn_armed = False
             return
+        if view.numel() == 0:
+            # Nothing to copy (and an empty tensor's data_ptr() is 0, the
+            # same as any other empty tensor's): the parameter's one partial
+            # stays the zero it was allocated with.
+            if part._hn_on:
+                part._hn_fired[i] += 1
+            p.grad = view
+            return
         if g is not None and g.data_ptr() != view.data_ptr():
             if not (part._hn_armed and part._copy_with_norm(i, g)):
                 view.copy_(g)

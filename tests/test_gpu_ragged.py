@@ -329,3 +329,53 @@ def test_ragged_random_lists_match_flat(gpu, seed):
         _lib.call("dsx_set_tuning_fold", ctypes.c_int64(fold_default))
     st = rag.read_state()
     assert st.t == (4 if fp16 else 5) and st.error == 0
+
+
+@pytest.mark.parametrize("handover", [False, True], ids=["grads-copied", "autograd-set-to-none"])
+def test_zero_element_parameters(gpu, handover):
+    """Parameters with no elements (torch's AdamW takes them) in both storage
+    forms: among others, first and last in the list, and a whole group of
+    them. They get no chunks and no elements of the flat buffer; every other
+    tensor steps bit for bit as in the flat form. With `handover` the grads
+    come from autograd after zero_grad(set_to_none=True), so the flat form's
+    hook copies (an empty grad included) and its segment reduce replace K1."""
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
+    shapes = ((0,), (257, 33), (0, 5), (1000,), (5,), (0,))
+    dt = torch.float16
+    sc = ScalerConfig(mode="dynamic", init_scale=2.0 ** 8, window=2, hysteresis=1)
+    opts = []
+    for cls in (AdamWOptimizer, MultiTensorAdamWOptimizer):
+        g = torch.Generator().manual_seed(11)
+        ps = [torch.nn.Parameter((torch.randn(s, generator=g) * 0.05).to(gpu, dt)) for s in shapes]
+        groups = [{"params": [ps[0], ps[2]]}, {"params": [ps[1], ps[3]], "lr": 3e-4},
+                  {"params": [ps[4], ps[5]], "betas": (0.8, 0.95)}]
+        opts.append(cls(groups, lr=1e-3, weight_decay=0.01, max_grad_norm=0.5, param_dtype=dt, loss_scaler=sc,
+                        device=gpu))
+    flat, rag = opts
+    before = [p.detach().clone() for p in rag.dsx_params]
+    ggen = torch.Generator(device=gpu).manual_seed(12)
+    _say(f"zero-element params, handover={handover}")
+    for step in range(4):
+        scale = float(flat.read_state().scale)
+        if handover:
+            w = [torch.randn(p.shape, generator=ggen, device=gpu) * 1e-2 for p in flat.dsx_params]
+            for opt in opts:
+                opt.zero_grad(set_to_none=True)
+                loss = sum((p.float() * wi).sum() for p, wi in zip(opt.dsx_params, w))
+                (loss * scale).backward()
+            assert flat.flat.hook_norm_ready(), "the flat step would take K1, not the hooks' partials"
+        else:
+            _set_grads(flat, rag, ggen, scale, dt, inf_at=(3 if step == 1 else None))
+        flat.step()
+        rag.step()
+        _check(flat, rag, f"zero-element step {step}")
+    # dsx_params are in group order
+    order = [0, 2, 1, 3, 4, 5]
+    assert [tuple(p.shape) for p in rag.dsx_params] == [tuple(shapes[k]) for k in order]
+    for p, b in zip(rag.dsx_params, before):
+        if p.numel():
+            assert not torch.equal(p.detach(), b), f"tensor of shape {tuple(p.shape)} did not step"
+    st = rag.read_state()
+    assert st.error == 0 and st.t == (4 if handover else 3)
