@@ -379,3 +379,23 @@ def test_zero_element_parameters(gpu, handover):
             assert not torch.equal(p.detach(), b), f"tensor of shape {tuple(p.shape)} did not step"
     st = rag.read_state()
     assert st.error == 0 and st.t == (4 if handover else 3)
+
+
+def test_only_zero_element_parameters(gpu):
+    """A model whose parameters all have no elements: an empty flat buffer and
+    an empty chunk table. Both forms step (norm 0, no skip, t advances) and
+    report no error, as torch's AdamW does nothing and raises nothing."""
+    import torch
+    from distributedspeed_amd.flat_step import ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
+    sc = ScalerConfig(mode="dynamic", init_scale=2.0 ** 8, window=2, hysteresis=1)
+    for cls in (AdamWOptimizer, MultiTensorAdamWOptimizer):
+        ps = [torch.nn.Parameter(torch.zeros(s, device=gpu, dtype=torch.float16)) for s in ((0,), (0, 5))]
+        opt = cls(ps, lr=1e-3, max_grad_norm=1.0, param_dtype=torch.float16, loss_scaler=sc, device=gpu)
+        _say(f"only zero-element params: {cls.__name__}")
+        for _ in range(2):
+            opt.zero_grad(set_to_none=True)
+            sum(p.float().sum() for p in opt.dsx_params).backward()
+            opt.step()
+        st = opt.read_state()
+        assert st.error == 0 and st.t == 2 and st.last_skip == 0 and st.last_norm == 0.0, cls.__name__
