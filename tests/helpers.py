@@ -2,6 +2,8 @@
 storage, and the tolerance used against torch's CPU AdamW."""
 from __future__ import annotations
 
+import hashlib
+
 import numpy as np
 
 F16, BF16 = 1, 2
@@ -74,3 +76,46 @@ def cancellation_ulp_ok(ours: np.ndarray, ref: np.ndarray, decayed: np.ndarray, 
     tol = k * np.spacing(scale)
     diff = np.abs(ours.astype(np.float64) - ref.astype(np.float64))
     return (diff <= tol) | (np.isnan(ours) & np.isnan(ref))
+
+
+# configs[0] (the 3-layer MLP partition) as the parity tests run it: fp16
+# grads and params, static loss scale 2^16, no clip, ten steps from zero
+# moments. Its per-step digests are committed (tests/golden/make_digests.py).
+MLP_CASE = dict(n=1_863_690, gdt=F16, pdt=F16, seed=0, g_sigma=0.01, steps=10, scale=2.0 ** 16,
+                hyper=dict(lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, max_grad_norm=0.0))
+
+
+def step_digests(p, m, v, p16) -> dict:
+    """SHA-256 of each array's bit pattern (fp32 as uint32, 16-bit as uint16)."""
+    def h(a, dt):
+        return hashlib.sha256(np.ascontiguousarray(a).view(dt).tobytes()).hexdigest()
+    return {"master": h(p, np.uint32), "exp_avg": h(m, np.uint32), "exp_avg_sq": h(v, np.uint32),
+            "param16": h(p16, np.uint16)}
+
+
+def mlp_case_inputs(O):
+    """MLP_CASE's initial master / exp_avg / exp_avg_sq / param16 and its
+    grads generator (one call per step), as _flat_run in the GPU parity
+    tests draws them."""
+    c = MLP_CASE
+    p, m, v, _ = make_state(c["n"], c["seed"], c["gdt"], c["g_sigma"], edges=False, mv_warm=False, p_sigma=0.02)
+    p16 = O.cast16(p, c["pdt"])
+    rng = np.random.default_rng(c["seed"] + 1)
+
+    def grads():
+        return O.cast16((rng.standard_normal(c["n"]) * c["g_sigma"] * c["scale"]).astype(np.float32), c["gdt"])
+    return p, m, v, p16, grads
+
+
+def mlp_case_oracle_digests(O) -> list:
+    """MLP_CASE through the oracle: the digests after every step."""
+    c = MLP_CASE
+    p, m, v, p16, grads = mlp_case_inputs(O)
+    orc = O.ZeroStepOracle(p, m, v, p16, c["pdt"], c["gdt"], O.Hyper(**c["hyper"]),
+                           O.LossScalerSpec(scale=c["scale"], dynamic=False))
+    out = []
+    for _ in range(c["steps"]):
+        r = orc.step(grads())
+        assert not r.skipped
+        out.append(step_digests(orc.p, orc.m, orc.v, orc.p16))
+    return out

@@ -4,13 +4,16 @@ bit-identical: the kernels follow the oracle's operation order and rounding
 (IEEE division/sqrt, explicit fma only), so any difference is a bug."""
 from __future__ import annotations
 
+import json
 import math
+import os
 import sys
 
 import numpy as np
 import pytest
 
-from helpers import (BF16, F16, f32_to_torch, make_state, np16_to_torch, torch16_to_np)
+from helpers import (BF16, F16, MLP_CASE, f32_to_torch, make_state, np16_to_torch, step_digests,
+                     torch16_to_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -118,9 +121,11 @@ def test_k1_detects_nonfinite(gpu, oracle, pos, bad, gdt):
     assert not math.isfinite(oracle.sumsq(g16, gdt, 1.0))
 
 
-def _flat_run(gpu, O, n, gdt, pdt, hyper, scaler_cfg, steps, seed, g_sigma, inject=None, p_sigma=0.02):
+def _flat_run(gpu, O, n, gdt, pdt, hyper, scaler_cfg, steps, seed, g_sigma, inject=None, p_sigma=0.02,
+              digests=None):
     """Run `steps` full steps through FlatStep and the oracle side by side;
-    compare every step bit-for-bit. inject(step) -> index to set to +inf."""
+    compare every step bit-for-bit. inject(step) -> index to set to +inf.
+    digests: per-step SHA-256 digests the GPU arrays must also match."""
     import torch
     from distributedspeed_amd import ops
     from distributedspeed_amd.flat_step import AdamWHyper, FlatStep, ScalerConfig
@@ -161,6 +166,9 @@ def _flat_run(gpu, O, n, gdt, pdt, hyper, scaler_cfg, steps, seed, g_sigma, inje
         for name, a, b in (("master", gp, p), ("exp_avg", gm, m), ("exp_avg_sq", gv, v)):
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {step} {name} differs"
         assert np.array_equal(torch16_to_np(tp16), p16), f"step {step} param16 differs"
+        if digests is not None:
+            got = step_digests(gp, gm, gv, torch16_to_np(tp16))
+            assert got == digests[step - 1], f"step {step}: {[k for k in got if got[k] != digests[step - 1][k]]}"
     return history, fs
 
 
@@ -169,9 +177,13 @@ def test_config1_mlp_ten_steps(gpu, oracle):
     n = 784 * 1024 + 1024 + 1024 * 1024 + 1024 + 1024 * 10 + 10
     assert n == 1_863_690
     _say("config1 mlp 10 steps")
-    hist, _ = _flat_run(gpu, oracle, n, F16, F16,
-                        dict(lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, max_grad_norm=0.0),
-                        dict(mode="static", init_scale=2.0 ** 16), steps=10, seed=0, g_sigma=0.01)
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config0_mlp_digests.json")) as f:
+        golden = json.load(f)
+    c = MLP_CASE
+    assert golden["case"]["n"] == n == c["n"] and golden["case"]["steps"] == c["steps"] == 10
+    hist, _ = _flat_run(gpu, oracle, n, c["gdt"], c["pdt"], c["hyper"],
+                        dict(mode="static", init_scale=c["scale"]), steps=c["steps"], seed=c["seed"],
+                        g_sigma=c["g_sigma"], digests=golden["digests"])
     assert [h[2] for h in hist] == list(range(1, 11))
 
 

@@ -280,3 +280,21 @@ def test_step_same_for_every_grad_storage_and_cast_matches(oracle, n, hi):
     for p, m, v in outs[1:]:
         for a, b in zip((p, m, v), outs[0]):
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_config0_mlp_digests_match_the_committed_ones(oracle):
+    """The oracle reproduces the committed per-step SHA-256 digests of
+    configs[0]'s partition over ten steps (tests/golden/make_digests.py); the
+    GPU parity test holds the kernels to the same digests."""
+    import json
+    import os
+
+    from helpers import MLP_CASE, mlp_case_oracle_digests
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config0_mlp_digests.json")
+    with open(path) as f:
+        d = json.load(f)
+    assert d["case"] == json.loads(json.dumps(MLP_CASE))
+    got = mlp_case_oracle_digests(oracle)
+    assert len(got) == MLP_CASE["steps"] == len(d["digests"])
+    for step, (a, b) in enumerate(zip(got, d["digests"]), 1):
+        assert a == b, f"step {step}: {[k for k in a if a[k] != b[k]]} differ"
