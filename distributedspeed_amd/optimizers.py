@@ -69,9 +69,20 @@ class _FusedAdamWBase(torch.optim.Optimizer):
         super().__init__(params, defaults)
         if len(self.param_groups) > DSX_MAX_GROUPS:
             raise ValueError(f"at most {DSX_MAX_GROUPS} parameter groups are supported")
-        plist = [p for g in self.param_groups for p in g["params"]]
-        if not plist:
+        everything = [p for g in self.param_groups for p in g["params"]]
+        if not everything:
             raise ValueError("optimizer got an empty parameter list")
+        # torch's AdamW steps a parameter only when it has a grad, so a frozen
+        # one (requires_grad=False) is never touched. Such parameters stay out
+        # of the stepped storage here; the state dict keeps torch's indexing
+        # over every parameter of the groups (_state_index maps a stepped
+        # parameter to its index there).
+        self._stepped = [[p for p in g["params"] if p.requires_grad] for g in self.param_groups]
+        self._frozen = [p for p in everything if not p.requires_grad]
+        self._state_index = [i for i, p in enumerate(everything) if p.requires_grad]
+        plist = [p for ps in self._stepped for p in ps]
+        if not plist:
+            raise ValueError("optimizer got no parameter that requires grad")
         if device is None:
             device = plist[0].device if plist[0].is_cuda else torch.device("cuda", torch.cuda.current_device())
         self.device = torch.device(device)
@@ -102,6 +113,11 @@ class _FusedAdamWBase(torch.optim.Optimizer):
         self._opt_called = True
         if self._adopted_from is not None:
             self._adopted_from._opt_called = True
+        for p in self._frozen:
+            if p.grad is not None:
+                raise RuntimeError("a parameter that did not require grad when the optimizer was built has a grad: "
+                                   "torch would step it, this optimizer holds no state for it; build the "
+                                   "optimizer again after changing requires_grad")
 
     # ---- skip flag on the host, without waiting for K2 ---------------------------------
 
@@ -160,6 +176,12 @@ class _FusedAdamWBase(torch.optim.Optimizer):
         capturable=True (a captured iteration must not depend on Python-side
         state)."""
         self.store.zero_grad(set_to_none=set_to_none and self._grads_may_move())
+        for p in self._frozen:  # as torch's zero_grad does for every parameter of the groups
+            if p.grad is not None:
+                if set_to_none:
+                    p.grad = None
+                else:
+                    p.grad.zero_()
 
     def _grads_may_move(self) -> bool:
         return True
@@ -355,7 +377,7 @@ class _FusedAdamWBase(torch.optim.Optimizer):
         state = {}
         for i in range(len(self.store.params)):
             v = self.store.views_of(i)
-            state[i] = {"step": torch.tensor(float(s.t)), "exp_avg": v["exp_avg"].detach().cpu().clone(),
+            state[self._state_index[i]] = {"step": torch.tensor(float(s.t)), "exp_avg": v["exp_avg"].detach().cpu().clone(),
                         "exp_avg_sq": v["exp_avg_sq"].detach().cpu().clone(),
                         "master": v["master"].detach().cpu().clone()}
         return {"state": state, "param_groups": groups,
@@ -377,20 +399,21 @@ class _FusedAdamWBase(torch.optim.Optimizer):
                 if k != "params":
                     g[k] = tuple(v) if k == "betas" else v
         st = state_dict["state"]
+        ix = self._state_index
         # A torch (or the reference's) state dict holds no master: those
         # parameters take theirs from the current params, which the caller
         # loads from the same checkpoint.
-        self.store.refresh_master([i for i in range(len(self.store.params)) if "master" not in st.get(i, {})])
+        self.store.refresh_master([i for i in range(len(self.store.params)) if "master" not in st.get(ix[i], {})])
         with torch.no_grad():
             for i in range(len(self.store.params)):
-                if i not in st:
+                if ix[i] not in st:
                     continue
                 views = self.store.views_of(i)
                 for key in ("exp_avg", "exp_avg_sq", "master"):
-                    if key in st[i]:
-                        src = st[i][key]
+                    if key in st[ix[i]]:
+                        src = st[ix[i]][key]
                         if src.shape != views[key].shape:
-                            raise ValueError(f"state for parameter {i} has shape {tuple(src.shape)}, "
+                            raise ValueError(f"state for parameter {ix[i]} has shape {tuple(src.shape)}, "
                                              f"expected {tuple(views[key].shape)}")
                         views[key].copy_(src.to(views[key].device, torch.float32))
             self.store.refresh_params16()
@@ -425,7 +448,7 @@ class AdamWOptimizer(_FusedAdamWBase):
             raise ValueError("graph=True / capturable=True need HBM-resident state (offload=False)")
         if graph and capturable:
             raise ValueError("graph=True captures the step itself; capturable=True is for callers that capture it")
-        self.flat = FlatPartition([g["params"] for g in self.param_groups], self.device, param_dtype, param_names,
+        self.flat = FlatPartition(self._stepped, self.device, param_dtype, param_names,
                                   offload=offload)
         self.store = self.flat
         self.streamer = HostStateStreamer(self.device, offload_chunk_elems) if offload else None
@@ -632,7 +655,7 @@ class MultiTensorAdamWOptimizer(_FusedAdamWBase):
         plist = self._init_common(params, lr, betas, eps, weight_decay, max_grad_norm, loss_scaler, device)
         if param_dtype is None and plist[0].dtype in (torch.float16, torch.bfloat16):
             param_dtype = plist[0].dtype
-        self.store = RaggedParams([g["params"] for g in self.param_groups], self.device, param_dtype, param_names,
+        self.store = RaggedParams(self._stepped, self.device, param_dtype, param_names,
                                   chunk_elems)
         self.streamer = None
         self.use_graph = False

@@ -710,3 +710,52 @@ def test_one_call_step_matches_three_launches(gpu):
     sa, sb = a.read_state(), b.read_state()
     assert bytes(sa) == bytes(sb)
     assert sa.t > 1024 and sa.overflow_count >= 1 and sa.error == 0
+
+
+@pytest.mark.parametrize("contiguous", [True, False], ids=["flat", "ragged"])
+def test_frozen_parameters_are_not_stepped(gpu, contiguous):
+    """torch's AdamW steps a parameter only when it has a grad, so a frozen
+    one (requires_grad=False) given with the others -- model.parameters() in
+    a fine-tune -- keeps its values bit for bit, and the others step exactly
+    as when it is left out. The state dict keeps torch's indexing over every
+    parameter of the groups (no state for the frozen one) and loads back; a
+    grad that later appears on the frozen parameter is refused."""
+    import torch
+    from distributedspeed_amd.optimizers import AdamWOptimizer, MultiTensorAdamWOptimizer
+    cls = AdamWOptimizer if contiguous else MultiTensorAdamWOptimizer
+
+    def model():
+        torch.manual_seed(0)
+        m = torch.nn.Sequential(torch.nn.Linear(16, 32), torch.nn.ReLU(), torch.nn.Linear(32, 4)).to(gpu)
+        m[0].weight.requires_grad_(False)
+        return m
+
+    a, b, c = model(), model(), model()
+    frozen = a[0].weight.detach().clone()
+    oa = cls(list(a.parameters()), lr=1e-2, weight_decay=0.1, device=gpu)
+    ob = cls([p for p in b.parameters() if p.requires_grad], lr=1e-2, weight_decay=0.1, device=gpu)
+    x = torch.randn(8, 16, device=gpu, generator=torch.Generator(device=gpu).manual_seed(1))
+    print(f"[gpu-test] frozen parameters, {'flat' if contiguous else 'ragged'}", file=sys.stderr, flush=True)
+    for _ in range(3):
+        for m, o in ((a, oa), (b, ob)):
+            o.zero_grad()
+            m(x).square().sum().backward()
+            o.step()
+    torch.cuda.synchronize()
+    assert torch.equal(a[0].weight, frozen)
+    for pa, pb in zip(a.parameters(), b.parameters()):
+        assert torch.equal(pa, pb)
+    sd = oa.state_dict()
+    assert sorted(sd["state"]) == [1, 2, 3] and sd["param_groups"][0]["params"] == [0, 1, 2, 3]
+    oc = cls(list(c.parameters()), lr=1e-2, weight_decay=0.1, device=gpu)
+    oc.load_state_dict(sd)
+    sc = oc.state_dict()
+    assert sorted(sc["state"]) == [1, 2, 3]
+    for k in (1, 2, 3):
+        for name in ("exp_avg", "exp_avg_sq", "master"):
+            assert torch.equal(sc["state"][k][name], sd["state"][k][name]), (k, name)
+    a[0].weight.requires_grad_(True)
+    oa.zero_grad()
+    a(x).square().sum().backward()
+    with pytest.raises(RuntimeError, match="did not require grad when the optimizer was built"):
+        oa.step()
