@@ -262,3 +262,21 @@ def test_c_caller_builds_and_checks_its_arguments():
     assert r.returncode == 1 and "usage" in r.stderr
     r = subprocess.run([exe, "0", "1", "4", "/tmp"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 1 and "bad arguments" in r.stderr
+
+
+def test_missing_library_fails_loudly():
+    """Without a built libdsx.so the binding raises (there is no CPU or torch
+    fallback); run in a fresh process, since a loaded library is cached."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "from distributedspeed_amd import _lib\n"
+            "try:\n"
+            "    _lib.load('/nonexistent/libdsx.so')\n"
+            "except RuntimeError as e:\n"
+            "    print('raised:', e)\n"
+            "    sys.exit(0)\n"
+            "sys.exit(1)\n") % ROOT
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "is not built" in r.stdout and "no non-HIP fallback" in r.stdout
