@@ -79,6 +79,15 @@ class DistributedSpeedEngine(torch.nn.Module):
         zcfg = {"stage": config.zero_optimization.stage,
                 "gradient_accumulation_steps": config.gradient_accumulation_steps}
         self.optimizer = ZeROOptimizer(optimizer, zcfg, list(optimizer.dsx_params))
+        if self.param_dtype is not None:
+            # The stepped parameters now live in the 16-bit buffer and forward
+            # takes 16-bit inputs; the parameters the optimizer does not step
+            # (frozen ones) take the same dtype, so the module runs in one.
+            stepped = {id(p) for p in optimizer.dsx_params}
+            with torch.no_grad():
+                for p in self.module.parameters():
+                    if id(p) not in stepped and p.is_floating_point() and p.dtype != self.param_dtype:
+                        p.data = p.data.to(self.param_dtype)
         # With 16-bit params the step reads and writes the fp32 master; a state
         # dict loaded into the module later writes only the params, so the
         # master follows them (the reference steps the params themselves).

@@ -759,3 +759,34 @@ def test_frozen_parameters_are_not_stepped(gpu, contiguous):
     a(x).square().sum().backward()
     with pytest.raises(RuntimeError, match="did not require grad when the optimizer was built"):
         oa.step()
+
+
+@pytest.mark.parametrize("contiguous", [True, False], ids=["flat", "ragged"])
+def test_engine_fine_tune_with_a_frozen_layer(gpu, contiguous):
+    """The fine-tune pattern: a frozen first layer and torch's AdamW over
+    model.parameters() handed to initialize() under bf16. The frozen layer
+    takes the 16-bit dtype with the rest, so the module runs in one; it
+    keeps its values through the steps while the trained layers move."""
+    import torch
+    import distributedspeed_amd as ds
+    model = _mlp(7).cuda()
+    model[0].weight.requires_grad_(False)
+    model[0].bias.requires_grad_(False)
+    topt = torch.optim.AdamW(model.parameters(), lr=1e-3, weight_decay=0.1)
+    cfg = {"bf16": {"enabled": True}, "max_grad_norm": 1.0,
+           "zero_optimization": {"stage": 2, "contiguous_gradients": contiguous}}
+    engine, opt, _, _ = ds.initialize(model, cfg, optimizer=topt)
+    assert all(p.dtype == torch.bfloat16 for p in model.parameters())
+    frozen = [model[0].weight.detach().clone(), model[0].bias.detach().clone()]
+    trained = model[2].weight.detach().clone()
+    x = torch.randn(16, 784, device=gpu, generator=torch.Generator(device=gpu).manual_seed(3))
+    y = torch.randint(0, 10, (16,), device=gpu, generator=torch.Generator(device=gpu).manual_seed(4))
+    _say(f"fine-tune with a frozen layer, contiguous={contiguous}")
+    for _ in range(3):
+        loss = torch.nn.functional.cross_entropy(engine(x).float(), y)
+        engine.backward(loss)
+        engine.step()
+    torch.cuda.synchronize()
+    assert torch.equal(model[0].weight, frozen[0]) and torch.equal(model[0].bias, frozen[1])
+    assert not torch.equal(model[2].weight, trained)
+    assert opt.current_step == 3
