@@ -1917,7 +1917,10 @@ int do_adamw_multi(const DsxTensorRef* tensors, const DsxChunk* chunks, int64_t 
   // CU, one block per CU walking the list as one front (like K2's
   // grid-stride); from 256 chunks per CU on, a grid of about four chunks per
   // block, far more blocks than the CUs hold at once, with K2's drain, is
-  // 4-5% faster (the blocks start as others finish).
+  // 4-5% faster (the blocks start as others finish). Five chunks per block
+  // beat four by 0.5-0.7% over freshly allocated lists of 321 and 496 chunks
+  // per CU, but lost by 0.6% in a process that had allocated and freed other
+  // large buffers first (the same 496-chunk list, alternated), so four stay.
   const int64_t cus = cu_count();
   int64_t bpc = g_tune.k3_blocks_per_cu;
   int unroll = g_tune.k3_unroll;
