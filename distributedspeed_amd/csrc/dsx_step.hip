@@ -1387,8 +1387,10 @@ __global__ __launch_bounds__(kBlock) void k3_adamw_fold(const DsxTensorRef* __re
                                                         DsxState* state, DsxScalerConfig scfg, DsxGroupsDev grp,
                                                         DsxStepScalars* __restrict__ out) {
   constexpr int U = 2;
-  const int64_t slot_blocks = (int64_t)gridDim.x - 1;
-  if (blockIdx.x == slot_blocks) {
+  // The host launches nchunks + 1 blocks: one per chunk, then the writer (a
+  // larger grid's extra blocks would return here).
+  if ((int64_t)blockIdx.x > nchunks) return;
+  if ((int64_t)blockIdx.x == nchunks) {
     double x = 0.0;
     for (int i = threadIdx.x; i < nparts; i += kBlock) x += partials[i];  // reduce_partials' order
     const double sumsq = block_sum_all(x);
