@@ -24,7 +24,7 @@ DSX_MAX_PARTIALS = 8192
 DSX_MAX_GROUPS = 16
 DSX_NOALLOC_MAX_PARTIALS = 8192
 DSX_NOALLOC_SCRATCH_BYTES = 8 * DSX_NOALLOC_MAX_PARTIALS + 256
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c = ctypes
 _P = _c.c_void_p

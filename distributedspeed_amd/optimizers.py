@@ -122,10 +122,15 @@ class _FusedAdamWBase(torch.optim.Optimizer):
     # ---- skip flag on the host, without waiting for K2 ---------------------------------
 
     def track_skips(self, on: bool = True) -> None:
-        """After every K0, copy DsxState.last_skip into pinned host memory
-        and record an event, so that last_step_skipped() waits for K1 and K0
-        only (not for K2). Costs one small device-to-host copy per step in
-        stream order; off by default."""
+        """After every step's skip decision, copy DsxState.last_skip into
+        pinned host memory and record an event, so that last_step_skipped()
+        need not synchronise the whole device. In the eager forms the step
+        then runs as separate launches and the copy sits right after K0, so
+        the wait covers K1 and K0 only. In the capturable and graph forms the
+        step is one recorded sequence (with K0 folded into K2 where the fold
+        applies), so the copy follows the whole step and the wait covers K2
+        too. Costs one small device-to-host copy per step in stream order;
+        off by default."""
         if on and self._skip_host is None:
             self._skip_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
             self._skip_event = torch.cuda.Event()
@@ -139,7 +144,9 @@ class _FusedAdamWBase(torch.optim.Optimizer):
 
     def last_step_skipped(self) -> bool:
         """Whether the last step was skipped (overflow). With track_skips on
-        this waits only for that step's K0; otherwise it synchronises."""
+        this waits for the event track_skips records (after K0 in the eager
+        forms, after the whole step in the capturable and graph forms);
+        otherwise it synchronises."""
         if self._skip_host is not None and self._skip_event is not None and self.steps_issued:
             self._skip_event.synchronize()
             return bool(int(self._skip_host[0]))

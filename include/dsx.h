@@ -57,7 +57,10 @@
 extern "C" {
 #endif
 
-#define DSX_ABI_VERSION 1
+/* Version 2: DsxState's last 16 bytes (reserved in version 1) hold the
+ * one-shot clip and the step's entry values, which K0, K1 and the folded
+ * K2/K3 read. */
+#define DSX_ABI_VERSION 2
 
 /* element types */
 #define DSX_F32  0
@@ -88,7 +91,11 @@ extern "C" {
 #define DSX_NOALLOC_MAX_PARTIALS 8192
 #define DSX_NOALLOC_SCRATCH_BYTES (8 * DSX_NOALLOC_MAX_PARTIALS + 256)
 
-/* Device-resident optimizer + loss-scaler state (64 bytes). */
+/* Device-resident optimizer + loss-scaler state (64 bytes). Write it with
+ * dsx_state_init, or copy back one the library wrote (a checkpoint). A
+ * caller that fills one itself must zero clip_once_coef, clip_once,
+ * step_scale and step_t2: a nonzero clip_once arms a one-shot clip for the
+ * next finalize. */
 typedef struct DsxState {
   float   scale;          /* loss scale the next backward multiplies by      */
   int32_t good_steps;     /* clean steps since the last overflow or growth   */

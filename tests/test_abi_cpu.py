@@ -48,7 +48,7 @@ def test_struct_layouts_match_header(lib):
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.dsx_abi_version() == 1
+    assert lib.dsx_abi_version() == 2
     assert isinstance(lib.dsx_last_error(), bytes)
 
 
@@ -88,6 +88,44 @@ def test_chunk_table_extreme_sizes(lib):
     assert lib.dsx_count_chunks(many, 7, 8) == 7 * 2 ** 60
     assert lib.dsx_count_chunks(many, 8, 8) == -1
     assert b"overflows" in lib.dsx_last_error()
+
+
+def test_chunk_table_fuzz(lib):
+    """Random and extreme tensor sizes and chunk sizes through
+    dsx_count_chunks / dsx_build_chunks (host code only): a table is built
+    exactly when it is counted, covers every tensor once in chunks of at most
+    chunk_elems, and a buffer one entry short is refused. tests/sanitize runs
+    this under ASan/UBSan."""
+    import random
+    from distributedspeed_amd import _lib
+    rnd = random.Random(7)
+    I64 = ctypes.c_int64
+    for _ in range(3000):
+        nt = rnd.choice([0, 1, 2, 5, 17, 100])
+        if rnd.random() < 0.8:
+            nums = [rnd.choice([0, 1, 7, 8, 4095, 4096, 4097, 65536, rnd.randrange(0, 300000)]) for _ in range(nt)]
+        else:
+            nums = [rnd.choice([0, -1, 1, 2**40, 2**62, 2**63 - 1, -(2**63)]) for _ in range(nt)]
+        ce = rnd.choice([0, 7, 8, 9, 16, 2048, 4096, 65536, 2**40, 2**62, 2**63 - 8])
+        arr = (I64 * max(nt, 1))(*nums)
+        cnt = lib.dsx_count_chunks(arr, nt, I64(ce))
+        bad = ce < 8 or ce % 8 or any(x < 0 for x in nums)
+        if bad:
+            assert cnt == -1, (nums, ce)
+            continue
+        assert cnt == sum(-(-x // ce) for x in nums), (nums, ce)
+        if cnt > 20000:
+            continue
+        out = (_lib.DsxChunk * max(cnt + 1, 1))()
+        assert lib.dsx_build_chunks(arr, nt, I64(ce), out, I64(cnt + rnd.choice([0, 1]))) == cnt
+        tot = [0] * nt
+        for k in range(cnt):
+            c = out[k]
+            assert 0 <= c.tensor < nt and 0 < c.len <= ce and c.start == tot[c.tensor]
+            tot[c.tensor] += c.len
+        assert tot == nums
+        if cnt > 0:
+            assert lib.dsx_build_chunks(arr, nt, I64(ce), out, I64(cnt - 1)) == -1
 
 
 def test_argument_checks_reject_before_launch(lib):
