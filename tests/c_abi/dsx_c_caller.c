@@ -9,7 +9,9 @@
  * second copy of the buffers, dsx_zero_step_flat_noalloc.
  *
  * usage: dsx_c_caller <n> <dtype 1 (fp16, dynamic loss scale) | 2 (bf16)>
- *                     <steps> <outdir>
+ *                     <steps> <outdir> [fold_max_elems]
+ * fold_max_elems, when given, goes to dsx_set_tuning_fold first: 0 makes
+ * every one-call step run K1, K0 and K2 as three launches.
  * Writes to outdir: master0.f32 (the initial master), grads.u16 (the 16-bit
  * grads of every step, step after step), master.f32, exp_avg.f32,
  * exp_avg_sq.f32, param16.u16 (after the last step) and states.bin (the
@@ -118,8 +120,8 @@ static int same(const void* a, const void* b, size_t bytes, void* ha, void* hb) 
 }
 
 int main(int argc, char** argv) {
-  if (argc != 5) {
-    fprintf(stderr, "usage: %s n dtype steps outdir\n", argv[0]);
+  if (argc != 5 && argc != 6) {
+    fprintf(stderr, "usage: %s n dtype steps outdir [fold_max_elems]\n", argv[0]);
     return 1;
   }
   const int64_t n = atoll(argv[1]);
@@ -134,6 +136,7 @@ int main(int argc, char** argv) {
     fprintf(stderr, "ABI %d, header %d\n", dsx_abi_version(), DSX_ABI_VERSION);
     return 1;
   }
+  if (argc == 6) CHECK_DSX(dsx_set_tuning_fold((int64_t)atoll(argv[5])));
   CHECK_HIP(hipSetDevice(0));
   hipStream_t stream;
   CHECK_HIP(hipStreamCreate(&stream));

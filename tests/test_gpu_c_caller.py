@@ -7,10 +7,15 @@ double, one dsx_zero_step_flat per step on a stream it created, and the
 same steps through dsx_zero_step_flat_noalloc on a second copy. It writes
 its inputs and results; here they are compared with the oracle, step by
 step for the state and bit for bit for master, exp_avg, exp_avg_sq and
-param16 at the end: a partition the library steps in two launches (fp16,
-dynamic loss scale, configs[0]'s size) and one it steps in three (bf16,
-above the fold's 3 * 2^23 bound). Step 1 holds an inf (skipped, scale backed
-off); the window of 2 makes the scale grow."""
+param16 at the end, for each form dsx_zero_step_flat takes:
+- two launches, K1 and K2 with K0's finalize folded in (fp16, dynamic loss
+  scale, configs[0]'s size, below the fold's 3 * 2^23-element bound);
+- fold-first (bf16, above that bound: K1, then K0 folded into the first of
+  K2's parts, then the other parts);
+- three launches, K1 -> K0 -> K2 (the same bf16 partition with the fold
+  switched off through dsx_set_tuning_fold(0)).
+Step 1 holds an inf (skipped, scale backed off); the window of 2 makes the
+scale grow."""
 from __future__ import annotations
 
 import os
@@ -33,15 +38,16 @@ def _say(msg):
     print(f"[gpu-test] {msg}", file=sys.stderr, flush=True)
 
 
-@pytest.mark.parametrize("n,dt", [(1_863_690, F16), (26_000_003, BF16)], ids=["fp16-two-launch", "bf16-three-launch"])
-def test_c_program_matches_oracle(gpu, oracle, tmp_path, n, dt):
+@pytest.mark.parametrize("n,dt,fold", [(1_863_690, F16, None), (26_000_003, BF16, None), (26_000_003, BF16, 0)],
+                         ids=["fp16-two-launch", "bf16-fold-first", "bf16-three-launch"])
+def test_c_program_matches_oracle(gpu, oracle, tmp_path, n, dt, fold):
     from distributedspeed_amd import _lib
     O = oracle
     if not os.path.exists(EXE):
         pytest.fail(f"{EXE} is not built: run build() (make -C tests/c_abi)")
-    _say(f"C caller n={n} dt={dt}")
-    r = subprocess.run([EXE, str(n), str(dt), str(STEPS), str(tmp_path)], capture_output=True, text=True,
-                       timeout=240)
+    _say(f"C caller n={n} dt={dt} fold={fold}")
+    args = [EXE, str(n), str(dt), str(STEPS), str(tmp_path)] + ([] if fold is None else [str(fold)])
+    r = subprocess.run(args, capture_output=True, text=True, timeout=240)
     assert r.returncode == 0, f"status {r.returncode}: {r.stderr[-2000:]}"
     assert "noalloc identical" in r.stdout
 
