@@ -182,7 +182,9 @@ def _progress(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def make_inputs(n: int, seed: int, device):
+def master_and_grad(n: int, seed: int, device):
+    """configs[2]'s values: fp32 master N(0, 0.02^2) and bf16 grads
+    N(0, 5e-4^2), drawn chunk by chunk from one seeded generator on the GPU."""
     import torch
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
@@ -193,6 +195,12 @@ def make_inputs(n: int, seed: int, device):
         e = min(n, s + chunk)
         master[s:e].normal_(0.0, 0.02, generator=gen)
         grad[s:e].copy_(torch.empty(e - s, dtype=torch.float32, device=device).normal_(0.0, 5e-4, generator=gen))
+    return master, grad
+
+
+def make_inputs(n: int, seed: int, device):
+    import torch
+    master, grad = master_and_grad(n, seed, device)
     exp_avg = torch.zeros(n, dtype=torch.float32, device=device)
     exp_avg_sq = torch.zeros(n, dtype=torch.float32, device=device)
     p16 = master.to(torch.bfloat16)
@@ -275,7 +283,7 @@ def measure_dropin(dev, gpt2: bool, steps: int, warmup: int,
         s1.record()
         torch.cuda.synchronize()
         ms = s0.elapsed_time(s1) / steps
-        st = opt.read_state()
+        st = opt.read_state() if fn is not entry_points else ops.read_state(st3)
         out[name] = {"ms_per_step": round(ms, 4), "gparam_per_s": round(n / ms / 1e6, 3),
                      "host_issue_us_per_step": round(t_issue / steps * 1e6, 1),
                      "achieved_tbps": round(30 * n / ms / 1e9, 4), "state_error": st.error,
@@ -286,6 +294,98 @@ def measure_dropin(dev, gpt2: bool, steps: int, warmup: int,
     return {"workload": "gpt2-small fp16 (BASELINE configs[1])" if gpt2 else "mlp fp16 (BASELINE configs[0])",
             "storage": "f32 state / fp16 grads+params", "tensors": len(shapes), "numel": n, "steps": steps,
             "warmup": warmup, "modes": out}
+
+
+def measure_dropin_headline(dev, n: int, steps: int, warmup: int, headline_ms: float,
+                            fold_restore: int = 3 << 23) -> dict:
+    """configs[2] through the drop-in classes: the same shard (one parameter
+    of n elements, the headline's seed and values, bf16 params and grads,
+    no loss scale, lr 3e-4, betas (0.9, 0.95), eps 1e-8, wd 0.1, clip 1.0)
+    stepped by AdamWOptimizer.step() -- what the reference's stages call,
+    Src/zero/stage2.py:609-612 -- and then by ZeROOptimizer.step(), the
+    engine's step (Src/zero/optimizer.py:212-274), on the same optimizer.
+    Both issue one dsx_zero_step_plan call per step: K1, then K0's finalize
+    folded into the first of K2's parts, then the other parts (the headline
+    times the three bare entry points instead). Between them, on the same
+    buffers, AdamWOptimizer.step() with the fold switched off
+    (dsx_set_tuning_fold(0): K1, K0 and the 15 K2 parts as three entry
+    points, the headline's form), so that the path's cost is told apart
+    from where this run's allocations landed; the fold bound is then set
+    back to fold_restore. Last, the headline's own three entry points
+    (unscale_norm, finalize, adamw_flat, with their own state and records)
+    over the optimizer's flat buffers: the headline's calls on this run's
+    allocations. Events around `steps` steps after `warmup` on the stream
+    the kernels run on."""
+    import torch
+    from distributedspeed_amd import _lib, ops
+    from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
+    from distributedspeed_amd.optimizers import AdamWOptimizer
+    from distributedspeed_amd.zero import ZeROOptimizer
+    master, grad = master_and_grad(n, 2, dev)
+    p = torch.nn.Parameter(master)
+    del master
+    opt = AdamWOptimizer([p], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0,
+                         param_dtype=torch.bfloat16, loss_scaler=ScalerConfig(mode="none"), device=dev)
+    p.grad.copy_(grad)  # the parameter's view of the flat grad buffer
+    del grad
+    zo = ZeROOptimizer(opt, config={"stage": 2, "gradient_accumulation_steps": 1})
+    torch.cuda.synchronize()
+    out = {}
+
+    def fold(v):
+        _lib.call("dsx_set_tuning_fold", ctypes.c_int64(v))
+
+    f = opt.flat
+    hyper = AdamWHyper(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    hc, scc = hyper.to_c(), ScalerConfig(mode="none").to_c()
+    bc = BiasCorrectionTable(dev, hyper.beta1, hyper.beta2)
+    bc.ensure(2 * (warmup + steps))
+    st3, rec3 = ops.new_state(dev, 1.0, 1), ops.new_scalars(dev)
+    np3 = ops.suggest_partials(n)
+    parts3 = torch.zeros(np3, dtype=torch.float64, device=dev)
+    g3 = f.grad[:n]
+    bufs3 = (f.master[:n], f.exp_avg[:n], f.exp_avg_sq[:n], f.param16[:n])
+
+    def entry_points():
+        ops.unscale_norm(g3, st3, parts3, np3)
+        ops.finalize(parts3, np3, st3, scc, hc, bc.table, bc.length, rec3)
+        ops.adamw_flat(*bufs3, g3, rec3)
+
+    for name, fn, fold_to in (("AdamWOptimizer.step", opt.step, fold_restore),
+                              ("AdamWOptimizer.step, fold off (three launches)", opt.step, 0),
+                              ("ZeROOptimizer.step", zo.step, fold_restore),
+                              ("the headline's three entry points on these buffers", entry_points, fold_restore)):
+        fold(fold_to)
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        s0.record()
+        for _ in range(steps):
+            fn()
+        t_issue = time.perf_counter() - t0
+        s1.record()
+        torch.cuda.synchronize()
+        ms = s0.elapsed_time(s1) / steps
+        st = opt.read_state() if fn is not entry_points else ops.read_state(st3)
+        out[name] = {"ms_per_step": round(ms, 4), "gparam_per_s": round(n / ms / 1e6, 3),
+                     "pct_of_8tbps_end_to_end": round(100 * 30 * n / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                     "over_headline_ms": round(ms / headline_ms, 4),
+                     "host_issue_us_per_step": round(t_issue / steps * 1e6, 1),
+                     "state_error": st.error, "last_skip": st.last_skip}
+        _progress(f"configs[2] drop-in {name}: {out[name]}")
+    fold(fold_restore)
+    out["ZeROOptimizer.step"]["current_step"] = zo.current_step
+    del zo, opt, p, f, g3, bufs3, parts3
+    torch.cuda.empty_cache()
+    return {"workload": "llama3-8b zero2 one-rank shard (BASELINE configs[2]) through the drop-in classes",
+            "storage": "f32 state / bf16 grads+params", "numel": n, "steps": steps, "warmup": warmup,
+            "path": "dsx_zero_step_plan: " + ("K1, then K2 with K0's finalize folded into every block"
+                                               if n <= 3 << 23 else
+                                               f"K1, then K2 in {k2_parts(n, None)} parts with K0's finalize "
+                                               "folded into the first"),
+            "headline_ms_per_step": round(headline_ms, 4), "modes": out}
 
 
 def bench_dropin(a, dev) -> int:
@@ -565,10 +665,14 @@ def bench_ragged(a, dev) -> int:
 
 def link_ceiling(dev) -> dict:
     """Plain pinned-host <-> HBM copy bandwidth (offload.measure_link),
-    measured in a fresh child process: within a process that has already
-    allocated and freed large device buffers, the runtime can run the two
-    directions one at a time (the figure then halves), while a fresh
-    process gives the machine's ceiling. Falls back to this process."""
+    measured in a fresh child process (the only child bench.py starts;
+    subprocess.run waits for it to exit). Either process may see the two
+    directions run one at a time (the both-ways figure then halves): on
+    these boxes that has happened both in a process that had freed large
+    device buffers and in the fresh child. So measure_offload also measures
+    the link on the step's own streams (offload.measure_streamer_link) and
+    takes the larger both-ways figure as the ceiling. Falls back to this
+    process."""
     import subprocess
     root = os.path.dirname(os.path.abspath(__file__))
     code = ("import json, sys, torch; sys.path.insert(0, %r); from distributedspeed_amd.offload import measure_link; "
@@ -648,6 +752,14 @@ def measure_offload(dev, full: int, budget_gib: float, steps: int) -> dict:
         times.append(time.perf_counter() - t0)
         _progress(f"step {i + 1}: {times[-1]:.3f} s")
     s = ops.read_state(st)
+    # The link measured right after the timed steps, in this process, on the
+    # step's own copy streams and pinned buffers; the ceiling is the larger
+    # of this and the fresh process's figure.
+    _progress("measuring the host link on the step's own streams")
+    from distributedspeed_amd.offload import measure_streamer_link
+    link_here = measure_streamer_link(streamer, (master, m, v))
+    link_here["measured_in"] = "this process, the step's copy streams and pinned buffers, after the timed steps"
+    ceiling = max(link["both_each_way"], link_here["both_each_way"])
     sec = sorted(times)[len(times) // 2]
     each_way = 12 * n / sec / 1e9
     del grad, p16, master, m, v, streamer
@@ -657,8 +769,12 @@ def measure_offload(dev, full: int, budget_gib: float, steps: int) -> dict:
             "steps": steps, "warmup": 1, "ms_per_step": round(sec * 1e3, 1),
             "gparam_per_s": round(n / sec / 1e9, 4), "link_gbs_each_way": round(each_way, 2),
             "link_ceiling_gbs": {k: (round(x, 2) if isinstance(x, float) else x) for k, x in link.items()},
-            "frac_of_measured_bidirectional_link": round(each_way / link["both_each_way"], 4),
-            "frac_of_one_direction_link": round(each_way / min(link["h2d"], link["d2h"]), 4),
+            "link_ceiling_in_process_gbs": {k: (round(x, 2) if isinstance(x, float) else x)
+                                            for k, x in link_here.items()},
+            "bidirectional_ceiling_gbs": round(ceiling, 2),
+            "frac_of_measured_bidirectional_link": round(each_way / ceiling, 4),
+            "frac_of_one_direction_link": round(each_way / max(min(link["h2d"], link["d2h"]),
+                                                               min(link_here["h2d"], link_here["d2h"])), 4),
             "reduced_from_numel": full if n != full else None,
             "reduction_reason": (f"pinned budget {budget_gib} GiB: this machine caps GPU-visible pinned host "
                                  "memory (no single hipHostMalloc above 32 GiB, ~64 GiB in total); the full shard "
@@ -676,7 +792,8 @@ def bench_offload(a, dev) -> int:
         "value": r["gparam_per_s"], "unit": "Gparam/s", "n_gpus": 1, "steps": r["steps"], "warmup": 1,
         "ms_per_step": r["ms_per_step"], "higher_is_better": True, "dtype": "f32", "data": "synthetic",
         "config": {k: r[k] for k in ("workload", "storage", "numel", "chunk_elems")},
-        **{k: r[k] for k in ("link_gbs_each_way", "link_ceiling_gbs", "frac_of_measured_bidirectional_link",
+        **{k: r[k] for k in ("link_gbs_each_way", "link_ceiling_gbs", "link_ceiling_in_process_gbs",
+                             "bidirectional_ceiling_gbs", "frac_of_measured_bidirectional_link",
                              "frac_of_one_direction_link", "reduced_from_numel", "reduction_reason", "state_t")},
         "skipped": r["skipped"],
     }), flush=True)
@@ -764,7 +881,8 @@ def cpu_threads() -> tuple[int, str]:
     return len(os.sched_getaffinity(0)), "the CPUs in this process's affinity set"
 
 
-def cpu_baseline(master_h, grad_h, hyper, steps: int = 5, shard: int | None = None) -> dict | None:
+def cpu_baseline(master_h, grad_h, hyper, steps: int = 5, shard: int | None = None,
+                 gpu_norm: float | None = None) -> dict | None:
     """The reference's CPU route timed on this host's cores, on the same
     inputs as the GPU run (copied to host memory). The reference has no CPU
     Adam kernel: its cpu_offload route parks the state on the host and steps
@@ -778,7 +896,14 @@ def cpu_baseline(master_h, grad_h, hyper, steps: int = 5, shard: int | None = No
     master, then the bf16 cast of the result. 1 warm-up step, then the median
     of `steps`. Beside it: torch's fused CPU AdamW (the fastest CPU route
     torch has) and this repository's C oracle (a port of the whole step on
-    OpenMP threads)."""
+    OpenMP threads).
+
+    The norms: torch's CPU fp32 reductions (the reference's compute_norm
+    and torch.linalg.vector_norm alike) lose accuracy as the sample grows
+    (about 19% low over 1.0e9 bf16 values), so the record holds each norm
+    beside an fp64 one (the oracle's compensated block sums) with its
+    relative error, and the GPU step's norm (gpu_norm: the step's
+    DsxStepScalars.norm over the same values) with its error too."""
     if master_h is None:
         return None
     import numpy as np
@@ -812,9 +937,19 @@ def cpu_baseline(master_h, grad_h, hyper, steps: int = 5, shard: int | None = No
         del opt, param, p16
         return sorted(times[1:])[len(times[1:]) // 2], norm, len(times) - 1
 
+    g16 = grad_h.view(torch.int16).numpy().view(np.uint16)
+    _progress("cpu baseline: the fp64 norm")
+    norm64 = O.sumsq_parallel(g16, O.BF16, 1.0, 1024) ** 0.5
+
     _progress(f"cpu baseline: torch.optim.AdamW(foreach=False) on {ns} elements, {threads} threads")
     t_ref, norm_ref, n_ref = torch_route(steps, foreach=False)
     norm_vec = float(torch.linalg.vector_norm(grad_h.float()).item())
+
+    def rel(x):
+        return None if x is None or not norm64 else abs(x - norm64) / norm64
+
+    def clip_of(x):
+        return mx / (x + 1e-6) if x is not None and mx > 0 and x > mx else 1.0
     _progress("cpu baseline: torch.optim.AdamW(fused=True)")
     t_fused, _, n_fused = torch_route(max(2, steps // 2), fused=True)
 
@@ -823,7 +958,6 @@ def cpu_baseline(master_h, grad_h, hyper, steps: int = 5, shard: int | None = No
     m = np.zeros(ns, np.float32)
     v = np.zeros(ns, np.float32)
     p16 = np.empty(ns, np.uint16)
-    g16 = grad_h.view(torch.int16).numpy().view(np.uint16)
     h = O.Hyper(lr=hyper.lr, beta1=hyper.beta1, beta2=hyper.beta2, eps=hyper.eps,
                 weight_decay=hyper.weight_decay, max_grad_norm=mx)
     times = []
@@ -850,8 +984,23 @@ def cpu_baseline(master_h, grad_h, hyper, steps: int = 5, shard: int | None = No
         "ms_per_step": round(t_ref * 1e3, 1),
         "threads": {"used": torch.get_num_threads(), "why": why},
         "host": host_info(),
-        "norm": {"reference_style": norm_ref, "torch_linalg_vector_norm": norm_vec,
-                 "rel_diff": abs(norm_ref - norm_vec) / norm_vec if norm_vec else 0.0},
+        "norm": {
+            "fp64": {"value": norm64, "what": "sqrt of the fp64 sum of squares (the oracle's 1024 compensated "
+                                              "block sums, added in block order)"},
+            "gpu_step": {"value": gpu_norm, "rel_err_vs_fp64": rel(gpu_norm),
+                         "what": "the GPU step's norm over the same values (DsxStepScalars.norm: K1's fp64 "
+                                 "partials reduced by the finalize)"},
+            "reference_style": {"value": norm_ref, "rel_err_vs_fp64": rel(norm_ref),
+                                "what": "the reference's compute_norm on the CPU: t.norm(dtype=float32).item() "
+                                        "** 2, then ** 0.5 (Src/zero/utils.py:146-154), torch's fp32 reduction"},
+            "torch_linalg_vector_norm": {"value": norm_vec, "rel_err_vs_fp64": rel(norm_vec),
+                                         "what": "torch.linalg.vector_norm on the CPU fp32 grads"},
+            "clip_coef": {"reference_cpu_route": clip_of(norm_ref), "from_fp64_norm": clip_of(norm64),
+                          "gpu_step": clip_of(gpu_norm) if gpu_norm is not None else None},
+            "note": "the timed reference CPU route clips by max_norm / (its own norm + 1e-6); torch's CPU fp32 "
+                    "reduction undercounts large samples, so that coefficient differs from the fp64 one by the "
+                    "norm's relative error; the GPU step's norm is held to 1e-6 of fp64",
+        },
         "torch_adamw_cpu_fused": {"value": round(ns / t_fused / 1e9, 4), "unit": "Gparam/s",
                                   "ms_per_step": round(t_fused * 1e3, 1), "steps": n_fused,
                                   "what": "torch.optim.AdamW(fused=True) on CPU, same sample and step"},
@@ -960,6 +1109,21 @@ def main() -> int:
         print(json.dumps({"error": f"step state error={st.error} skip={scal.skip}"}))
         return 1
 
+    # The GPU step's norm over the CPU baseline's sample: the step's own
+    # record when the sample is the whole shard (every timed step saw the
+    # same grads), else K1 over the sample's grads, its fp64 partials summed
+    # here.
+    gpu_norm = None
+    if ns == n:
+        gpu_norm = float(scal.norm)
+    elif ns > 0:
+        import math
+        np_s = ops.suggest_partials(ns)
+        ps = torch.zeros(np_s, dtype=torch.float64, device=dev)
+        ops.unscale_norm(grad[:ns], fs.state, ps, np_s)
+        gpu_norm = math.sqrt(math.fsum(ps.cpu().tolist()))
+        del ps
+
     gparams = n / (ms_step * 1e-3) / 1e9
     e2e_gbs = (K1_BYTES + K2_BYTES) * n / (ms_step * 1e-3) / 1e9
     k2_gbs = K2_BYTES * n / (k2_ms * 1e-3) / 1e9
@@ -1010,6 +1174,8 @@ def main() -> int:
     if a.secondary:
         del master, exp_avg, exp_avg_sq, p16, grad, fs
         torch.cuda.empty_cache()
+        run_secondary("configs[2]", lambda: measure_dropin_headline(
+            dev, n, a.steps, a.warmup, ms_step, 3 << 23 if a.fold is None else a.fold))
         run_secondary("configs[0]", lambda: measure_dropin(dev, False, max(a.steps, 200), max(a.warmup, 20),
                                                            modes=("flat_eager",)))
         run_secondary("configs[1]", lambda: measure_dropin(dev, True, a.steps, a.warmup, modes=("flat_eager",)))
@@ -1017,7 +1183,7 @@ def main() -> int:
         secondary = {k: secondary[k] for k in sorted(secondary)}
     else:
         secondary = None
-    cpu = cpu_baseline(*cpu_in, hyper, a.cpu_steps, shard=n)
+    cpu = cpu_baseline(*cpu_in, hyper, a.cpu_steps, shard=n, gpu_norm=gpu_norm)
 
     out = {
         "metric": "AdamW step Gparam/s + achieved HBM TB/s (% of 8 TB/s), 1.0B-elt bf16 shard",

@@ -103,9 +103,13 @@ class HostStateStreamer:
         self.last_seconds = 0.0
 
     def run(self, host_state: tuple[torch.Tensor, torch.Tensor, torch.Tensor], param16: torch.Tensor | None,
-            grad: torch.Tensor, pieces: list[tuple[int, int, torch.Tensor]]) -> None:
+            grad: torch.Tensor | None, pieces: list[tuple[int, int, torch.Tensor | None]], *,
+            copy_only: bool = False) -> None:
         """pieces: (start, end, scalars) ranges of the flat partition, each
-        with the DsxStepScalars (device uint8[64]) of its parameter group."""
+        with the DsxStepScalars (device uint8[64]) of its parameter group.
+        copy_only (measurement only): the same copies, streams and events
+        with the AdamW launch left out, so every chunk goes back unchanged;
+        param16, grad and the scalars are then unused."""
         compute = torch.cuda.current_stream(self.device)
         # Everything earlier on the compute stream (K0, the previous step's
         # K2s) and every earlier copy out is ordered before this step's copies.
@@ -126,7 +130,9 @@ class HostStateStreamer:
                         dst.copy_(src[s:e], non_blocking=True)
                     self.ev_in[slot].record(self.s_in)
                 compute.wait_event(self.ev_in[slot])
-                ops.adamw_flat(st[0], st[1], st[2], param16[s:e] if param16 is not None else None, grad[s:e], scal)
+                if not copy_only:
+                    ops.adamw_flat(st[0], st[1], st[2], param16[s:e] if param16 is not None else None, grad[s:e],
+                                   scal)
                 self.ev_done[slot].record(compute)
                 with torch.cuda.stream(self.s_out):
                     self.s_out.wait_event(self.ev_done[slot])
@@ -176,4 +182,68 @@ def measure_link(device: torch.device, nbytes: int = 1 << 30) -> dict:
                 h2.copy_(d2, non_blocking=True)
         torch.cuda.synchronize()
     out["both_each_way"] = reps * nbytes / (time.perf_counter() - t0) / 1e9
+    return out
+
+
+def measure_streamer_link(streamer: HostStateStreamer, host_state: tuple, reps: int = 4, trials: int = 3,
+                          pipeline_passes: int = 2) -> dict:
+    """The host link as the streamed step sees it, on the streamer's own
+    copy-in and copy-out streams, staging buffers and the pinned state
+    arrays:
+      h2d, d2h        one direction alone (three arrays of one chunk per
+                      repetition), best of `trials`;
+      pairs_each_way  both at once, the same copies, best of `trials`;
+      copy_pipeline_each_way  the step's whole copy schedule over every
+                      chunk of the state with the AdamW launch left out
+                      (run(copy_only=True)), best of `pipeline_passes`;
+      both_each_way   the larger of the two both-ways figures.
+    Every copy out writes back the values a copy in read (staging slot 0 is
+    first loaded from the arrays' first chunk), so the state is unchanged.
+    Needs at least two chunks of state."""
+    c = streamer.chunk
+    if min(t.numel() for t in host_state) < 2 * c:
+        raise ValueError("measure_streamer_link needs at least two chunks of state")
+    a_slot, b_slot = streamer.stage[0], streamer.stage[1]
+    s_in, s_out = streamer.s_in, streamer.s_out
+    for d, h in zip(a_slot, host_state):
+        d.copy_(h[:c])
+    torch.cuda.synchronize(streamer.device)
+
+    def copy_in():
+        with torch.cuda.stream(s_in):
+            for d, h in zip(b_slot, host_state):
+                d.copy_(h[c:2 * c], non_blocking=True)
+
+    def copy_out():
+        with torch.cuda.stream(s_out):
+            for d, h in zip(a_slot, host_state):
+                h[:c].copy_(d, non_blocking=True)
+
+    def timed(fns) -> float:
+        best = 0.0
+        for _ in range(trials):
+            torch.cuda.synchronize(streamer.device)
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                for fn in fns:
+                    fn()
+            torch.cuda.synchronize(streamer.device)
+            best = max(best, reps * 12 * c / (time.perf_counter() - t0) / 1e9)
+        return best
+
+    copy_in()
+    copy_out()
+    out = {"h2d": timed([copy_in]), "d2h": timed([copy_out]), "pairs_each_way": timed([copy_in, copy_out]),
+           "bytes_each_way_per_rep": 12 * c}
+    n = min(t.numel() for t in host_state)
+    best = 0.0
+    for _ in range(max(1, pipeline_passes)):
+        torch.cuda.synchronize(streamer.device)
+        t0 = time.perf_counter()
+        streamer.run(tuple(host_state), None, None, [(0, n, None)], copy_only=True)
+        torch.cuda.synchronize(streamer.device)
+        best = max(best, 12 * n / (time.perf_counter() - t0) / 1e9)
+    out["copy_pipeline_each_way"] = best
+    out["copy_pipeline_bytes_each_way"] = 12 * n
+    out["both_each_way"] = max(out["pairs_each_way"], best)
     return out

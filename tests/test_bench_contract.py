@@ -45,7 +45,11 @@ def test_bench_line_contract(gpu):
     assert cb["kind"] == "reference" and cb["cores"] >= 1 and cb["value"] > 0 and cb["sample"]
     assert cb["threads"]["used"] == cb["cores"] and cb["host"]["os_cpu_count"] >= 1
     assert cb["port"]["value"] > 0 and cb["torch_adamw_cpu_fused"]["value"] > 0
-    assert cb["norm"]["rel_diff"] < 1e-5
+    nm = cb["norm"]
+    # the GPU step's norm against the fp64 one, at the north star's 1e-6
+    assert nm["gpu_step"]["value"] > 0 and nm["gpu_step"]["rel_err_vs_fp64"] <= 1e-6, nm
+    for k in ("reference_style", "torch_linalg_vector_norm"):
+        assert nm[k]["rel_err_vs_fp64"] == abs(nm[k]["value"] - nm["fp64"]["value"]) / nm["fp64"]["value"], k
     assert d["secondary_configs"] is None
     assert d["torch_gpu_reference_path"]["foreach_ms_per_step"] > 0
     tp = d["k2_traffic_probe"]
@@ -79,3 +83,28 @@ def test_secondary_workloads_print_one_line(gpu, workload):
     d = json.loads(lines[0])
     assert d["metric"] and d["unit"] and d["value"] > 0, d
     assert isinstance(d["config"], dict) and d["config"], d
+
+
+@pytest.mark.gpu
+def test_dropin_headline_measurement(gpu):
+    """The headline line's secondary_configs["configs[2]"] entry: the
+    drop-in AdamWOptimizer.step() and ZeROOptimizer.step() on one shard (here
+    2^25 + 5 elements: above the fold bound, so the fold-first form), every
+    step clean (also with the fold switched off), and ZeROOptimizer's
+    current_step counting every form's steps."""
+    sys.path.insert(0, ROOT)
+    import bench
+    n = (1 << 25) + 5
+    print(f"[gpu-test] measure_dropin_headline n={n}", file=sys.stderr, flush=True)
+    r = bench.measure_dropin_headline(gpu, n, 3, 1, 1.0)
+    assert r["numel"] == n and "folded into the first" in r["path"]
+    assert set(r["modes"]) == {"AdamWOptimizer.step", "AdamWOptimizer.step, fold off (three launches)",
+                               "ZeROOptimizer.step", "the headline's three entry points on these buffers"}
+    for k, m in r["modes"].items():
+        assert m["ms_per_step"] > 0 and m["state_error"] == 0 and m["last_skip"] == 0, m
+        assert m["over_headline_ms"] > 0
+    assert r["modes"]["ZeROOptimizer.step"]["current_step"] == 12
+    # whatever happened above, the tests after this one (same process) see
+    # the library's default fold bound
+    from distributedspeed_amd import _lib
+    assert _lib.load().dsx_set_tuning_fold(3 << 23) == 0
