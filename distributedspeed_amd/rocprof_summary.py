@@ -100,11 +100,24 @@ def parts_per_call(numel: int, part_elems: int) -> int:
     return -(-numel // part_elems) if part_elems > 0 and numel > part_elems else 1
 
 
+def call_spans(trace_dir: str, kernel: str, parts: int) -> list[int]:
+    """Per call of a parted kernel, in ns: from its first dispatch's start to
+    its last dispatch's end in the kernel trace, gaps between the dispatches
+    included (what events recorded around the call measure). The kernel's
+    dispatches are taken in time order, `parts` to a call."""
+    rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+                  for r in csv.DictReader(open(_csv(trace_dir, "kernel_trace.csv")))
+                  if _short(r["Kernel_Name"]) == kernel)
+    return [rows[i + parts - 1][1] - rows[i][0] for i in range(0, len(rows) - parts + 1, parts)]
+
+
 def summarise(trace_dir, fetch_dir, write_dir, numel, part_elems: int = 1 << 26,
-              kernel_numel: dict | None = None) -> dict:
+              kernel_numel: dict | None = None, timed_calls: int = 0) -> dict:
     """kernel_numel: elements one call of a kernel covers where that is not
     `numel` (a ragged list whose large tensors step through K2 and the rest
-    through K3)."""
+    through K3). timed_calls: for the parted kernels, the mean span is also
+    taken over the last this many calls (a benchmark's timed calls, after
+    its warm-up)."""
     kernel_numel = kernel_numel or {}
     stats = kernel_stats(trace_dir)
     fetch = counter_per_dispatch(fetch_dir)
@@ -137,6 +150,14 @@ def summarise(trace_dir, fetch_dir, write_dir, numel, part_elems: int = 1 << 26,
         if "avg_ms" in d and per_elt:
             d["achieved_gbs"] = per_elt * kn / (d["avg_ms"] * 1e-3) / 1e9
             d["frac_of_8tbs"] = d["achieved_gbs"] / 8000.0
+        if k in PARTED and k in stats and per_elt:
+            spans = call_spans(trace_dir, k, parts)
+            if spans:
+                tail = spans[-timed_calls:] if 0 < timed_calls <= len(spans) else spans
+                d["span_calls"] = len(tail)
+                d["span_ms"] = sum(tail) / len(tail) / 1e6
+                d["span_achieved_gbs"] = per_elt * kn / (d["span_ms"] * 1e-3) / 1e9
+                d["span_frac_of_8tbs"] = d["span_achieved_gbs"] / 8000.0
         res["kernels"][k] = d
     k2 = res["kernels"].get("k2_adamw_flat", {})
     res["k2_hbm_bytes_per_launch"] = k2.get("hbm_bytes")
@@ -224,6 +245,25 @@ def markdown(res: dict, command: str, title: str, intro: str = "") -> str:
             f"{d['fetch_bytes'] / 1e9:.3f}" if "fetch_bytes" in d else "",
             f"{d['write_bytes'] / 1e9:.3f}" if "write_bytes" in d else "",
             f"{d['traffic_over_algorithmic']:.4f}" if "traffic_over_algorithmic" in d else ""))
+    spans = [(k, d) for k, d in res["kernels"].items() if "span_ms" in d]
+    if spans:
+        lines += ["", "The same calls timed as a benchmark's events time them: per call, from the first dispatch's "
+                  "start to the last dispatch's end, gaps included (the mean over the last `calls` calls).", "",
+                  "| kernel | calls | span ms | achieved GB/s | frac of 8 TB/s |", "|---|---|---|---|---|"]
+        for k, d in spans:
+            lines.append(f"| {k} | {d['span_calls']} | {d['span_ms']:.4f} | {d['span_achieved_gbs']:.0f} | "
+                         f"{d['span_frac_of_8tbs']:.4f} |")
+    b = res.get("bench_line")
+    if b:
+        rf = b.get("roofline", {})
+        lines += ["", "The traced run's own bench line (events on the kernels' stream, same process):", "",
+                  "| ms / step | % of 8 TB/s end to end | K1 ms | K0 ms | K2 ms | roofline.achieved GB/s | "
+                  "roofline.frac |", "|---|---|---|---|---|---|---|",
+                  "| {} | {} | {} | {} | {} | {} | {} |".format(
+                      b.get("ms_per_step"), b.get("pct_of_8tbps_end_to_end"),
+                      *(b.get("kernels_ms", {}).get(k) for k in ("k1_unscale_norm", "k0_finalize",
+                                                                "k2_adamw_flat")),
+                      rf.get("achieved"), rf.get("frac"))]
     return "\n".join(lines) + "\n"
 
 
@@ -244,6 +284,9 @@ def main() -> None:
     ap.add_argument("--intro", default="", help="a paragraph placed under the title")
     ap.add_argument("--kernel-numel", action="append", default=[],
                     help="KERNEL=N: elements one call of KERNEL covers, where it is not --numel")
+    ap.add_argument("--timed-calls", type=int, default=0,
+                    help="take the parted kernels' mean span over the last this many calls")
+    ap.add_argument("--bench-json", help="the traced run's bench.py output: its JSON line goes into the summary")
     a = ap.parse_args()
     if a.chains:
         res = step_chains(a.trace)
@@ -256,7 +299,13 @@ def main() -> None:
     if not (a.fetch and a.write and a.numel):
         ap.error("--fetch, --write and --numel are required without --chains")
     kn = {k: int(v) for k, v in (x.split("=", 1) for x in a.kernel_numel)}
-    res = summarise(a.trace, a.fetch, a.write, a.numel, a.part_elems, kn)
+    res = summarise(a.trace, a.fetch, a.write, a.numel, a.part_elems, kn, a.timed_calls)
+    if a.bench_json:
+        lines = [x for x in open(a.bench_json).read().splitlines() if x.startswith("{")]
+        if lines:
+            b = json.loads(lines[-1])
+            res["bench_line"] = {k: b.get(k) for k in ("ms_per_step", "pct_of_8tbps_end_to_end", "kernels_ms",
+                                                       "roofline", "k2_traffic_probe")}
     with open(a.out_json, "w") as f:
         json.dump(res, f, indent=1)
     with open(a.out_md, "w") as f:

@@ -380,6 +380,30 @@ def test_k2_parts_per_call_follow_the_library_rule():
 
 
 
+def test_rocprof_call_spans_include_the_gaps_between_parts(tmp_path):
+    """call_spans (the summary's events-like figure for a parted kernel)
+    takes each call as `parts` consecutive dispatches of that kernel and
+    measures from the first start to the last end, gaps included; other
+    kernels in between do not count."""
+    import csv
+    from distributedspeed_amd.rocprof_summary import call_spans
+    k2 = "void (anonymous namespace)::k2_adamw_flat<2, 2, 2, true, false>(float*)"
+    k1 = "void (anonymous namespace)::k1_unscale_norm<2, 4, true>(void const*, long)"
+    rows, t = [], 0
+    for call in range(3):
+        rows.append({"Start_Timestamp": t, "End_Timestamp": t + 50, "Kernel_Name": k1})
+        t += 60
+        for part in range(3):  # 100 ns each, 7 ns gaps
+            rows.append({"Start_Timestamp": t, "End_Timestamp": t + 100, "Kernel_Name": k2})
+            t += 107
+    with open(tmp_path / "t_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Start_Timestamp", "End_Timestamp", "Kernel_Name"])
+        w.writeheader()
+        w.writerows(rows[::-1])  # the trace need not be in time order
+    assert call_spans(str(tmp_path), "k2_adamw_flat", 3) == [314, 314, 314]
+    assert call_spans(str(tmp_path), "k2_adamw_flat", 1) == [100] * 9
+
+
 def test_rocprof_step_chains_count_the_parts_after_a_folded_first_part(tmp_path):
     """The kernel-trace summary (rocprof_summary --chains) groups a step's
     launches by form: K1 then the folded K2 and the plain K2 parts after it
