@@ -283,7 +283,7 @@ def measure_dropin(dev, gpt2: bool, steps: int, warmup: int,
         s1.record()
         torch.cuda.synchronize()
         ms = s0.elapsed_time(s1) / steps
-        st = opt.read_state() if fn is not entry_points else ops.read_state(st3)
+        st = opt.read_state()
         out[name] = {"ms_per_step": round(ms, 4), "gparam_per_s": round(n / ms / 1e6, 3),
                      "host_issue_us_per_step": round(t_issue / steps * 1e6, 1),
                      "achieved_tbps": round(30 * n / ms / 1e9, 4), "state_error": st.error,

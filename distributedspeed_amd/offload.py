@@ -196,7 +196,12 @@ def measure_streamer_link(streamer: HostStateStreamer, host_state: tuple, reps: 
       copy_pipeline_each_way  the step's whole copy schedule over every
                       chunk of the state with the AdamW launch left out
                       (run(copy_only=True)), best of `pipeline_passes`;
-      both_each_way   the larger of the two both-ways figures.
+      sweep_each_way  both directions free-running, no dependency between
+                      them, a step's bytes each way: copies in of every
+                      chunk of the state (its own host addresses) into
+                      staging slots 1 and 2, while copies out of slot 0 write
+                      the first chunk back; best of `pipeline_passes`;
+      both_each_way   the largest of the three both-ways figures.
     Every copy out writes back the values a copy in read (staging slot 0 is
     first loaded from the arrays' first chunk), so the state is unchanged.
     Needs at least two chunks of state."""
@@ -245,5 +250,32 @@ def measure_streamer_link(streamer: HostStateStreamer, host_state: tuple, reps: 
         best = max(best, 12 * n / (time.perf_counter() - t0) / 1e9)
     out["copy_pipeline_each_way"] = best
     out["copy_pipeline_bytes_each_way"] = 12 * n
-    out["both_each_way"] = max(out["pairs_each_way"], best)
+    nch = -(-n // c)
+    slots = (streamer.stage[1], streamer.stage[2 % streamer.nbuf])
+
+    def sweep():
+        with torch.cuda.stream(s_in):
+            for k in range(nch):
+                s0, e0 = k * c, min(n, (k + 1) * c)
+                for d, h in zip(slots[k % 2], host_state):
+                    d[:e0 - s0].copy_(h[s0:e0], non_blocking=True)
+        with torch.cuda.stream(s_out):
+            for k in range(nch):
+                e0 = min(n, (k + 1) * c) - k * c
+                for d, h in zip(a_slot, host_state):
+                    h[:e0].copy_(d[:e0], non_blocking=True)
+
+    # the pipeline passed every chunk through the staging slots: slot 0 gets
+    # the first chunk again, which the sweep's copies out write back
+    for d, h in zip(a_slot, host_state):
+        d.copy_(h[:c])
+    best = 0.0
+    for _ in range(max(1, pipeline_passes)):
+        torch.cuda.synchronize(streamer.device)
+        t0 = time.perf_counter()
+        sweep()
+        torch.cuda.synchronize(streamer.device)
+        best = max(best, 12 * n / (time.perf_counter() - t0) / 1e9)
+    out["sweep_each_way"] = best
+    out["both_each_way"] = max(out["pairs_each_way"], out["copy_pipeline_each_way"], best)
     return out

@@ -145,9 +145,9 @@ def test_streamer_link_probe_leaves_the_state_unchanged(gpu):
         h.copy_(torch.randn(h.numel(), generator=gen))
     before = [h.clone() for h in host]
     r = measure_streamer_link(st, tuple(host), reps=2, trials=2)
-    for k in ("h2d", "d2h", "pairs_each_way", "copy_pipeline_each_way"):
+    for k in ("h2d", "d2h", "pairs_each_way", "copy_pipeline_each_way", "sweep_each_way"):
         assert r[k] > 0, r
-    assert r["both_each_way"] == max(r["pairs_each_way"], r["copy_pipeline_each_way"])
+    assert r["both_each_way"] == max(r["pairs_each_way"], r["copy_pipeline_each_way"], r["sweep_each_way"])
     assert r["copy_pipeline_bytes_each_way"] == 12 * host[0].numel()
     assert r["bytes_each_way_per_rep"] == 12 * chunk
     for h, b in zip(host, before):
