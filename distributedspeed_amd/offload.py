@@ -199,8 +199,9 @@ def measure_streamer_link(streamer: HostStateStreamer, host_state: tuple, reps: 
       sweep_each_way  both directions free-running, no dependency between
                       them, a step's bytes each way: copies in of every
                       chunk of the state (its own host addresses) into
-                      staging slots 1 and 2, while copies out of slot 0 write
-                      the first chunk back; best of `pipeline_passes`;
+                      staging slots 1 and 2 (slot 1 alone with two slots),
+                      while copies out of slot 0 write the first chunk back;
+                      best of `pipeline_passes`;
       both_each_way   the largest of the three both-ways figures.
     Every copy out writes back the values a copy in read (staging slot 0 is
     first loaded from the arrays' first chunk), so the state is unchanged.
@@ -251,7 +252,9 @@ def measure_streamer_link(streamer: HostStateStreamer, host_state: tuple, reps: 
     out["copy_pipeline_each_way"] = best
     out["copy_pipeline_bytes_each_way"] = 12 * n
     nch = -(-n // c)
-    slots = (streamer.stage[1], streamer.stage[2 % streamer.nbuf])
+    # copies in never land in slot 0, which the copies out read (with two
+    # slots they all go to slot 1)
+    slots = (streamer.stage[1], streamer.stage[2 if streamer.nbuf > 2 else 1])
 
     def sweep():
         with torch.cuda.stream(s_in):

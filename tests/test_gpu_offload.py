@@ -130,27 +130,29 @@ def test_config4_offloaded_shard_matches_oracle_and_in_hbm(gpu, oracle):
 def test_streamer_link_probe_leaves_the_state_unchanged(gpu):
     """measure_streamer_link (the offload line's in-process link ceiling)
     copies between the streamer's own staging buffers and the pinned state on
-    its own streams, pairwise and as the step's copy schedule without the
-    kernel (a ragged last chunk here); its copies out write back what its
-    copies in read, so the state is bit-identical afterwards, and every
-    figure is a rate."""
+    its own streams: pairwise, as the step's copy schedule without the
+    kernel, and free-running both ways (a ragged last chunk here; three
+    staging slots, and two, where the free-running copies in share slot 1).
+    Its copies out write back what its copies in read, so the state is
+    bit-identical afterwards, and every figure is a rate."""
     import torch
     from distributedspeed_amd.offload import HostStateStreamer, measure_streamer_link, pinned_empty
     chunk = 1 << 20
-    _say(f"streamer link probe chunk={chunk}")
-    st = HostStateStreamer(gpu, chunk)
     gen = torch.Generator().manual_seed(7)
-    host = [pinned_empty(2 * chunk + 40) for _ in range(3)]
+    host = [pinned_empty(3 * chunk + 40) for _ in range(3)]
     for h in host:
         h.copy_(torch.randn(h.numel(), generator=gen))
     before = [h.clone() for h in host]
-    r = measure_streamer_link(st, tuple(host), reps=2, trials=2)
-    for k in ("h2d", "d2h", "pairs_each_way", "copy_pipeline_each_way", "sweep_each_way"):
-        assert r[k] > 0, r
-    assert r["both_each_way"] == max(r["pairs_each_way"], r["copy_pipeline_each_way"], r["sweep_each_way"])
-    assert r["copy_pipeline_bytes_each_way"] == 12 * host[0].numel()
-    assert r["bytes_each_way_per_rep"] == 12 * chunk
-    for h, b in zip(host, before):
-        assert torch.equal(h.view(torch.int32), b.view(torch.int32))
+    for nbuf in (3, 2):
+        _say(f"streamer link probe chunk={chunk} nbuf={nbuf}")
+        st = HostStateStreamer(gpu, chunk, nbuf)
+        r = measure_streamer_link(st, tuple(host), reps=2, trials=2)
+        for k in ("h2d", "d2h", "pairs_each_way", "copy_pipeline_each_way", "sweep_each_way"):
+            assert r[k] > 0, r
+        assert r["both_each_way"] == max(r["pairs_each_way"], r["copy_pipeline_each_way"], r["sweep_each_way"])
+        assert r["copy_pipeline_bytes_each_way"] == 12 * host[0].numel()
+        assert r["bytes_each_way_per_rep"] == 12 * chunk
+        for h, b in zip(host, before):
+            assert torch.equal(h.view(torch.int32), b.view(torch.int32)), nbuf
     with pytest.raises(ValueError):
         measure_streamer_link(st, tuple(h[:chunk] for h in host))
