@@ -181,7 +181,14 @@ class DistributedSpeedEngine(torch.nn.Module):
         with open(os.path.join(path, "layout.json")) as f:
             layout = json.load(f)
         mine = self.optimizer.base_optimizer.layout()
-        if [(p["name"], p["numel"]) for p in layout["params"]] != [(p["name"], p["numel"]) for p in mine]:
+        # Names, shapes and group indices (not offsets: a checkpoint moves
+        # between storage forms) are checked before anything is loaded, so
+        # that a refused checkpoint leaves the engine as it was.
+        def key(p, shape=True):
+            return (p["name"], int(p["numel"]), tuple(p["shape"]) if shape else None, int(p.get("group", 0)))
+
+        shaped = all("shape" in p for p in layout["params"])  # every layout this library writes has shapes
+        if [key(p, shaped) for p in layout["params"]] != [key(p, shaped) for p in mine]:
             raise ValueError("checkpoint parameter layout does not match this model")
         ms = torch.load(os.path.join(path, "model_states.pt"), weights_only=True)
         osd = torch.load(os.path.join(path, "optim_states.pt"), weights_only=True)

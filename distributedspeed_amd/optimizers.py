@@ -393,6 +393,11 @@ class _FusedAdamWBase(torch.optim.Optimizer):
                         "layout": self.store.layout(), "scaler": dict(vars(self.scaler))}}
 
     def load_state_dict(self, state_dict: dict) -> None:
+        """Loads this optimizer's state dict or torch AdamW's (the
+        reference's, Src/zero/optimizer.py:356-404). Every check runs before
+        anything changes: a refused state dict (ValueError: another group
+        count or group size, a state tensor of another shape) leaves the
+        optimizer as it was."""
         if getattr(self, "streamer", None) is not None:
             torch.cuda.synchronize(self.device)  # no copy of an earlier step may still write the host state
         groups = state_dict["param_groups"]
@@ -402,11 +407,32 @@ class _FusedAdamWBase(torch.optim.Optimizer):
             if len(g["params"]) != len(sg["params"]):
                 raise ValueError("loaded state dict contains a parameter group that doesn't match the size "
                                  "of optimizer's group")
+        st = state_dict["state"]
+        ix = self._state_index
+        for i in range(len(self.store.params)):
+            if ix[i] not in st:
+                continue
+            views = self.store.views_of(i)
+            for key in ("exp_avg", "exp_avg_sq", "master"):
+                if key in st[ix[i]] and tuple(st[ix[i]][key].shape) != tuple(views[key].shape):
+                    raise ValueError(f"state for parameter {ix[i]} has shape {tuple(st[ix[i]][key].shape)}, "
+                                     f"expected {tuple(views[key].shape)}")
+        dsx = state_dict.get("dsx")
+        t = int(dsx["t"]) if dsx else int(max((float(v["step"]) for v in st.values()), default=0))
+        from ._lib import DsxState
+        hs = DsxState()
+        hs.scale = float(dsx["scale"]) if dsx else (self.scaler.init_scale if self.scaler.mode != "none" else 1.0)
+        hs.good_steps = int(dsx["good_steps"]) if dsx else 0
+        hs.hyst_left = int(dsx["hyst_left"]) if dsx else max(1, self.scaler.hysteresis)
+        hs.t = t
+        hs.iter = int(dsx["iter"]) if dsx else t
+        hs.overflow_count = int(dsx["overflow_count"]) if dsx else 0
+        steps_issued = int(dsx["steps_issued"]) if dsx else t
+        # checked: now change
+        for g, sg in zip(self.param_groups, groups):
             for k, v in sg.items():
                 if k != "params":
                     g[k] = tuple(v) if k == "betas" else v
-        st = state_dict["state"]
-        ix = self._state_index
         # A torch (or the reference's) state dict holds no master: those
         # parameters take theirs from the current params, which the caller
         # loads from the same checkpoint.
@@ -418,24 +444,10 @@ class _FusedAdamWBase(torch.optim.Optimizer):
                 views = self.store.views_of(i)
                 for key in ("exp_avg", "exp_avg_sq", "master"):
                     if key in st[ix[i]]:
-                        src = st[ix[i]][key]
-                        if src.shape != views[key].shape:
-                            raise ValueError(f"state for parameter {ix[i]} has shape {tuple(src.shape)}, "
-                                             f"expected {tuple(views[key].shape)}")
-                        views[key].copy_(src.to(views[key].device, torch.float32))
+                        views[key].copy_(st[ix[i]][key].to(views[key].device, torch.float32))
             self.store.refresh_params16()
-        dsx = state_dict.get("dsx")
-        t = int(dsx["t"]) if dsx else int(max((float(v["step"]) for v in st.values()), default=0))
-        from ._lib import DsxState
-        hs = DsxState()
-        hs.scale = float(dsx["scale"]) if dsx else (self.scaler.init_scale if self.scaler.mode != "none" else 1.0)
-        hs.good_steps = int(dsx["good_steps"]) if dsx else 0
-        hs.hyst_left = int(dsx["hyst_left"]) if dsx else max(1, self.scaler.hysteresis)
-        hs.t = t
-        hs.iter = int(dsx["iter"]) if dsx else t
-        hs.overflow_count = int(dsx["overflow_count"]) if dsx else 0
         self.dstate.copy_(torch.frombuffer(bytearray(bytes(hs)), dtype=torch.uint8).to(self.device))
-        self.steps_issued = int(dsx["steps_issued"]) if dsx else t
+        self.steps_issued = steps_issued
         self._bind_state()
 
 

@@ -182,13 +182,17 @@ class ZeROOptimizer:
         return sd
 
     def load_state_dict(self, state_dict: Dict[str, Any]) -> None:
+        """The reference's keys (Src/zero/optimizer.py:356-404) around the
+        base optimizer's state dict. A state dict the base optimizer refuses
+        (ValueError) leaves this object unchanged as well."""
         state_dict = dict(state_dict)
         current_step = state_dict.pop("current_step", None)
         overflow_count = state_dict.pop("overflow_count", None)
-        self.gradient_accumulation_count = state_dict.pop("gradient_accumulation_count", 0)
+        accumulation = int(state_dict.pop("gradient_accumulation_count", 0))
         scaler = state_dict.pop("grad_scaler", None)
         state_dict.pop("zero_stage", None)
         self.base_optimizer.load_state_dict(state_dict)
+        self.gradient_accumulation_count = accumulation
         if "dsx" not in state_dict and scaler and "scale" in scaler:
             # the reference's state dict: its GradScaler's state
             # (Src/zero/optimizer.py:375-376, 397-398; torch's GradScaler.state_dict keys)

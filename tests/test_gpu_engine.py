@@ -790,3 +790,112 @@ def test_engine_fine_tune_with_a_frozen_layer(gpu, contiguous):
     assert torch.equal(model[0].weight, frozen[0]) and torch.equal(model[0].bias, frozen[1])
     assert not torch.equal(model[2].weight, trained)
     assert opt.current_step == 3
+
+
+@pytest.mark.parametrize("contiguous", [True, False])
+def test_refused_checkpoints_and_state_dicts_change_nothing(gpu, tmp_path, contiguous):
+    """What does not fit is refused before anything changes. load_checkpoint
+    refuses a checkpoint of another model: layers of another width, or a
+    parameter of the same name and size but another shape, which a check of
+    names and sizes alone would have let through. load_state_dict (the
+    ZeROOptimizer's, and so the base optimizer's, Src/zero/optimizer.py:
+    356-404) refuses a state dict with another group count, a group of
+    another size, or a state tensor of another shape. Each refusal is a
+    ValueError. Afterwards master, exp_avg, exp_avg_sq, params, the device
+    state, lr and the accumulation count are what they were, and the good
+    state dict still loads."""
+    import copy
+
+    import torch
+    import distributedspeed_amd as ds
+    from distributedspeed_amd import _lib
+    _say(f"refused loads, contiguous_gradients={contiguous}")
+
+    class Reshaped(torch.nn.Module):
+        """One 784x1024 weight stored in a given shape (the same size either
+        way), then a 10-way head."""
+
+        def __init__(self, shape, seed):
+            super().__init__()
+            g = torch.Generator().manual_seed(seed)
+            self.w = torch.nn.Parameter(torch.randn(*shape, generator=g) * 0.02)
+            self.head = torch.nn.Linear(1024, 10)
+
+        def forward(self, x):
+            return self.head(x @ self.w.reshape(784, 1024))
+
+    cfg = {"fp16": {"enabled": True, "hysteresis": 1}, "max_grad_norm": 1.0,
+           "zero_optimization": {"stage": 2, "contiguous_gradients": contiguous}}
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(31)
+    data = [(torch.randn(16, 784, device=gpu, generator=gen), torch.randint(0, 10, (16,), device=gpu, generator=gen))
+            for _ in range(2)]
+
+    def train(engine):
+        for x, y in data:
+            engine.backward(torch.nn.functional.cross_entropy(engine(x).float(), y))
+            engine.step()
+
+    def snapshot(engine):
+        b = engine.optimizer.base_optimizer
+        torch.cuda.synchronize(gpu)
+        views = [{k: v.detach().cpu().clone() for k, v in b.store.views_of(i).items()} for i in range(len(b.dsx_params))]
+        params = [p.detach().cpu().clone() for p in b.dsx_params]
+        st = bytes(b.read_state())
+        return views, params, st, [g["lr"] for g in b.param_groups], engine.optimizer.gradient_accumulation_count
+
+    def same(a, b):
+        assert a[2] == b[2] and a[3] == b[3] and a[4] == b[4]
+        for va, vb in zip(a[0], b[0]):
+            for k in va:
+                assert torch.equal(va[k].view(torch.int32), vb[k].view(torch.int32)), k
+        for pa, pb in zip(a[1], b[1]):
+            assert torch.equal(pa.view(torch.int16), pb.view(torch.int16))
+
+    wide, _, _, _ = ds.initialize(_mlp(5), cfg)
+    train(wide)
+    wide.save_checkpoint(str(tmp_path / "wide"))
+    narrow_model = torch.nn.Sequential(torch.nn.Linear(784, 512), torch.nn.ReLU(), torch.nn.Linear(512, 1024),
+                                       torch.nn.ReLU(), torch.nn.Linear(1024, 10))
+    narrow, _, _, _ = ds.initialize(narrow_model, cfg)
+    train(narrow)
+    before = snapshot(narrow)
+    with pytest.raises(ValueError, match="layout does not match"):
+        narrow.load_checkpoint(str(tmp_path / "wide"))
+    same(before, snapshot(narrow))
+
+    a, _, _, _ = ds.initialize(Reshaped((784, 1024), 1), cfg)
+    train(a)
+    a.save_checkpoint(str(tmp_path / "a"))
+    b, _, _, _ = ds.initialize(Reshaped((1024, 784), 2), cfg)
+    train(b)
+    before = snapshot(b)
+    with pytest.raises(ValueError, match="layout does not match"):
+        b.load_checkpoint(str(tmp_path / "a"))
+    same(before, snapshot(b))
+
+    zo = wide.optimizer
+    good = zo.state_dict()
+    before = snapshot(wide)
+    bad_count = copy.deepcopy(good)
+    bad_count["param_groups"].append(dict(bad_count["param_groups"][0], params=[]))
+    bad_size = copy.deepcopy(good)
+    bad_size["param_groups"][0]["params"] = bad_size["param_groups"][0]["params"][:-1]
+    bad_shape = copy.deepcopy(good)
+    k0 = bad_shape["param_groups"][0]["params"][0]
+    bad_shape["state"][k0]["exp_avg"] = bad_shape["state"][k0]["exp_avg"].reshape(-1)
+    for bad, what in ((bad_count, "number of parameter groups"), (bad_size, "doesn't match the size"),
+                      (bad_shape, "has shape")):
+        for g in bad["param_groups"]:
+            g["lr"] = 123.0  # would show if the hyper-parameters were taken before the refusal
+        bad["gradient_accumulation_count"] = 3
+        with pytest.raises(ValueError, match=what):
+            zo.load_state_dict(bad)
+        same(before, snapshot(wide))
+    zo.load_state_dict(good)
+    after = snapshot(wide)
+    # a load carries the state, not the last step's record (last_norm, last_skip)
+    fields = ("scale", "good_steps", "hyst_left", "t", "iter", "overflow_count", "error")
+    sa, sb = (_lib.DsxState.from_buffer_copy(x[2]) for x in (before, after))
+    assert [getattr(sa, f) for f in fields] == [getattr(sb, f) for f in fields]
+    same(before[:2] + (b"",) + before[3:], after[:2] + (b"",) + after[3:])
