@@ -757,7 +757,10 @@ def measure_offload(dev, full: int, budget_gib: float, steps: int) -> dict:
     # of this and the fresh process's figure.
     _progress("measuring the host link on the step's own streams")
     from distributedspeed_amd.offload import measure_streamer_link
-    link_here = measure_streamer_link(streamer, (master, m, v))
+    # the copy-only schedule is also started as a step starts it, behind K1
+    # (which reads the grads and writes the partials, and changes no state)
+    link_here = measure_streamer_link(streamer, (master, m, v), pipeline_passes=3,
+                                      lead=lambda: ops.unscale_norm(grad, st, parts, nparts))
     link_here["measured_in"] = "this process, the step's copy streams and pinned buffers, after the timed steps"
     ceiling = max(link["both_each_way"], link_here["both_each_way"])
     sec = sorted(times)[len(times) // 2]

@@ -131,10 +131,11 @@ def test_streamer_link_probe_leaves_the_state_unchanged(gpu):
     """measure_streamer_link (the offload line's in-process link ceiling)
     copies between the streamer's own staging buffers and the pinned state on
     its own streams: pairwise, as the step's copy schedule without the
-    kernel, and free-running both ways (a ragged last chunk here; three
-    staging slots, and two, where the free-running copies in share slot 1).
-    Its copies out write back what its copies in read, so the state is
-    bit-identical afterwards, and every figure is a rate."""
+    kernel (also behind a lead-in call, run before each pass), and
+    free-running both ways (a ragged last chunk here; three staging slots,
+    and two, where the free-running copies in share slot 1). Its copies out
+    write back what its copies in read, so the state is bit-identical
+    afterwards, and every figure is a rate."""
     import torch
     from distributedspeed_amd.offload import HostStateStreamer, measure_streamer_link, pinned_empty
     chunk = 1 << 20
@@ -143,16 +144,21 @@ def test_streamer_link_probe_leaves_the_state_unchanged(gpu):
     for h in host:
         h.copy_(torch.randn(h.numel(), generator=gen))
     before = [h.clone() for h in host]
+    leads = []
     for nbuf in (3, 2):
         _say(f"streamer link probe chunk={chunk} nbuf={nbuf}")
         st = HostStateStreamer(gpu, chunk, nbuf)
-        r = measure_streamer_link(st, tuple(host), reps=2, trials=2)
-        for k in ("h2d", "d2h", "pairs_each_way", "copy_pipeline_each_way", "sweep_each_way"):
+        r = measure_streamer_link(st, tuple(host), reps=2, trials=2, lead=lambda: leads.append(1))
+        ways = ("pairs_each_way", "copy_pipeline_each_way", "sweep_each_way", "copy_pipeline_behind_lead_each_way")
+        for k in ("h2d", "d2h") + ways:
             assert r[k] > 0, r
-        assert r["both_each_way"] == max(r["pairs_each_way"], r["copy_pipeline_each_way"], r["sweep_each_way"])
+        assert r["both_each_way"] == max(r[k] for k in ways)
         assert r["copy_pipeline_bytes_each_way"] == 12 * host[0].numel()
         assert r["bytes_each_way_per_rep"] == 12 * chunk
         for h, b in zip(host, before):
             assert torch.equal(h.view(torch.int32), b.view(torch.int32)), nbuf
+    assert len(leads) == 4  # once before each of the two passes, per streamer
+    assert "copy_pipeline_behind_lead_each_way" not in measure_streamer_link(st, tuple(host), reps=1, trials=1,
+                                                                             pipeline_passes=1)
     with pytest.raises(ValueError):
         measure_streamer_link(st, tuple(h[:chunk] for h in host))
