@@ -99,8 +99,7 @@ class HostStateStreamer:
         self.ev_in = [torch.cuda.Event() for _ in range(self.nbuf)]
         self.ev_done = [torch.cuda.Event() for _ in range(self.nbuf)]
         self.ev_out = [torch.cuda.Event() for _ in range(self.nbuf)]
-        self.last_bytes = 0
-        self.last_seconds = 0.0
+        self.last_bytes = 0  # host<->HBM bytes the last run() moved (both directions)
 
     def run(self, host_state: tuple[torch.Tensor, torch.Tensor, torch.Tensor], param16: torch.Tensor | None,
             grad: torch.Tensor | None, pieces: list[tuple[int, int, torch.Tensor | None]], *,
