@@ -69,14 +69,15 @@ def test_cpu_baseline_host_facts():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("workload", ["mlp", "mlp-train", "gpt2-small", "ffn-train"])
+@pytest.mark.parametrize("workload", ["mlp", "mlp-train", "gpt2-small", "ffn-train", "llama8b-dropin"])
 def test_secondary_workloads_print_one_line(gpu, workload):
     """The secondary workloads (configs[0] and [1] through the drop-in
     classes, the training iterations) still run and print one JSON line with
     a positive value. configs[3] and [4] run inside the headline line's
     secondary_configs."""
     print(f"[gpu-test] bench.py --workload {workload}", file=sys.stderr, flush=True)
-    r = _run(["--workload", workload, "--steps", "3", "--warmup", "1"], 280)
+    extra = ["--numel", str((1 << 25) + 5)] if workload == "llama8b-dropin" else []
+    r = _run(["--workload", workload, "--steps", "3", "--warmup", "1"] + extra, 280)
     assert r.returncode == 0, r.stderr[-2000:]
     lines = [x for x in r.stdout.splitlines() if x.startswith("{")]
     assert len(lines) == 1, r.stdout[-2000:]
