@@ -297,7 +297,7 @@ def measure_dropin(dev, gpt2: bool, steps: int, warmup: int,
             "warmup": warmup, "modes": out}
 
 
-def measure_dropin_headline(dev, n: int, steps: int, warmup: int, headline_ms: float,
+def measure_dropin_headline(dev, n: int, steps: int, warmup: int, headline_ms: float | None,
                             fold_restore: int = 3 << 23) -> dict:
     """configs[2] through the drop-in classes: the same shard (one parameter
     of n elements, the headline's seed and values, bf16 params and grads,
@@ -316,7 +316,8 @@ def measure_dropin_headline(dev, n: int, steps: int, warmup: int, headline_ms: f
     (unscale_norm, finalize, adamw_flat, with their own state and records)
     over the optimizer's flat buffers: the headline's calls on this run's
     allocations. Events around `steps` steps after `warmup` on the stream
-    the kernels run on."""
+    the kernels run on. headline_ms (None when no headline ran in this
+    process) gives each form's over_headline_ms."""
     import torch
     from distributedspeed_amd import _lib, ops
     from distributedspeed_amd.flat_step import AdamWHyper, BiasCorrectionTable, ScalerConfig
@@ -372,7 +373,7 @@ def measure_dropin_headline(dev, n: int, steps: int, warmup: int, headline_ms: f
         st = opt.read_state() if fn is not entry_points else ops.read_state(st3)
         out[name] = {"ms_per_step": round(ms, 4), "gparam_per_s": round(n / ms / 1e6, 3),
                      "pct_of_8tbps_end_to_end": round(100 * 30 * n / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
-                     "over_headline_ms": round(ms / headline_ms, 4),
+                     "over_headline_ms": round(ms / headline_ms, 4) if headline_ms else None,
                      "host_issue_us_per_step": round(t_issue / steps * 1e6, 1),
                      "state_error": st.error, "last_skip": st.last_skip}
         _progress(f"configs[2] drop-in {name}: {out[name]}")
@@ -386,16 +387,15 @@ def measure_dropin_headline(dev, n: int, steps: int, warmup: int, headline_ms: f
                                                if n <= 3 << 23 else
                                                f"K1, then K2 in {k2_parts(n, None)} parts with K0's finalize "
                                                "folded into the first"),
-            "headline_ms_per_step": round(headline_ms, 4), "modes": out}
+            "headline_ms_per_step": round(headline_ms, 4) if headline_ms else None, "modes": out}
 
 
 def bench_dropin_headline(a, dev) -> int:
     """configs[2] through the drop-in classes as its own line, in a fresh
     process (measure_dropin_headline with no headline run before it, so its
-    buffers are the process's first large allocations). over_headline_ms is
-    then against 1.0 ms, i.e. the ms per step itself."""
+    buffers are the process's first large allocations)."""
     n = int(a.numel)
-    r = measure_dropin_headline(dev, n, a.steps, a.warmup, 1.0, 3 << 23 if a.fold is None else a.fold)
+    r = measure_dropin_headline(dev, n, a.steps, a.warmup, None, 3 << 23 if a.fold is None else a.fold)
     modes = r["modes"]
     bad = [k for k, v in modes.items() if v["state_error"] or v["last_skip"]]
     if bad:
